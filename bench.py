@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused per-layer kernels on one MI355X.
+
+A step is one pass of the layer hot path over one batch of the workload, in
+engine order: embedding gather, residual-add + RMSNorm, RoPE + paged-KV write,
+residual-add + RMSNorm, SwiGLU.  Default workload: Llama-3.1-8B decode at
+batch 32 (C2), the configuration the headline metric is quoted on.
+
+Every step is a replay of a HIP graph holding the five launches for one of R
+rotating input sets (R sets > 512 MB, so the 256 MB Infinity Cache cannot serve
+the "HBM" traffic); K steps are timed between HIP events on the launch stream.
+Per-kernel figures time R back-to-back launches of one kernel in a graph.  The
+prefill-sized workloads (C3 mixed 4096 rows, C4 INT8 KV 16k tokens, C5 Qwen2
+16k) are timed per kernel as well, since only they can approach the HBM
+roofline.  `value` = algorithmic bytes of a step / time of a step (GB/s).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2]
+                       [--no-cpu] [--no-extra] [--only KERNEL] [--reps N]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 640 << 20  # > 2 x Infinity Cache
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class LayerData:
+    """Device buffers of one workload: R rotating activation sets, the shared
+    embedding table / norm weight / RoPE tables / KV cache."""
+
+    def __init__(self, torch, K, w, rotations=None, seed=0):
+        from redline_amd.configs import build_batch, token_ids
+        import redline_amd as ra
+        self.torch, self.K, self.w = torch, K, w
+        m = w.model
+        self.T = T = w.num_tokens
+        dev = "cuda"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.table = (torch.randn((m.vocab, m.hidden), generator=g, device=dev) * 0.02).half()
+        self.weight = (1 + 0.1 * torch.randn(m.hidden, generator=g, device=dev)).half()
+        cos, sin = ra.rope_cos_sin_tables(m.theta, m.head_dim, w.max_pos)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        dtype = K.KVDType.kINT8 if w.kv_int8 else K.KVDType.kFP16
+        self.cache = K.KVCache(1, w.num_blocks, m.hkv, m.head_dim, w.block_size, dtype)
+        set_bytes = T * (2 * m.hidden * 3 + 2 * m.qkv_cols + 6 * m.inter)
+        self.R = rotations or max(2, min(256, -(-ROTATE_BYTES // set_bytes)))
+        rng = np.random.default_rng(seed + 17)
+        self.sets = []
+        for r in range(self.R):
+            meta, shape, lay, _ = build_batch(w, np.random.default_rng(seed * 1000 + r + 1))
+            d_meta = torch.from_numpy(meta[:lay["total_words"]]).to(dev)
+            s = {
+                "ids": torch.from_numpy(token_ids(w, rng)).to(dev),
+                "pos": d_meta[lay["positions"]:lay["positions"] + T],
+                "slot": d_meta[lay["slot_mapping"]:lay["slot_mapping"] + T],
+                "meta": d_meta,
+                "emb": torch.empty((T, m.hidden), dtype=torch.float16, device=dev),
+                "res": torch.randn((T, m.hidden), generator=g, device=dev).half(),
+                "delta": torch.randn((T, m.hidden), generator=g, device=dev).half(),
+                "normed": torch.empty((T, m.hidden), dtype=torch.float16, device=dev),
+                "qkv": torch.randn((T, m.qkv_cols), generator=g, device=dev).half(),
+                "gu": torch.randn((T, 2 * m.inter), generator=g, device=dev).half(),
+                "act": torch.empty((T, m.inter), dtype=torch.float16, device=dev),
+            }
+            self.sets.append(s)
+        torch.cuda.synchronize()
+
+    # individual launches on set r (stream = torch's current stream)
+    def embedding(self, r):
+        s, m = self.sets[r], self.w.model
+        self.K.embedding_lookup(s["ids"], self.table, self.T, m.hidden, s["emb"])
+
+    def norm(self, r):
+        s, m = self.sets[r], self.w.model
+        self.K.fused_add_rmsnorm(s["res"], s["delta"], self.weight, self.T, m.hidden, m.eps,
+                                 s["normed"])
+
+    def rope(self, r):
+        s, m = self.sets[r], self.w.model
+        self.K.rope_and_write_kv(s["qkv"], s["pos"], s["slot"], self.T, m.hq, self.cos, self.sin,
+                                 self.cache.layer(0))
+
+    def swiglu(self, r):
+        s, m = self.sets[r], self.w.model
+        self.K.silu_and_mul(s["gu"], self.T, m.inter, s["act"])
+
+    def step(self, r):
+        self.embedding(r)
+        self.norm(r)
+        self.rope(r)
+        self.norm(r)
+        self.swiglu(r)
+
+    def bytes(self):
+        from redline_amd import configs as C
+        m, T = self.w.model, self.T
+        return {
+            "embedding_lookup": C.bytes_embedding(T, m.hidden),
+            "fused_add_rmsnorm": C.bytes_add_rmsnorm(T, m.hidden),
+            "rope_and_write_kv": C.bytes_rope_kv(T, m.hq, m.hkv, m.head_dim, self.w.kv_int8),
+            "silu_and_mul": C.bytes_swiglu(T, m.inter),
+        }
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_graph(torch, graph, reps):
+    """Average ms per replay, HIP events on the replay stream."""
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+KERNELS = ("embedding_lookup", "fused_add_rmsnorm", "rope_and_write_kv", "silu_and_mul")
+
+
+def per_kernel(torch, data, reps, only=None):
+    fns = {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
+           "rope_and_write_kv": data.rope, "silu_and_mul": data.swiglu}
+    nbytes = data.bytes()
+    out = {}
+    for name in KERNELS:
+        if only and name != only:
+            continue
+        f = fns[name]
+        g = capture(torch, lambda: [f(r) for r in range(data.R)])
+        ms = time_graph(torch, g, reps) / data.R
+        gbs = nbytes[name] / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_call": round(ms * 1e3, 3), "gb_per_s": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                     "bytes_per_call": nbytes[name]}
+        log(f"  {data.w.key} {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s "
+            f"({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)  R={data.R}")
+        del g
+    return out
+
+
+def cpu_baseline(torch, data, seconds=10.0):
+    """The CPU oracle (oracle/oracle.c, single thread) on the same step:
+    a bounded number of full steps over one input set, copied to host."""
+    import ctypes as C
+    import oracle
+    L = oracle.lib()
+    w, m, T = data.w, data.w.model, data.T
+    s = data.sets[0]
+    h = lambda t: np.ascontiguousarray(t.cpu().numpy())  # noqa: E731
+    table, ids = h(data.table).view(np.uint16), h(s["ids"])
+    emb = np.empty((T, m.hidden), np.uint16)
+    res, delta, wgt = h(s["res"]).view(np.uint16), h(s["delta"]).view(np.uint16), h(data.weight).view(np.uint16)
+    normed = np.empty_like(res)
+    qkv = h(s["qkv"]).view(np.uint16)
+    pos, slot = h(s["pos"]), h(s["slot"])
+    cos, sin = h(data.cos), h(data.sin)
+    shape = (w.num_blocks, m.hkv, w.block_size, m.head_dim)
+    kc = np.zeros(shape, np.int8 if w.kv_int8 else np.uint16)
+    vc = np.zeros_like(kc)
+    ks = np.zeros(shape[:3], np.float32) if w.kv_int8 else None
+    vs = np.zeros(shape[:3], np.float32) if w.kv_int8 else None
+    gu, act = h(s["gu"]).view(np.uint16), np.empty((T, m.inter), np.uint16)
+    p = oracle.p
+    args = (p(ids), p(table), T, m.hidden, p(emb), p(res), p(delta), p(wgt), C.c_float(m.eps),
+            p(normed), p(qkv), p(pos), p(slot), m.hq, m.hkv, m.head_dim, p(cos), p(sin), p(kc),
+            p(vc), p(ks), p(vs), w.block_size, int(w.kv_int8), p(gu), m.inter, p(act))
+    L.orc_layer_step(*args)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        L.orc_layer_step(*args)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    nb = data.bytes()
+    step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
+    return {"value": round(step_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port", "ms_per_step": round(dt / n * 1e3, 3),
+            "sample": f"{n} full {w.key} steps (embedding, 2x add+RMSNorm, RoPE+KV, SwiGLU) "
+                      f"in {dt:.1f} s, single thread, oracle/oracle.c"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--workload", default="C2")
+    ap.add_argument("--reps", type=int, default=20, help="graph replays per kernel timing")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the fused per-layer kernels are row-independent "
+              "and this build has no multi-GPU path (see DESIGN.md, 'How it would shard').",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from redline_amd import kernels as K
+    from redline_amd.configs import make_workload
+    torch.cuda.set_device(0)
+
+    w = make_workload(args.workload)
+    log(f"setting up {w.key} ({w.model.name}, T={w.num_tokens})")
+    data = LayerData(torch, K, w)
+    nb = data.bytes()
+    step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
+
+    result = {}
+    if args.only is None:
+        graphs = [capture(torch, lambda r=r: data.step(r)) for r in range(data.R)]
+        for i in range(args.warmup):
+            graphs[i % data.R].replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(args.steps):
+            graphs[i % data.R].replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms_step = start.elapsed_time(end) / args.steps
+        del graphs
+        value = step_bytes / (ms_step * 1e-3) / 1e9
+        log(f"{w.key} step: {ms_step * 1e3:.2f} us, {value:.1f} GB/s")
+        result.update(ms_per_step=round(ms_step, 5), value=round(value, 2))
+
+    kern = per_kernel(torch, data, args.reps, args.only)
+    rot = data.R
+    del data
+    torch.cuda.empty_cache()
+    if args.only is not None:
+        print(json.dumps({"only": args.only, "workload": w.key, "kernels": kern}))
+        return
+
+    dominant = max(KERNELS, key=lambda k: nb[k])
+    dk = kern[dominant]
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": dk["gb_per_s"],
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_of_hbm_peak"],
+                "traffic": None, "bytes_per_launch": nb[dominant]}
+
+    extra = {}
+    if not args.no_extra:
+        for key in ("C3", "C4", "C5"):
+            wx = make_workload(key)
+            log(f"setting up {key} ({wx.model.name}, T={wx.num_tokens})")
+            dx = LayerData(torch, K, wx)
+            extra[key] = per_kernel(torch, dx, max(3, args.reps // 4))
+            del dx
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle) ...")
+        dcpu = LayerData(torch, K, w, rotations=1)
+        cpu = cpu_baseline(torch, dcpu, args.cpu_seconds)
+        del dcpu
+        log(f"CPU: {cpu['value']} GB/s, {cpu['ms_per_step']} ms/step")
+
+    line = {
+        "metric": "achieved HBM GB/s (% of peak) and us/call per fused layer kernel, 8B decode b32",
+        "value": result["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": result["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"{w.key}: {w.model.name}-shaped decode, batch {w.num_tokens}"
+                               if w.key == "C2" else f"{w.key}: {w.model.name}, T={w.num_tokens}",
+                   "step": "embedding_lookup, fused_add_rmsnorm, rope_and_write_kv (FP16 KV), "
+                           "fused_add_rmsnorm, silu_and_mul",
+                   "global_batch": w.num_tokens, "rotating_input_sets": rot,
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kern,
+        "prefill": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

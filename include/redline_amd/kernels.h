@@ -1,0 +1,111 @@
+// C++ launch interface of the MI355X fused per-layer kernels.
+//
+// Same namespace, names, parameter order and KVLayerView field layout as the
+// reference's redline::kernels (src/cuda/kernels/kernels.h:13-27, 64-88), spelled
+// with hipStream_t and __half.  Each launcher forwards to the C ABI in rlk.h and
+// turns a non-zero status into a thrown redline::Error, which is how the
+// reference reports RL_CHECK failures (src/core/common.h:25-32) and failed
+// launches (src/cuda/cuda_utils.h:19).  Launchers are asynchronous on `stream`,
+// never allocate or synchronise, and are capturable into HIP graphs.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "redline_amd/rlk.h"
+
+namespace redline {
+
+class Error : public std::runtime_error {
+ public:
+  explicit Error(const std::string& msg) : std::runtime_error(msg) {}
+};
+
+enum class KVDType { kFP16 = RLK_KV_FP16, kINT8 = RLK_KV_INT8 };
+
+// One layer of the paged KV cache.
+//   k, v:             [num_blocks, num_kv_heads, block_size, head_dim]  (half or int8)
+//   k_scale, v_scale: [num_blocks, num_kv_heads, block_size] float     (INT8 only)
+struct KVLayerView {
+  void* k = nullptr;
+  void* v = nullptr;
+  float* k_scale = nullptr;
+  float* v_scale = nullptr;
+  int block_size = 16;
+  int num_kv_heads = 0;
+  int head_dim = 0;
+  KVDType dtype = KVDType::kFP16;
+};
+
+static_assert(sizeof(KVLayerView) == sizeof(rlk_kv_layer_view), "KVLayerView layout");
+static_assert(offsetof(KVLayerView, block_size) == offsetof(rlk_kv_layer_view, block_size),
+              "KVLayerView layout");
+static_assert(offsetof(KVLayerView, dtype) == offsetof(rlk_kv_layer_view, dtype),
+              "KVLayerView layout");
+
+namespace kernels {
+namespace detail {
+
+inline void check(int status) {
+  if (status != RLK_OK) throw Error(rlk_last_error());
+}
+inline uint16_t* bits(half* p) { return reinterpret_cast<uint16_t*>(p); }
+inline const uint16_t* bits(const half* p) { return reinterpret_cast<const uint16_t*>(p); }
+
+}  // namespace detail
+
+// input_ids[i] = src[i] >= 0 ? prev_sampled[src[i]] : input_ids[i]
+inline void resolve_input_ids(int32_t* input_ids, const int32_t* src, const int32_t* prev_sampled,
+                              int n, hipStream_t stream) {
+  detail::check(rlk_resolve_input_ids(input_ids, src, prev_sampled, n, stream));
+}
+
+inline void embedding_lookup(const int32_t* ids, const half* table, int n, int hidden, half* out,
+                             hipStream_t stream) {
+  detail::check(rlk_embedding_lookup(ids, detail::bits(table), n, hidden, detail::bits(out), stream));
+}
+
+// residual += delta (skipped when delta == nullptr); out = rmsnorm(residual) * weight.
+inline void fused_add_rmsnorm(half* residual, const half* delta, const half* weight, int rows,
+                              int hidden, float eps, half* out, hipStream_t stream) {
+  detail::check(rlk_fused_add_rmsnorm(detail::bits(residual), detail::bits(delta),
+                                      detail::bits(weight), rows, hidden, eps, detail::bits(out),
+                                      stream));
+}
+
+// out[r, i] = silu(gate_up[r, i]) * gate_up[r, inter + i]
+inline void silu_and_mul(const half* gate_up, int rows, int inter, half* out, hipStream_t stream) {
+  detail::check(rlk_silu_and_mul(detail::bits(gate_up), rows, inter, detail::bits(out), stream));
+}
+
+// Same, for gate/up columns interleaved as (gate_0, up_0, gate_1, up_1, ...).
+inline void silu_and_mul_interleaved(const half* gate_up, int rows, int inter, half* out,
+                                     hipStream_t stream) {
+  detail::check(
+      rlk_silu_and_mul_interleaved(detail::bits(gate_up), rows, inter, detail::bits(out), stream));
+}
+
+// dst[i, :] = src[idx[i], :]
+inline void gather_rows(const half* src, const int32_t* idx, int n, int cols, half* dst,
+                        hipStream_t stream) {
+  detail::check(rlk_gather_rows(detail::bits(src), idx, n, cols, detail::bits(dst), stream));
+}
+
+// RoPE on the q and k heads of qkv [num_tokens, (Hq + 2 Hkv) * D]; roped q is
+// written back in place and k/v go to the paged cache at slot_mapping[t]
+// (block * block_size + offset; negative = skip).
+inline void rope_and_write_kv(half* qkv, const int32_t* positions, const int32_t* slot_mapping,
+                              int num_tokens, int num_heads, const float* cos_table,
+                              const float* sin_table, const KVLayerView& kv, hipStream_t stream) {
+  detail::check(rlk_rope_and_write_kv(detail::bits(qkv), positions, slot_mapping, num_tokens,
+                                      num_heads, cos_table, sin_table,
+                                      reinterpret_cast<const rlk_kv_layer_view*>(&kv), stream));
+}
+
+}  // namespace kernels
+}  // namespace redline

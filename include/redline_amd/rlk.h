@@ -1,0 +1,200 @@
+/*
+ * rlk.h — C ABI of the MI355X (gfx950) fused per-layer kernels.
+ *
+ * Every device entry point is asynchronous on the given HIP stream, never
+ * allocates, frees or synchronises, and is therefore capturable into a HIP
+ * graph.  Pointers are device pointers owned by the caller.  fp16 tensors are
+ * passed as uint16_t* holding IEEE binary16 bit patterns.
+ *
+ * Return value: RLK_OK (0) on success; a negative RLK_E* code for an argument
+ * error detected on the host before anything is launched; a positive hipError_t
+ * value when the launch itself failed.  rlk_last_error() gives the message of
+ * the most recent failure on the calling thread.
+ *
+ * Reference interface replaced: redline::kernels in
+ * src/cuda/kernels/kernels.h:64-88 (Neil456/Redline).  The C++ header
+ * redline_amd/kernels.h wraps these entry points with the reference's exact
+ * names, parameter order and exception behaviour.
+ */
+#ifndef REDLINE_AMD_RLK_H_
+#define REDLINE_AMD_RLK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RLK_OK 0
+#define RLK_EINVAL (-1)      /* invalid shape / argument (reference: RL_CHECK throw) */
+#define RLK_EUNSUPPORTED (-2) /* unsupported configuration, e.g. head_dim */
+
+/* KV cache element type; values match redline::KVDType (kernels.h:13). */
+#define RLK_KV_FP16 0
+#define RLK_KV_INT8 1
+
+/*
+ * One layer of the paged KV cache.  Field order, types and sizes are those of
+ * redline::KVLayerView (src/cuda/kernels/kernels.h:18-27), so a pointer to the
+ * reference struct can be passed unchanged.
+ *   k, v              [num_blocks, num_kv_heads, block_size, head_dim]  fp16 or int8
+ *   k_scale, v_scale  [num_blocks, num_kv_heads, block_size]  fp32 (INT8 only)
+ */
+typedef struct rlk_kv_layer_view {
+  void* k;
+  void* v;
+  float* k_scale;
+  float* v_scale;
+  int block_size;
+  int num_kv_heads;
+  int head_dim;
+  int dtype; /* RLK_KV_FP16 | RLK_KV_INT8 */
+} rlk_kv_layer_view;
+
+/* Message of the last failure on this thread ("" if none). */
+const char* rlk_last_error(void);
+/* Library version string. */
+const char* rlk_version(void);
+
+/* ------------------------------------------------------------ elementwise */
+
+/* out[t, :] = table[ids[t], :]   (table [V, hidden], out [n, hidden]).
+ * Replaces kernels::embedding_lookup, elementwise.cu:106-112.
+ * n <= 0: no-op.  hidden % 8 != 0: RLK_EINVAL.  ids are not bounds-checked. */
+int rlk_embedding_lookup(const int32_t* ids, const uint16_t* table, int n, int hidden,
+                         uint16_t* out, hipStream_t stream);
+
+/* residual = fp16(residual + delta) in place (skipped when delta == NULL);
+ * out = fp16(fp16(residual * rsqrt(mean(residual^2) + eps)) * weight).
+ * Replaces kernels::fused_add_rmsnorm, elementwise.cu:114-121.
+ * rows <= 0: no-op.  hidden % 8 != 0: RLK_EINVAL. */
+int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta, const uint16_t* weight,
+                          int rows, int hidden, float eps, uint16_t* out, hipStream_t stream);
+
+/* out[r, i] = fp16(fp16(silu(gate_up[r, i])) * gate_up[r, inter + i]).
+ * Replaces kernels::silu_and_mul, elementwise.cu:140-145.
+ * rows <= 0: no-op.  inter % 8 != 0: RLK_EINVAL. */
+int rlk_silu_and_mul(const uint16_t* gate_up, int rows, int inter, uint16_t* out,
+                     hipStream_t stream);
+
+/* Same with gate/up interleaved: gate = gate_up[r, 2i], up = gate_up[r, 2i+1].
+ * Replaces kernels::silu_and_mul_interleaved, elementwise.cu:133-138.
+ * rows <= 0: no-op.  Any inter >= 1 is accepted (as in the reference). */
+int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, uint16_t* out,
+                                 hipStream_t stream);
+
+/* dst[i, :] = src[idx[i], :].  Replaces kernels::gather_rows,
+ * elementwise.cu:147-153.  n <= 0: no-op.  cols % 8 != 0: RLK_EINVAL. */
+int rlk_gather_rows(const uint16_t* src, const int32_t* idx, int n, int cols, uint16_t* dst,
+                    hipStream_t stream);
+
+/* input_ids[i] = prev_sampled[src[i]] where src[i] >= 0.  Replaces
+ * kernels::resolve_input_ids, elementwise.cu:99-104.  n <= 0: no-op. */
+int rlk_resolve_input_ids(int32_t* input_ids, const int32_t* src, const int32_t* prev_sampled,
+                          int n, hipStream_t stream);
+
+/* ------------------------------------------------------------- rope / kv */
+
+/* RoPE (rotate-half pairs (i, i + D/2)) on the q and k heads of
+ * qkv [num_tokens, (num_heads + 2*kv->num_kv_heads) * D]; the roped q heads are
+ * written back in place (the k section of qkv is left as it was); roped k and
+ * unchanged v are written into the paged cache cell
+ * ((slot / bs * Hkv + kvh) * bs + slot % bs) * D for slot = slot_mapping[t]
+ * (slot < 0: no KV write).  INT8 cache: per-(token, head) scale amax/127
+ * stored as fp32, codes rint(clamp(x / scale, -127, 127)).
+ * cos_table / sin_table: fp32 [max_pos, D/2].
+ * Replaces kernels::rope_and_write_kv, rope_kv.cu:107-123.
+ * num_tokens <= 0: no-op.  head_dim not in {64, 128}: RLK_EUNSUPPORTED. */
+int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_t* slot_mapping,
+                          int num_tokens, int num_heads, const float* cos_table,
+                          const float* sin_table, const rlk_kv_layer_view* kv,
+                          hipStream_t stream);
+
+/* ------------------------------------------------------ host-side helpers */
+
+/* IEEE fp16 <-> fp32 with round-to-nearest-even.
+ * Replace redline::float_to_half_bits / half_bits_to_float, common.cpp:37-89. */
+uint16_t rlk_float_to_half_bits(float f);
+float rlk_half_bits_to_float(uint16_t h);
+
+/* Rotary inverse frequencies [head_dim/2] in double, with optional scaling:
+ * scaling_type 0 = none, 1 = linear, 2 = llama3.
+ * Replaces redline::rope_inv_freq, model_config.cpp:126-153. */
+int rlk_rope_inv_freq(double theta, int head_dim, int scaling_type, double factor,
+                      double low_freq_factor, double high_freq_factor,
+                      int original_max_position_embeddings, double* inv_freq);
+
+/* fp32 cos/sin tables [max_pos, head_dim/2], angle = float(p) * float(inv[i]).
+ * Replaces redline::rope_cos_sin_tables, model_config.cpp:155-169. */
+int rlk_rope_cos_sin_tables(double theta, int head_dim, int scaling_type, double factor,
+                            double low_freq_factor, double high_freq_factor,
+                            int original_max_position_embeddings, int max_pos,
+                            float* cos_table, float* sin_table);
+
+/* ------------------------------------------------- batch metadata (host) */
+
+/* Shape of a serialized batch; fields of redline::BatchShape, batch_builder.h:16-26. */
+typedef struct rlk_batch_shape {
+  int num_tokens;
+  int num_seqs;
+  int num_logit_rows;
+  int num_decode_items;
+  int num_prefill_seqs;
+  int max_prefill_q_tiles;
+  int max_context;
+} rlk_batch_shape;
+
+/* Word offsets inside the metadata buffer; fields of redline::MetaLayout,
+ * batch_builder.h:29-38, in the same order. */
+typedef struct rlk_meta_layout {
+  size_t input_ids, input_src, positions, slot_mapping;
+  size_t seq_q_start, seq_q_len, seq_ctx_len;
+  size_t block_tables;
+  size_t decode_token, decode_seq;
+  size_t prefill_seq;
+  size_t logit_token, param_row;
+  size_t temperature, top_k, top_p, seed_lo, seed_hi;
+  size_t total_words;
+} rlk_meta_layout;
+
+/* Logits selection of BatchBuilder::add (redline::LogitsMode). */
+#define RLK_LOGITS_NONE 0
+#define RLK_LOGITS_LAST 1
+#define RLK_LOGITS_ALL 2
+
+typedef struct rlk_batch_builder rlk_batch_builder;
+
+/* Replaces MetaLayout::make, batch_builder.cpp:17-46. */
+int rlk_meta_layout_make(const rlk_batch_shape* shape, int max_blocks_per_seq,
+                         rlk_meta_layout* out);
+
+/* Replaces the BatchBuilder constructor, batch_builder.cpp:48-55.  NULL on bad args. */
+rlk_batch_builder* rlk_batch_builder_create(int max_tokens, int max_seqs, int max_logit_rows,
+                                            int max_blocks_per_seq, int block_size,
+                                            int decode_query_threshold);
+void rlk_batch_builder_destroy(rlk_batch_builder* b);
+void rlk_batch_builder_reset(rlk_batch_builder* b);
+size_t rlk_batch_builder_max_meta_words(const rlk_batch_builder* b);
+/* Replaces BatchBuilder::add, batch_builder.cpp:80-122.  tokens may be NULL
+ * when every src_rows[i] >= 0; src_rows may be NULL.  *first_row receives the
+ * first logits row added (or -1).  Errors (RLK_EINVAL) leave the builder
+ * unchanged. */
+int rlk_batch_builder_add(rlk_batch_builder* b, const int32_t* tokens, int start_pos, int n,
+                          const int32_t* src_rows, const int32_t* blocks, int num_blocks,
+                          float temperature, int top_k, float top_p, uint64_t seed,
+                          int logits_mode, int* first_row);
+/* Replaces BatchBuilder::pad_decode_to, batch_builder.cpp:124-129. */
+int rlk_batch_builder_pad_decode_to(rlk_batch_builder* b, int num_seqs);
+/* Replaces BatchBuilder::shape / write, batch_builder.cpp:131-188.  dst holds
+ * at least rlk_batch_builder_max_meta_words() int32 words. */
+int rlk_batch_builder_shape(const rlk_batch_builder* b, rlk_batch_shape* shape);
+int rlk_batch_builder_write(const rlk_batch_builder* b, int32_t* dst, rlk_batch_shape* shape);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* REDLINE_AMD_RLK_H_ */

@@ -1,0 +1,167 @@
+"""numpy front end of the CPU oracle (oracle.c).  TEST INFRASTRUCTURE ONLY.
+
+Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, always as the checker — never as the thing measured or shipped.
+`ref()` exposes the compiled reference host core (oracle/_ref), present only
+in the container that has /root/reference.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libredline_ref_core.so"
+
+_P = C.c_void_p
+_I = C.c_int
+_o = None
+_r = None
+
+
+def build(ref: bool = False) -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    if ref:
+        subprocess.run(["make", "-s", "-C", str(HERE), "ref"], check=True)
+
+
+def lib() -> C.CDLL:
+    global _o
+    if _o is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        L.orc_f2h.restype, L.orc_f2h.argtypes = C.c_uint16, [C.c_float]
+        L.orc_h2f.restype, L.orc_h2f.argtypes = C.c_float, [C.c_uint16]
+        L.orc_rope_cos_sin_tables.argtypes = [C.c_double, _I, _I, C.c_double, C.c_double,
+                                              C.c_double, _I, _I, _P, _P]
+        L.orc_embedding_lookup.argtypes = [_P, _P, _I, _I, _P]
+        L.orc_gather_rows.argtypes = [_P, _P, _I, _I, _P]
+        L.orc_resolve_input_ids.argtypes = [_P, _P, _P, _I]
+        L.orc_fused_add_rmsnorm.argtypes = [_P, _P, _P, _I, _I, C.c_float, _P]
+        L.orc_silu_and_mul.argtypes = [_P, _I, _I, _P]
+        L.orc_silu_and_mul_interleaved.argtypes = [_P, _I, _I, _P]
+        L.orc_rope_and_write_kv.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P,
+                                            _I, _I]
+        L.orc_layer_step.argtypes = [_P, _P, _I, _I, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P,
+                                     _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P]
+        _o = L
+    return _o
+
+
+def has_ref() -> bool:
+    return REF_LIB.exists()
+
+
+def ref() -> C.CDLL:
+    """The reference's own host core (float_to_half_bits, rope tables, BatchBuilder)."""
+    global _r
+    if _r is None:
+        L = C.CDLL(str(REF_LIB))
+        L.ref_float_to_half_bits.restype, L.ref_float_to_half_bits.argtypes = C.c_uint16, [C.c_float]
+        L.ref_half_bits_to_float.restype, L.ref_half_bits_to_float.argtypes = C.c_float, [C.c_uint16]
+        L.ref_float_to_half_many.argtypes = [_P, C.c_size_t, _P]
+        L.ref_rope_inv_freq.argtypes = [C.c_double, _I, _I, C.c_double, C.c_double, C.c_double, _I, _P]
+        L.ref_rope_cos_sin_tables.argtypes = [C.c_double, _I, _I, C.c_double, C.c_double,
+                                              C.c_double, _I, _I, _P, _P]
+        L.ref_bb_create.restype, L.ref_bb_create.argtypes = _P, [_I] * 6
+        L.ref_bb_destroy.argtypes = [_P]
+        L.ref_bb_max_meta_words.restype, L.ref_bb_max_meta_words.argtypes = C.c_size_t, [_P]
+        L.ref_bb_add.restype = _I
+        L.ref_bb_add.argtypes = [_P, _P, _I, _I, _P, _P, _I, C.c_float, _I, C.c_float, C.c_uint64, _I]
+        L.ref_bb_pad_decode_to.argtypes = [_P, _I]
+        L.ref_bb_write.argtypes = [_P, _P, _P]
+        L.ref_meta_layout.argtypes = [_P, _I, _P]
+        _r = L
+    return _r
+
+
+def p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ------------------------------------------------------------------ wrappers
+
+def f2h(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 bit patterns through the oracle's own conversion."""
+    f = lib().orc_f2h
+    flat = np.asarray(x, np.float32).ravel()
+    return np.fromiter((f(float(v)) for v in flat), np.uint16, flat.size).reshape(np.shape(x))
+
+
+def rope_cos_sin_tables(theta, head_dim, max_pos, scaling=0, factor=1.0, lo=1.0, hi=4.0,
+                        old_ctx=8192):
+    c = np.empty((max_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    lib().orc_rope_cos_sin_tables(theta, head_dim, scaling, factor, lo, hi, old_ctx, max_pos,
+                                  p(c), p(s))
+    return c, s
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    assert a.dtype == np.uint16
+    return a
+
+
+def embedding_lookup(ids, table, hidden):
+    ids = np.ascontiguousarray(ids, np.int32)
+    table = _u16(table)
+    out = np.empty((ids.size, hidden), np.uint16)
+    lib().orc_embedding_lookup(p(ids), p(table), ids.size, hidden, p(out))
+    return out.view(np.float16)
+
+
+def gather_rows(src, idx, cols):
+    idx = np.ascontiguousarray(idx, np.int32)
+    out = np.empty((idx.size, cols), np.uint16)
+    lib().orc_gather_rows(p(_u16(src)), p(idx), idx.size, cols, p(out))
+    return out.view(np.float16)
+
+
+def resolve_input_ids(ids, src, prev):
+    ids = np.array(ids, np.int32)
+    lib().orc_resolve_input_ids(p(ids), p(np.ascontiguousarray(src, np.int32)),
+                                p(np.ascontiguousarray(prev, np.int32)), ids.size)
+    return ids
+
+
+def fused_add_rmsnorm(residual, delta, weight, eps):
+    """Returns (new residual, out) as float16 arrays [rows, hidden]."""
+    res = np.array(_u16(residual), copy=True)
+    rows, hidden = res.shape
+    out = np.empty_like(res)
+    d = None if delta is None else _u16(delta)
+    lib().orc_fused_add_rmsnorm(p(res), p(d), p(_u16(weight)), rows, hidden, eps, p(out))
+    return res.view(np.float16), out.view(np.float16)
+
+
+def silu_and_mul(gate_up, inter, interleaved=False):
+    gu = _u16(gate_up)
+    rows = gu.size // (2 * inter)
+    out = np.empty((rows, inter), np.uint16)
+    fn = lib().orc_silu_and_mul_interleaved if interleaved else lib().orc_silu_and_mul
+    fn(p(gu), rows, inter, p(out))
+    return out.view(np.float16)
+
+
+def rope_and_write_kv(qkv, positions, slots, hq, hkv, d, cos_t, sin_t, k_cache, v_cache,
+                      k_scale=None, v_scale=None, block_size=16, int8=False):
+    """Updates qkv (fp16 [T, (hq+2hkv)*d]) and the caches in place."""
+    q = _u16(qkv)
+    assert q.flags.c_contiguous
+    positions = np.ascontiguousarray(positions, np.int32)
+    slots = np.ascontiguousarray(slots, np.int32)
+    T = positions.size
+    kc = k_cache.view(np.uint16) if k_cache.dtype == np.float16 else k_cache
+    vc = v_cache.view(np.uint16) if v_cache.dtype == np.float16 else v_cache
+    lib().orc_rope_and_write_kv(p(q), p(positions), p(slots), T, hq, hkv, d,
+                                p(np.ascontiguousarray(cos_t, np.float32)),
+                                p(np.ascontiguousarray(sin_t, np.float32)), p(kc), p(vc),
+                                p(k_scale), p(v_scale), block_size, int(int8))

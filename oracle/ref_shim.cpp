@@ -1,0 +1,105 @@
+// extern "C" entry points onto the reference's own host core (compiled from
+// /root/reference/src/core by oracle/Makefile's `ref` target).  TEST
+// INFRASTRUCTURE ONLY: used by tests/golden/make_golden.py to write golden
+// vectors and by tests/test_oracle.py to pin the oracle; never shipped.
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <vector>
+
+#include "core/batch_builder.h"
+#include "core/common.h"
+#include "core/model_config.h"
+
+using namespace redline;
+
+namespace {
+ModelConfig rope_cfg(double theta, int head_dim, int scaling, double factor, double lo, double hi,
+                     int old_ctx) {
+  ModelConfig c;
+  c.head_dim = head_dim;
+  c.rope_theta = theta;
+  c.rope_scaling.type = scaling == 1 ? "linear" : (scaling == 2 ? "llama3" : "none");
+  c.rope_scaling.factor = factor;
+  c.rope_scaling.low_freq_factor = lo;
+  c.rope_scaling.high_freq_factor = hi;
+  c.rope_scaling.original_max_position_embeddings = old_ctx;
+  return c;
+}
+}  // namespace
+
+extern "C" {
+
+uint16_t ref_float_to_half_bits(float f) { return float_to_half_bits(f); }
+float ref_half_bits_to_float(uint16_t h) { return half_bits_to_float(h); }
+
+void ref_float_to_half_many(const float* in, size_t n, uint16_t* out) {
+  for (size_t i = 0; i < n; ++i) out[i] = float_to_half_bits(in[i]);
+}
+
+void ref_rope_inv_freq(double theta, int head_dim, int scaling, double factor, double lo, double hi,
+                       int old_ctx, double* out) {
+  const auto v = rope_inv_freq(rope_cfg(theta, head_dim, scaling, factor, lo, hi, old_ctx));
+  std::memcpy(out, v.data(), v.size() * sizeof(double));
+}
+
+void ref_rope_cos_sin_tables(double theta, int head_dim, int scaling, double factor, double lo,
+                             double hi, int old_ctx, int max_pos, float* cos_t, float* sin_t) {
+  std::vector<float> c, s;
+  rope_cos_sin_tables(rope_cfg(theta, head_dim, scaling, factor, lo, hi, old_ctx), max_pos, &c, &s);
+  std::memcpy(cos_t, c.data(), c.size() * sizeof(float));
+  std::memcpy(sin_t, s.data(), s.size() * sizeof(float));
+}
+
+void* ref_bb_create(int max_tokens, int max_seqs, int max_rows, int max_blocks, int bs, int thr) {
+  return new BatchBuilder(max_tokens, max_seqs, max_rows, max_blocks, bs, thr);
+}
+void ref_bb_destroy(void* b) { delete static_cast<BatchBuilder*>(b); }
+size_t ref_bb_max_meta_words(void* b) { return static_cast<BatchBuilder*>(b)->max_meta_words(); }
+
+// Returns the first logits row (>= -1), or -2 when the reference threw.
+int ref_bb_add(void* b, const int32_t* tokens, int start_pos, int n, const int32_t* src_rows,
+               const int32_t* blocks, int num_blocks, float temperature, int top_k, float top_p,
+               uint64_t seed, int mode) {
+  SamplingParams sp;
+  sp.temperature = temperature;
+  sp.top_k = top_k;
+  sp.top_p = top_p;
+  sp.seed = seed;
+  const LogitsMode m = mode == 0 ? LogitsMode::kNone : (mode == 1 ? LogitsMode::kLast : LogitsMode::kAll);
+  try {
+    return static_cast<BatchBuilder*>(b)->add(tokens, start_pos, n, src_rows,
+                                              std::vector<int32_t>(blocks, blocks + num_blocks), sp, m);
+  } catch (const std::exception&) {
+    return -2;
+  }
+}
+
+void ref_bb_pad_decode_to(void* b, int n) { static_cast<BatchBuilder*>(b)->pad_decode_to(n); }
+
+void ref_bb_write(void* b, int32_t* dst, int* shape7) {
+  const BatchShape s = static_cast<BatchBuilder*>(b)->write(dst);
+  const int v[7] = {s.num_tokens, s.num_seqs, s.num_logit_rows, s.num_decode_items,
+                    s.num_prefill_seqs, s.max_prefill_q_tiles, s.max_context};
+  std::memcpy(shape7, v, sizeof(v));
+}
+
+void ref_meta_layout(const int* shape7, int max_blocks, size_t* out19) {
+  BatchShape s;
+  s.num_tokens = shape7[0];
+  s.num_seqs = shape7[1];
+  s.num_logit_rows = shape7[2];
+  s.num_decode_items = shape7[3];
+  s.num_prefill_seqs = shape7[4];
+  s.max_prefill_q_tiles = shape7[5];
+  s.max_context = shape7[6];
+  const MetaLayout m = MetaLayout::make(s, max_blocks);
+  const size_t v[19] = {m.input_ids,   m.input_src,   m.positions,    m.slot_mapping,
+                        m.seq_q_start, m.seq_q_len,   m.seq_ctx_len,  m.block_tables,
+                        m.decode_token, m.decode_seq, m.prefill_seq,  m.logit_token,
+                        m.param_row,   m.temperature, m.top_k,        m.top_p,
+                        m.seed_lo,     m.seed_hi,     m.total_words};
+  std::memcpy(out19, v, sizeof(v));
+}
+
+}  // extern "C"

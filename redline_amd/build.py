@@ -1,0 +1,60 @@
+"""Builds redline_amd/librlk.so (gfx950 HIP kernels + C ABI) with hipcc.
+
+Usage: python -m redline_amd.build   (or redline_amd.build.build_library()).
+The library is built in-tree so that it travels with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+OBJ = PKG / "_obj"
+LIB = PKG / "librlk.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+SOURCES = ["elementwise.hip", "rope_kv.hip", "host.cpp", "status.cpp"]
+
+COMMON = [
+    "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wextra",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+]
+# Device code: gfx950 only; packed-fp32 instructions disabled (they have
+# produced sporadic wrong results on this hardware pool).
+DEVICE = [
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics",
+]
+
+
+def _compile(src: str) -> Path:
+    out = OBJ / (src + ".o")
+    cmd = [HIPCC, *COMMON]
+    if src.endswith(".hip"):
+        cmd += [*DEVICE, "-x", "hip"]
+    cmd += ["-c", str(CSRC / src), "-o", str(out)]
+    subprocess.run(cmd, check=True)
+    return out
+
+
+def build_library(verbose: bool = True) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=4) as pool:
+        objs = list(pool.map(_compile, SOURCES))
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(LIB), *map(str, objs)]
+    subprocess.run(cmd, check=True)
+    if verbose:
+        print(f"built {LIB}", file=sys.stderr)
+    return LIB
+
+
+if __name__ == "__main__":
+    build_library()

@@ -1,0 +1,68 @@
+// Device-side building blocks for the gfx950 kernels: 128-bit vector types,
+// fp16 <-> fp32 conversion of 8-element packets, wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rlk {
+
+// Native clang vector types map to single 128-bit global_load/store_dwordx4.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ f32x8 unpack8(u32x4 v) {
+  return __builtin_convertvector(__builtin_bit_cast(f16x8, v), f32x8);
+}
+
+// Round-to-nearest-even fp32 -> fp16 of 8 values, packed into 16 bytes.
+__device__ __forceinline__ u32x4 pack8(f32x8 f) {
+  return __builtin_bit_cast(u32x4, __builtin_convertvector(f, f16x8));
+}
+
+// x rounded to fp16 and back (the rounding points of the fp16 activations).
+__device__ __forceinline__ f32x8 round_f16(f32x8 f) {
+  return __builtin_convertvector(__builtin_convertvector(f, f16x8), f32x8);
+}
+
+__device__ __forceinline__ float round_f16(float f) {
+  return static_cast<float>(static_cast<_Float16>(f));
+}
+
+// Butterfly reductions over all 64 lanes of a wavefront; every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Max over aligned groups of G consecutive lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Streaming variants: data touched once, keep it from displacing reused lines.
+__device__ __forceinline__ u32x4 load16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void store16_stream(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+}  // namespace rlk

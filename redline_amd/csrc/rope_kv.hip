@@ -1,0 +1,180 @@
+// Rotary position embedding fused with the paged KV-cache write, for gfx950.
+//
+// Work decomposition (wave64-first):
+//   * a head of D = 128 (64) elements holds D/2 rotation pairs (i, i + D/2);
+//     each lane owns 8 consecutive pairs, so a head is LPH = D/16 lanes and
+//     every lane moves its data with two 16-byte loads and two 16-byte stores
+//     (8 lanes of a D = 128 head write a full 256-byte cache row, coalesced);
+//   * one wave64 therefore covers 64/LPH heads of a token at once; WPT waves
+//     work on the same token, and the (token, head-group) loop walks the
+//     q, k, v heads of the row;
+//   * cos/sin for the lane's 8 pairs are loaded once per token (two float4
+//     each) and stay in registers for every head the lane visits — the
+//     register path needs no LDS staging;
+//   * INT8: the per-(token, head) absmax is a 3-step xor butterfly across the
+//     head's 8 lanes, no LDS and no barrier.
+// Numerics follow src/cuda/kernels/rope_kv.cu:44-84 (Neil456/Redline): the
+// rotation is evaluated in fp32 and rounded to fp16; INT8 uses
+// scale = amax / 127 (amax over the fp16-rounded values; 1 when amax is 0),
+// inv = 1 / scale, code = round-half-even(clamp(x * inv, -127, 127)).
+// Contraction into FMA is disabled in the rotation so that the rounding of
+// every intermediate is fixed by the source, and the INT8 codes are a
+// deterministic function of the inputs.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device.hpp"
+#include "redline_amd/rlk.h"
+#include "status.hpp"
+
+namespace rlk {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct RopeArgs {
+  _Float16* qkv;
+  const int32_t* positions;
+  const int32_t* slots;
+  const float* cos_t;
+  const float* sin_t;
+  void* k;
+  void* v;
+  float* k_scale;
+  float* v_scale;
+  int num_tokens;
+  int hq;
+  int hkv;
+  int block_size;
+};
+
+template <int D, bool kInt8, int WPT>
+__global__ __launch_bounds__(kThreads) void rope_kv_kernel(RopeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int kHalf = D / 2;
+  constexpr int kLPH = kHalf / 8;            // lanes per head
+  constexpr int kHeadsPerWave = kWave / kLPH;
+  constexpr int kTokPerBlock = kThreads / (kWave * WPT);
+  constexpr int kGroups = kHeadsPerWave * WPT;  // heads of one token in flight
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTokPerBlock + wave / WPT;
+  if (t >= a.num_tokens) return;  // uniform per wave
+  const int hg = (wave % WPT) * kHeadsPerWave + lane / kLPH;
+  const int p0 = (lane % kLPH) * 8;  // first pair index owned by this lane
+  const int heads = a.hq + 2 * a.hkv;
+  const int pos = a.positions[t];
+  const int slot = a.slots[t];
+
+  const float* cp = a.cos_t + static_cast<int64_t>(pos) * kHalf + p0;
+  const float* sp = a.sin_t + static_cast<int64_t>(pos) * kHalf + p0;
+  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp), c1 = *reinterpret_cast<const f32x4*>(cp + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+  const f32x8 c = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const f32x8 s = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+
+  _Float16* row = a.qkv + t * heads * D;
+  int blk = 0, off = 0;
+  if (slot >= 0) {
+    blk = slot / a.block_size;
+    off = slot - blk * a.block_size;
+  }
+  for (int h = hg; h < heads; h += kGroups) {  // all lanes of a head share h
+    _Float16* hp = row + h * D;
+    f32x8 x0 = unpack8(load16(hp + p0));
+    f32x8 x1 = unpack8(load16(hp + kHalf + p0));
+    if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
+      const f32x8 y0 = x0 * c - x1 * s;
+      const f32x8 y1 = x1 * c + x0 * s;
+      x0 = round_f16(y0);
+      x1 = round_f16(y1);
+    }
+    if (h < a.hq) {  // query: back in place
+      store16(hp + p0, pack8(x0));
+      store16(hp + kHalf + p0, pack8(x1));
+      continue;
+    }
+    if (slot < 0) continue;
+    const bool is_v = h >= a.hq + a.hkv;
+    const int kvh = is_v ? h - a.hq - a.hkv : h - a.hq;
+    const int64_t cell = (static_cast<int64_t>(blk) * a.hkv + kvh) * a.block_size + off;
+    if constexpr (!kInt8) {
+      _Float16* dst = static_cast<_Float16*>(is_v ? a.v : a.k) + cell * D;
+      store16(dst + p0, pack8(x0));
+      store16(dst + kHalf + p0, pack8(x1));
+    } else {
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fmaxf(__builtin_fabsf(x0[j]), __builtin_fabsf(x1[j])));
+      amax = group_max<kLPH>(amax);
+      const float scale = amax > 0.f ? amax / 127.f : 1.f;
+      const float inv = 1.f / scale;
+      i8x8 q0, q1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        q0[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x0[j] * inv, -127.f), 127.f)));
+        q1[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x1[j] * inv, -127.f), 127.f)));
+      }
+      int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
+      *reinterpret_cast<u32x2*>(dst + p0) = __builtin_bit_cast(u32x2, q0);
+      *reinterpret_cast<u32x2*>(dst + kHalf + p0) = __builtin_bit_cast(u32x2, q1);
+      if (p0 == 0) (is_v ? a.v_scale : a.k_scale)[cell] = scale;
+    }
+  }
+}
+
+template <int D, bool kInt8>
+void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
+  const int tok_per_block = kThreads / (kWave * wpt);
+  const int blocks = (a.num_tokens + tok_per_block - 1) / tok_per_block;
+  switch (wpt) {
+    case 1: rope_kv_kernel<D, kInt8, 1><<<blocks, kThreads, 0, stream>>>(a); break;
+    case 2: rope_kv_kernel<D, kInt8, 2><<<blocks, kThreads, 0, stream>>>(a); break;
+    default: rope_kv_kernel<D, kInt8, 4><<<blocks, kThreads, 0, stream>>>(a); break;
+  }
+}
+
+}  // namespace
+}  // namespace rlk
+
+using namespace rlk;
+
+extern "C" int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions,
+                                     const int32_t* slot_mapping, int num_tokens, int num_heads,
+                                     const float* cos_table, const float* sin_table,
+                                     const rlk_kv_layer_view* kv, hipStream_t stream) {
+  if (num_tokens <= 0) return RLK_OK;
+  if (kv == nullptr) return fail(RLK_EINVAL, "rope_and_write_kv: null KV layer view");
+  if (kv->head_dim != 64 && kv->head_dim != 128)
+    return fail(RLK_EUNSUPPORTED, "unsupported head_dim %d (supported: 64, 128)", kv->head_dim);
+  if (kv->dtype != RLK_KV_FP16 && kv->dtype != RLK_KV_INT8)
+    return fail(RLK_EINVAL, "rope_and_write_kv: unknown KV dtype %d", kv->dtype);
+  if (num_heads < 0 || kv->num_kv_heads < 0 || kv->block_size <= 0)
+    return fail(RLK_EINVAL, "rope_and_write_kv: bad head counts (%d, %d) or block size %d",
+                num_heads, kv->num_kv_heads, kv->block_size);
+  RopeArgs a;
+  a.qkv = reinterpret_cast<_Float16*>(qkv);
+  a.positions = positions;
+  a.slots = slot_mapping;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.k = kv->k;
+  a.v = kv->v;
+  a.k_scale = kv->k_scale;
+  a.v_scale = kv->v_scale;
+  a.num_tokens = num_tokens;
+  a.hq = num_heads;
+  a.hkv = kv->num_kv_heads;
+  a.block_size = kv->block_size;
+  // Waves per token: several for decode-sized batches (more heads in flight
+  // per token, more CUs busy), one once the batch alone fills the chip.
+  int wpt = num_tokens >= 2048 ? 1 : (num_tokens >= 512 ? 2 : 4);
+  wpt = tune_knob("RLK_TUNE_ROPE_WPT", wpt);
+  const bool int8 = kv->dtype == RLK_KV_INT8;
+  if (kv->head_dim == 128) {
+    int8 ? launch_d<128, true>(a, wpt, stream) : launch_d<128, false>(a, wpt, stream);
+  } else {
+    int8 ? launch_d<64, true>(a, wpt, stream) : launch_d<64, false>(a, wpt, stream);
+  }
+  return launch_status("rope_and_write_kv");
+}

@@ -1,0 +1,167 @@
+"""Python launch interface over the C ABI, mirroring redline::kernels.
+
+Names, parameter order and meaning follow the reference's launchers
+(src/cuda/kernels/kernels.h:64-88 in Neil456/Redline).  Arguments are torch
+tensors on the GPU (device memory and streams come from PyTorch; the compute
+is the HIP code in librlk.so).  Errors raise redline_amd.Error before anything
+is launched, as the reference's RL_CHECK throws.  Every launcher is
+asynchronous on `stream` (default: torch's current stream).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import KVLayerView, check, lib
+
+__all__ = [
+    "embedding_lookup", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
+    "gather_rows", "resolve_input_ids", "rope_and_write_kv", "KVDType", "KVCache",
+]
+
+
+class KVDType:
+    kFP16 = _lib.RLK_KV_FP16
+    kINT8 = _lib.RLK_KV_INT8
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def _ptr(t, dtype, what, allow_none=False):
+    if t is None:
+        if allow_none:
+            return None
+        raise _lib.Error(_lib.RLK_EINVAL, f"{what} must not be None")
+    if not isinstance(t, torch.Tensor):
+        raise _lib.Error(_lib.RLK_EINVAL, f"{what} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise _lib.Error(_lib.RLK_EINVAL, f"{what} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise _lib.Error(_lib.RLK_EINVAL, f"{what} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise _lib.Error(_lib.RLK_EINVAL, f"{what} must be contiguous")
+    return t.data_ptr()
+
+
+def _need(t, n, what):
+    if t is not None and t.numel() < n:
+        raise _lib.Error(_lib.RLK_EINVAL, f"{what} holds {t.numel()} elements, needs {n}")
+
+
+def embedding_lookup(ids, table, n, hidden, out, stream=None):
+    """out[t, :] = table[ids[t], :] for t < n (kernels::embedding_lookup)."""
+    if n > 0:
+        _need(ids, n, "ids"); _need(out, n * hidden, "out")
+    check(lib().rlk_embedding_lookup(_ptr(ids, torch.int32, "ids"), _ptr(table, torch.float16, "table"),
+                                     n, hidden, _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def fused_add_rmsnorm(residual, delta, weight, rows, hidden, eps, out, stream=None):
+    """residual += delta (unless None); out = rmsnorm(residual) * weight."""
+    if rows > 0:
+        for t, w in ((residual, "residual"), (delta, "delta"), (out, "out")):
+            _need(t, rows * hidden, w)
+        _need(weight, hidden, "weight")
+    check(lib().rlk_fused_add_rmsnorm(
+        _ptr(residual, torch.float16, "residual"), _ptr(delta, torch.float16, "delta", True),
+        _ptr(weight, torch.float16, "weight"), rows, hidden, float(eps),
+        _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def silu_and_mul(gate_up, rows, inter, out, stream=None):
+    """out[r, i] = silu(gate_up[r, i]) * gate_up[r, inter + i]."""
+    if rows > 0:
+        _need(gate_up, rows * 2 * inter, "gate_up"); _need(out, rows * inter, "out")
+    check(lib().rlk_silu_and_mul(_ptr(gate_up, torch.float16, "gate_up"), rows, inter,
+                                 _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def silu_and_mul_interleaved(gate_up, rows, inter, out, stream=None):
+    """Same with (gate_i, up_i) interleaved columns."""
+    if rows > 0:
+        _need(gate_up, rows * 2 * inter, "gate_up"); _need(out, rows * inter, "out")
+    check(lib().rlk_silu_and_mul_interleaved(_ptr(gate_up, torch.float16, "gate_up"), rows, inter,
+                                             _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def gather_rows(src, idx, n, cols, dst, stream=None):
+    """dst[i, :] = src[idx[i], :]."""
+    if n > 0:
+        _need(idx, n, "idx"); _need(dst, n * cols, "dst")
+    check(lib().rlk_gather_rows(_ptr(src, torch.float16, "src"), _ptr(idx, torch.int32, "idx"), n, cols,
+                                _ptr(dst, torch.float16, "dst"), _stream(stream)))
+
+
+def resolve_input_ids(input_ids, src, prev_sampled, n, stream=None):
+    """input_ids[i] = prev_sampled[src[i]] where src[i] >= 0."""
+    if n > 0:
+        _need(input_ids, n, "input_ids"); _need(src, n, "src")
+    check(lib().rlk_resolve_input_ids(_ptr(input_ids, torch.int32, "input_ids"),
+                                      _ptr(src, torch.int32, "src"),
+                                      _ptr(prev_sampled, torch.int32, "prev_sampled"), n,
+                                      _stream(stream)))
+
+
+def rope_and_write_kv(qkv, positions, slot_mapping, num_tokens, num_heads, cos_table, sin_table,
+                      kv: KVLayerView, stream=None):
+    """RoPE on q/k heads (q in place) and paged KV write at slot_mapping[t]."""
+    if num_tokens > 0:
+        _need(positions, num_tokens, "positions"); _need(slot_mapping, num_tokens, "slot_mapping")
+        _need(qkv, num_tokens * (num_heads + 2 * kv.num_kv_heads) * kv.head_dim, "qkv")
+    check(lib().rlk_rope_and_write_kv(
+        _ptr(qkv, torch.float16, "qkv"), _ptr(positions, torch.int32, "positions"),
+        _ptr(slot_mapping, torch.int32, "slot_mapping"), num_tokens, num_heads,
+        _ptr(cos_table, torch.float32, "cos_table"), _ptr(sin_table, torch.float32, "sin_table"),
+        C.byref(kv), _stream(stream)))
+
+
+class KVCache:
+    """Paged KV cache in one zeroed device allocation, laid out per layer as
+    K, V (then k_scale, v_scale for INT8), each [num_blocks, Hkv, bs, D]
+    (scales [num_blocks, Hkv, bs] fp32) — the layout of the reference's
+    KVCache (src/cuda/model/kv_cache.cpp:25-52).  Block 0 is the scratch block
+    that padded rows write into."""
+
+    def __init__(self, num_layers, num_blocks, num_kv_heads, head_dim, block_size=16,
+                 dtype=KVDType.kFP16, device="cuda"):
+        if num_blocks <= 1 or block_size <= 0 or num_layers <= 0:
+            raise _lib.Error(_lib.RLK_EINVAL, "bad KV cache config")
+        self.num_layers, self.num_blocks = num_layers, num_blocks
+        self.num_kv_heads, self.head_dim, self.block_size, self.dtype = (
+            num_kv_heads, head_dim, block_size, dtype)
+        cells = num_blocks * num_kv_heads * block_size
+        elem = 2 if dtype == KVDType.kFP16 else 1
+        per_layer = 2 * cells * head_dim * elem + (2 * cells * 4 if dtype == KVDType.kINT8 else 0)
+        self.storage = torch.zeros(per_layer * num_layers, dtype=torch.uint8, device=device)
+        self._views, self._tensors = [], []
+        shape = (num_blocks, num_kv_heads, block_size, head_dim)
+        tdt = torch.float16 if dtype == KVDType.kFP16 else torch.int8
+        off = 0
+        for _ in range(num_layers):
+            kb = cells * head_dim * elem
+            k = self.storage[off:off + kb].view(tdt).view(shape); off += kb
+            v = self.storage[off:off + kb].view(tdt).view(shape); off += kb
+            ks = vs = None
+            if dtype == KVDType.kINT8:
+                ks = self.storage[off:off + cells * 4].view(torch.float32).view(shape[:3]); off += cells * 4
+                vs = self.storage[off:off + cells * 4].view(torch.float32).view(shape[:3]); off += cells * 4
+            view = KVLayerView(k.data_ptr(), v.data_ptr(), ks.data_ptr() if ks is not None else None,
+                               vs.data_ptr() if vs is not None else None, block_size, num_kv_heads,
+                               head_dim, dtype)
+            self._views.append(view)
+            self._tensors.append((k, v, ks, vs))
+
+    def layer(self, i) -> KVLayerView:
+        return self._views[i]
+
+    def tensors(self, i):
+        """(k, v, k_scale, v_scale) torch views of layer i (scales None for FP16)."""
+        return self._tensors[i]

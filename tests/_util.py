@@ -1,0 +1,53 @@
+"""Shared helpers for the parity tests."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+# Tolerances for fp16 outputs (fp32 accumulation): elementwise
+# |a - b| <= ATOL + RTOL * |b|, plus the reference's own metric
+# max|a - b| / max|b| <= REL_MAX (tests/cuda/cuda_test_utils.h:83-90).
+ATOL = 2e-3
+RTOL = 1e-2
+REL_MAX = 2e-3
+
+
+def say(*msg):
+    """Names the case on stdout before a GPU step (flushed, survives a crash)."""
+    print(*msg, flush=True)
+    sys.stdout.flush()
+
+
+def randn_f16(rng: np.random.Generator, shape, std=1.0, mean=0.0) -> np.ndarray:
+    return (rng.standard_normal(shape, dtype=np.float32) * std + mean).astype(np.float16)
+
+
+def rel_max_err(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / (np.max(np.abs(b)) + 1e-12)) if a.size else 0.0
+
+
+def assert_close_f16(got, want, atol=ATOL, rtol=RTOL, rel_max=REL_MAX, what=""):
+    g = np.asarray(got, np.float32)
+    w = np.asarray(want, np.float32)
+    assert g.shape == w.shape, (what, g.shape, w.shape)
+    assert np.all(np.isfinite(g) == np.isfinite(w)), f"{what}: finiteness differs"
+    fin = np.isfinite(w)
+    diff = np.abs(g[fin] - w[fin])
+    bound = atol + rtol * np.abs(w[fin])
+    bad = diff > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of tolerance; worst "
+                           f"diff {float(diff.max()):.3g}")
+    assert rel_max_err(g[fin], w[fin]) <= rel_max, f"{what}: rel max err {rel_max_err(g[fin], w[fin])}"
+
+
+def assert_bits_equal(got, want, what=""):
+    g = np.ascontiguousarray(got)
+    w = np.ascontiguousarray(want)
+    assert g.shape == w.shape, (what, g.shape, w.shape)
+    gv, wv = g.view(np.uint8), w.view(np.uint8)
+    if not np.array_equal(gv, wv):
+        n = int(np.sum(g.reshape(-1) != w.reshape(-1)))
+        raise AssertionError(f"{what}: {n} elements differ bitwise")
