@@ -56,8 +56,10 @@ class LayerData:
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         dtype = K.KVDType.kINT8 if w.kv_int8 else K.KVDType.kFP16
         self.cache = K.KVCache(1, w.num_blocks, m.hkv, m.head_dim, w.block_size, dtype)
-        set_bytes = T * (2 * m.hidden * 3 + 2 * m.qkv_cols + 6 * m.inter)
-        self.R = rotations or max(2, min(256, -(-ROTATE_BYTES // set_bytes)))
+        # enough sets that every kernel's own footprint over the rotation
+        # exceeds twice the Infinity Cache
+        smallest = min(self.bytes().values())
+        self.R = rotations or max(2, min(1024, -(-ROTATE_BYTES // smallest)))
         rng = np.random.default_rng(seed + 17)
         self.sets = []
         for r in range(self.R):
@@ -114,6 +116,17 @@ class LayerData:
             "rope_and_write_kv": C.bytes_rope_kv(T, m.hq, m.hkv, m.head_dim, self.w.kv_int8),
             "silu_and_mul": C.bytes_swiglu(T, m.inter),
         }
+
+
+def copy_baseline(torch, nbytes=1 << 30, reps=20):
+    """A plain device-to-device copy (torch) of `nbytes`: the practical
+    streaming ceiling, read + write bytes counted."""
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    g = capture(torch, lambda: dst.copy_(src))
+    ms = time_graph(torch, g, reps)
+    del g, src, dst
+    return round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
 
 
 def capture(torch, fn):
@@ -213,6 +226,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-calls", type=int, default=0,
+                    help="counter-collection mode: N eager calls of each kernel (rotating sets) "
+                         "plus N copies of 256 MiB for calibration, then exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the fused per-layer kernels are row-independent "
@@ -230,6 +246,24 @@ def main():
     data = LayerData(torch, K, w)
     nb = data.bytes()
     step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
+
+    if args.profile_calls:
+        fns = {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
+               "rope_and_write_kv": data.rope, "silu_and_mul": data.swiglu}
+        for name in KERNELS:
+            if args.only and name != args.only:
+                continue
+            for i in range(args.profile_calls):
+                fns[name](i % data.R)
+        src = torch.empty(128 << 20, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.profile_calls):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_calls": args.profile_calls, "workload": w.key,
+                          "bytes_per_call": nb, "copy_bytes": 2 * src.numel() * 2,
+                          "rotating_input_sets": data.R}))
+        return
 
     result = {}
     if args.only is None:
@@ -273,6 +307,9 @@ def main():
             del dx
             torch.cuda.empty_cache()
 
+    copy = copy_baseline(torch)
+    log(f"device copy baseline: {copy} GB/s")
+
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle) ...")
@@ -296,6 +333,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kern,
         "prefill": extra,
+        "copy_baseline_gb_per_s": copy,
     }
     print(json.dumps(line))
 

@@ -16,6 +16,6 @@ def __getattr__(name):
     # The torch-facing launchers import torch lazily so host-only users
     # (metadata, tables) do not pay for it.
     if name == "kernels":
-        from . import kernels
-        return kernels
+        import importlib
+        return importlib.import_module(".kernels", __name__)
     raise AttributeError(name)

@@ -57,12 +57,30 @@ __device__ __forceinline__ u32x4 load16(const void* p) {
 }
 __device__ __forceinline__ void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-// Streaming variants: data touched once, keep it from displacing reused lines.
-__device__ __forceinline__ u32x4 load16_stream(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// 16-byte access with a compile-time cache policy: kNT selects the
+// non-temporal (streaming) variant for data touched exactly once, which keeps
+// it from displacing reused lines and measurably raises HBM throughput of
+// large streaming launches on gfx950.
+template <bool kNT>
+__device__ __forceinline__ u32x4 ld16(const u32x4* p) {
+  if constexpr (kNT) return __builtin_nontemporal_load(p);
+  return *p;
 }
-__device__ __forceinline__ void store16_stream(void* p, u32x4 v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+template <bool kNT>
+__device__ __forceinline__ void st16(u32x4* p, u32x4 v) {
+  if constexpr (kNT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
+template <bool kNT>
+__device__ __forceinline__ void st8(u32x2* p, u32x2 v) {
+  if constexpr (kNT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
 }
 
 }  // namespace rlk

@@ -1,11 +1,15 @@
 // Row-streaming kernels for gfx950: embedding gather / row gather, fused
 // residual-add + RMSNorm, SwiGLU (split and interleaved), input-id resolve.
 //
-// All of them are HBM-bound (a few flops per byte), so the design goal is to
-// keep enough 128-bit loads in flight per CU: every lane issues its NV
-// 16-byte loads before it consumes any of them, workgroups are 256 lanes (four
-// wave64s), and the grid is sized so that small batches still spread over many
-// CUs.  Numerics follow the reference kernels' fp16 rounding points
+// All of them are HBM-bound (a few flops per byte).  What sets their speed on
+// MI355X is how many 16-byte accesses are in flight and how the memory system
+// treats them, so every kernel is templated on
+//   BS  lanes per workgroup (64 = one wave64: the most workgroups, which
+//       spreads a launch evenly over the 256 CUs / 8 XCDs),
+//   NT  non-temporal (streaming) loads/stores, which measured faster than
+//       cached accesses at every launch size from decode b32 to 16k rows,
+// and the launch policy (`pick_flat`, the norm/rope launchers) chooses them.
+// Numerics follow the reference kernels' fp16 rounding points
 // (src/cuda/kernels/elementwise.cu:29-82,123-131 in Neil456/Redline).
 #include <hip/hip_runtime.h>
 
@@ -19,94 +23,100 @@
 namespace rlk {
 namespace {
 
-constexpr int kThreads = 256;
+struct FlatPolicy {
+  int bs;   // lanes per workgroup: 64, 128 or 256
+  bool nt;  // non-temporal accesses
+};
+
+// Launch policy of the flat streaming kernels (measured on MI355X with cold,
+// rotating buffers at decode b32 and 4k-16k-row prefill shapes): non-temporal
+// accesses were faster at every size, by 8-20%; the best block width depends
+// weakly on the launch size.  RLK_TUNE_<NAME>_BS / _NT override the policy for
+// tuning runs.
+FlatPolicy pick_flat(int bs, const char* bs_knob, const char* nt_knob) {
+  FlatPolicy p;
+  p.bs = tune_knob(bs_knob, bs);
+  p.nt = tune_knob(nt_knob, 1) != 0;
+  return p;
+}
+
+// The flat kernels index the [rows, vecs] space of 16-byte vectors: lane l of
+// block b handles vector b * BS + l, so every wave access is 1 KiB
+// contiguous (except at row ends) and no lane idles when a row is not a
+// multiple of the block width.
 
 // ------------------------------------------------------------------ gathers
 
 // dst[r, :] = src[idx ? idx[r] : r, :] for rows of `vecs` 16-byte vectors.
-// Block b copies chunk (b % chunks) of row (b / chunks); a chunk is
-// kThreads * NV vectors, each lane loading its NV vectors before storing.
-template <int NV>
-__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const int32_t* __restrict__ idx,
-                                                               const u32x4* __restrict__ src,
-                                                               int vecs, int chunks,
-                                                               u32x4* __restrict__ dst) {
-  const int64_t row = blockIdx.x / chunks;
-  const int chunk = blockIdx.x - static_cast<int>(row) * chunks;
-  const int64_t src_row = idx != nullptr ? idx[row] : row;
-  const u32x4* s = src + src_row * vecs;
-  u32x4* d = dst + row * vecs;
-  const int base = chunk * kThreads * NV + threadIdx.x;
-  u32x4 v[NV];
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = base + k * kThreads;
-    if (i < vecs) v[k] = s[i];
-  }
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = base + k * kThreads;
-    if (i < vecs) d[i] = v[k];
-  }
+template <int BS, bool NT>
+__global__ __launch_bounds__(BS) void gather_rows_kernel(const int32_t* __restrict__ idx,
+                                                         const u32x4* __restrict__ src,
+                                                         uint32_t vecs, uint32_t total,
+                                                         u32x4* __restrict__ dst) {
+  const uint32_t g = blockIdx.x * BS + threadIdx.x;
+  if (g >= total) return;
+  const uint32_t row = g / vecs;
+  const uint32_t col = g - row * vecs;
+  const uint64_t srow = idx != nullptr ? static_cast<uint32_t>(idx[row]) : row;
+  st16<NT>(dst + g, ld16<NT>(src + srow * vecs + col));
 }
 
-// Vectors per lane for a row-chunked launch: the largest NV in {1, 2, 4} that
-// still leaves at least `min_blocks` workgroups (small batches favour more,
-// smaller blocks; large ones favour more bytes in flight per lane).
-int pick_nv(int64_t rows, int vecs, int64_t min_blocks) {
-  int nv = 4;
-  while (nv > 1) {
-    const int64_t chunks = (vecs + kThreads * nv - 1) / (kThreads * nv);
-    if (rows * chunks >= min_blocks) break;
-    nv >>= 1;
+template <int BS>
+void launch_gather_bs(bool nt, uint64_t blocks, const int32_t* idx, const u32x4* s, uint32_t vecs,
+                      uint32_t total, u32x4* d, hipStream_t stream) {
+  if (nt) {
+    gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, total, d);
+  } else {
+    gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, total, d);
   }
-  return nv;
 }
 
 int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* dst,
                   hipStream_t stream, const char* what) {
-  const int nv = tune_knob("RLK_TUNE_GATHER_NV", pick_nv(n, vecs, 2048));
-  const int chunks = (vecs + kThreads * nv - 1) / (kThreads * nv);
-  const int64_t blocks = static_cast<int64_t>(n) * chunks;
-  if (blocks > 0x7fffffff) return fail(RLK_EINVAL, "%s: too many rows (%d)", what, n);
+  const uint64_t total = static_cast<uint64_t>(n) * vecs;
+  if (total > 0x7fffffffull)
+    return fail(RLK_EINVAL, "%s: %d rows x %d vectors exceed one launch; split the call", what, n,
+                vecs);
+  const FlatPolicy p = pick_flat(total >= (1u << 20) ? 256 : 128, "RLK_TUNE_GATHER_BS",
+                                 "RLK_TUNE_GATHER_NT");
+  const uint64_t blocks = (total + p.bs - 1) / p.bs;
   const auto* s = static_cast<const u32x4*>(src);
   auto* d = static_cast<u32x4*>(dst);
-  switch (nv) {
-    case 1: gather_rows_kernel<1><<<blocks, kThreads, 0, stream>>>(idx, s, vecs, chunks, d); break;
-    case 2: gather_rows_kernel<2><<<blocks, kThreads, 0, stream>>>(idx, s, vecs, chunks, d); break;
-    default: gather_rows_kernel<4><<<blocks, kThreads, 0, stream>>>(idx, s, vecs, chunks, d); break;
+  const uint32_t t32 = static_cast<uint32_t>(total);
+  switch (p.bs) {
+    case 128: launch_gather_bs<128>(p.nt, blocks, idx, s, vecs, t32, d, stream); break;
+    case 256: launch_gather_bs<256>(p.nt, blocks, idx, s, vecs, t32, d, stream); break;
+    default: launch_gather_bs<64>(p.nt, blocks, idx, s, vecs, t32, d, stream); break;
   }
   return launch_status(what);
 }
 
 // ----------------------------------------------------------- add + RMSNorm
 
-// TPR lanes own one row; the row lives in registers (NV vectors per lane), so
-// the residual is read once, the sum of squares is a wave64 butterfly (plus a
-// tiny LDS exchange when TPR > 64), and the output pass needs no re-read.
-// Rounding points follow elementwise.cu:45,52,61: the residual sum is rounded
-// to fp16, the sum of squares is fp32, x * inv is rounded to fp16 before the
-// fp16 weight multiply.
-template <int TPR, int NV, bool kDelta>
-__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
+// One workgroup of TPR lanes owns one row, held in registers (NV vectors of 8
+// halves per lane): the residual is read once, the sum of squares is a wave64
+// butterfly plus one LDS exchange when TPR > 64, and the output pass needs no
+// re-read.  Rounding points follow elementwise.cu:45,52,61: the residual sum
+// is rounded to fp16, the sum of squares is fp32, x * inv is rounded to fp16
+// before the fp16 weight multiply.
+template <int TPR, int NV, bool kDelta, bool NT>
+__global__ __launch_bounds__(TPR) void add_rmsnorm_kernel(
     u32x4* __restrict__ residual, const u32x4* __restrict__ delta,
-    const u32x4* __restrict__ weight, int rows, int vecs, float hidden, float eps,
+    const u32x4* __restrict__ weight, int vecs, float hidden, float eps,
     u32x4* __restrict__ out) {
-  constexpr int kRowsPerBlock = kThreads / TPR;
-  constexpr int kWavesPerRow = TPR / kWave;
-  __shared__ float partial[kThreads / kWave];
-  const int lt = threadIdx.x % TPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
-  const bool active = row < rows;
+  constexpr int kWaves = TPR / kWave;
+  __shared__ float partial[kWaves];
+  const int lt = threadIdx.x;
+  const int64_t row = blockIdx.x;
   u32x4* res = residual + row * vecs;
 
   u32x4 rv[NV], dv[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = lt + k * TPR;
-    const bool ok = active && i < vecs;
-    rv[k] = ok ? res[i] : u32x4{0, 0, 0, 0};
-    if constexpr (kDelta) dv[k] = ok ? delta[row * vecs + i] : u32x4{0, 0, 0, 0};
+    const bool ok = i < vecs;
+    rv[k] = ok ? ld16<NT>(res + i) : u32x4{0, 0, 0, 0};
+    if constexpr (kDelta) dv[k] = ok ? ld16<NT>(delta + row * vecs + i) : u32x4{0, 0, 0, 0};
   }
   f32x8 x[NV];
   float ss = 0.f;
@@ -116,43 +126,40 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
     if constexpr (kDelta) {
       x[k] = round_f16(x[k] + unpack8(dv[k]));
       const int i = lt + k * TPR;
-      if (active && i < vecs) res[i] = pack8(x[k]);
+      if (i < vecs) st16<NT>(res + i, pack8(x[k]));
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += x[k][j] * x[k][j];
   }
   ss = wave_sum(ss);
-  if constexpr (kWavesPerRow > 1) {
-    const int wave = threadIdx.x / kWave;
-    if (threadIdx.x % kWave == 0) partial[wave] = ss;
+  if constexpr (kWaves > 1) {
+    if (lt % kWave == 0) partial[lt / kWave] = ss;
     __syncthreads();
-    const int first = (threadIdx.x / TPR) * kWavesPerRow;
     ss = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWavesPerRow; ++w) ss += partial[first + w];
+    for (int w = 0; w < kWaves; ++w) ss += partial[w];
   }
   const float inv = 1.0f / __builtin_sqrtf(ss / hidden + eps);
-  if (!active) return;
   u32x4* o = out + row * vecs;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = lt + k * TPR;
-    if (i < vecs) o[i] = pack8(round_f16(x[k] * inv) * unpack8(weight[i]));
+    if (i < vecs) st16<NT>(o + i, pack8(round_f16(x[k] * inv) * unpack8(weight[i])));
   }
 }
 
 // Rows wider than the register-resident variants cover: one block per row,
 // two passes (the second re-reads the residual from cache).
 template <bool kDelta>
-__global__ __launch_bounds__(kThreads) void add_rmsnorm_wide_kernel(
+__global__ __launch_bounds__(256) void add_rmsnorm_wide_kernel(
     u32x4* __restrict__ residual, const u32x4* __restrict__ delta,
     const u32x4* __restrict__ weight, int vecs, float hidden, float eps,
     u32x4* __restrict__ out) {
-  __shared__ float partial[kThreads / kWave];
+  __shared__ float partial[256 / kWave];
   const int64_t row = blockIdx.x;
   u32x4* res = residual + row * vecs;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < vecs; i += kThreads) {
+  for (int i = threadIdx.x; i < vecs; i += 256) {
     f32x8 x = unpack8(res[i]);
     if constexpr (kDelta) {
       x = round_f16(x + unpack8(delta[row * vecs + i]));
@@ -166,34 +173,39 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_wide_kernel(
   __syncthreads();
   ss = 0.f;
 #pragma unroll
-  for (int w = 0; w < kThreads / kWave; ++w) ss += partial[w];
+  for (int w = 0; w < 256 / kWave; ++w) ss += partial[w];
   const float inv = 1.0f / __builtin_sqrtf(ss / hidden + eps);
   u32x4* o = out + row * vecs;
-  for (int i = threadIdx.x; i < vecs; i += kThreads)
+  for (int i = threadIdx.x; i < vecs; i += 256)
     o[i] = pack8(round_f16(unpack8(res[i]) * inv) * unpack8(weight[i]));
 }
 
-template <int TPR, int NV>
-void launch_norm_tn(u32x4* res, const u32x4* del, const u32x4* w, int rows, int vecs,
-                    float hidden_f, float eps, u32x4* out, hipStream_t stream) {
-  constexpr int rpb = kThreads / TPR;
-  const int blocks = (rows + rpb - 1) / rpb;
-  if (del != nullptr) {
-    add_rmsnorm_kernel<TPR, NV, true>
-        <<<blocks, kThreads, 0, stream>>>(res, del, w, rows, vecs, hidden_f, eps, out);
+struct NormArgs {
+  u32x4* res;
+  const u32x4* del;
+  const u32x4* w;
+  int rows, vecs;
+  float hidden, eps;
+  u32x4* out;
+};
+
+template <int TPR, int NV, bool NT>
+void launch_norm_tn(const NormArgs& a, hipStream_t stream) {
+  if (a.del != nullptr) {
+    add_rmsnorm_kernel<TPR, NV, true, NT>
+        <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out);
   } else {
-    add_rmsnorm_kernel<TPR, NV, false>
-        <<<blocks, kThreads, 0, stream>>>(res, del, w, rows, vecs, hidden_f, eps, out);
+    add_rmsnorm_kernel<TPR, NV, false, NT>
+        <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out);
   }
 }
 
 // Register-resident variants: NV vectors (8 halves each) per lane.
-template <int TPR>
-bool launch_norm_t(int nv, u32x4* res, const u32x4* del, const u32x4* w, int rows, int vecs,
-                   float hidden_f, float eps, u32x4* out, hipStream_t stream) {
-#define RLK_NORM_CASE(N)                                                                    \
-  case N:                                                                                   \
-    launch_norm_tn<TPR, N>(res, del, w, rows, vecs, hidden_f, eps, out, stream);          \
+template <int TPR, bool NT>
+bool launch_norm_t(int nv, const NormArgs& a, hipStream_t stream) {
+#define RLK_NORM_CASE(N)                     \
+  case N:                                    \
+    launch_norm_tn<TPR, N, NT>(a, stream);   \
     return true;
   switch (nv) {
     RLK_NORM_CASE(1)
@@ -217,6 +229,18 @@ int round_up_nv(int nv) {
   return nv <= 16 ? 16 : -1;
 }
 
+template <bool NT>
+bool launch_norm_nt(int tpr, const NormArgs& a, hipStream_t stream) {
+  const int nv = round_up_nv((a.vecs + tpr - 1) / tpr);
+  if (nv < 0) return false;
+  switch (tpr) {
+    case 64: return launch_norm_t<64, NT>(nv, a, stream);
+    case 128: return launch_norm_t<128, NT>(nv, a, stream);
+    case 512: return launch_norm_t<512, NT>(nv, a, stream);
+    default: return launch_norm_t<256, NT>(nv, a, stream);
+  }
+}
+
 // ------------------------------------------------------------------ SwiGLU
 
 // silu(g) rounded to fp16 (elementwise.cu:77), then times up.  exp and the
@@ -226,88 +250,81 @@ __device__ __forceinline__ float silu_f16(float g) {
   return round_f16(__fdividef(g, 1.0f + __expf(-g)));
 }
 
-// Split layout: gate in [r, 0:I], up in [r, I:2I].  Block b handles chunk
-// (b % chunks) of row (b / chunks), kThreads * NV output vectors per chunk.
-template <int NV>
-__global__ __launch_bounds__(kThreads) void silu_and_mul_kernel(const u32x4* __restrict__ gate_up,
-                                                                int vecs, int chunks,
-                                                                u32x4* __restrict__ out) {
-  const int64_t row = blockIdx.x / chunks;
-  const int chunk = blockIdx.x - static_cast<int>(row) * chunks;
-  const u32x4* g = gate_up + row * 2 * vecs;
-  const u32x4* u = g + vecs;
-  u32x4* o = out + row * vecs;
-  const int base = chunk * kThreads * NV + threadIdx.x;
-  u32x4 gv[NV], uv[NV];
+// Split layout: gate in [r, 0:I], up in [r, I:2I]; flat over the [rows, vecs]
+// output vectors (vecs = I / 8).
+template <int BS, bool NT>
+__global__ __launch_bounds__(BS) void silu_and_mul_kernel(const u32x4* __restrict__ gate_up,
+                                                          uint32_t vecs, uint32_t total,
+                                                          u32x4* __restrict__ out) {
+  const uint32_t g = blockIdx.x * BS + threadIdx.x;
+  if (g >= total) return;
+  const uint32_t row = g / vecs;
+  const uint64_t at = static_cast<uint64_t>(g) + static_cast<uint64_t>(row) * vecs;
+  const u32x4 gv = ld16<NT>(gate_up + at);
+  const u32x4 uv = ld16<NT>(gate_up + at + vecs);
+  const f32x8 gf = unpack8(gv);
+  f32x8 s;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = base + k * kThreads;
-    if (i < vecs) {
-      gv[k] = g[i];
-      uv[k] = u[i];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = base + k * kThreads;
-    if (i < vecs) {
-      const f32x8 gf = unpack8(gv[k]);
-      f32x8 s;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s[j] = silu_f16(gf[j]);
-      o[i] = pack8(s * unpack8(uv[k]));
-    }
-  }
+  for (int j = 0; j < 8; ++j) s[j] = silu_f16(gf[j]);
+  st16<NT>(out + g, pack8(s * unpack8(uv)));
 }
 
-// Interleaved layout (gate_i, up_i): each lane reads two 16-byte vectors (8
-// pairs) and writes one 16-byte vector of 8 outputs.  Needs inter % 8 == 0.
-template <int NV>
-__global__ __launch_bounds__(kThreads) void silu_and_mul_interleaved_kernel(
-    const u32x4* __restrict__ gate_up, int vecs, int chunks, u32x4* __restrict__ out) {
-  const int64_t row = blockIdx.x / chunks;
-  const int chunk = blockIdx.x - static_cast<int>(row) * chunks;
-  const u32x4* gu = gate_up + row * 2 * vecs;
-  u32x4* o = out + row * vecs;
-  const int base = chunk * kThreads * NV + threadIdx.x;
-  u32x4 a[NV], b[NV];
+// Interleaved layout (gate_i, up_i): output vector g (8 outputs) reads input
+// vectors 2g and 2g + 1.  Needs inter % 8 == 0.
+template <int BS, bool NT>
+__global__ __launch_bounds__(BS) void silu_and_mul_interleaved_kernel(
+    const u32x4* __restrict__ gate_up, uint32_t total, u32x4* __restrict__ out) {
+  const uint32_t g = blockIdx.x * BS + threadIdx.x;
+  if (g >= total) return;
+  const f32x8 lo = unpack8(ld16<NT>(gate_up + 2 * static_cast<uint64_t>(g)));
+  const f32x8 hi = unpack8(ld16<NT>(gate_up + 2 * static_cast<uint64_t>(g) + 1));
+  f32x8 y;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = base + k * kThreads;
-    if (i < vecs) {
-      a[k] = gu[2 * i];
-      b[k] = gu[2 * i + 1];
-    }
+  for (int j = 0; j < 4; ++j) {
+    y[j] = silu_f16(lo[2 * j]) * lo[2 * j + 1];
+    y[4 + j] = silu_f16(hi[2 * j]) * hi[2 * j + 1];
   }
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = base + k * kThreads;
-    if (i < vecs) {
-      const f32x8 lo = unpack8(a[k]), hi = unpack8(b[k]);
-      f32x8 y;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        y[j] = silu_f16(lo[2 * j]) * lo[2 * j + 1];
-        y[4 + j] = silu_f16(hi[2 * j]) * hi[2 * j + 1];
-      }
-      o[i] = pack8(y);
-    }
-  }
+  st16<NT>(out + g, pack8(y));
 }
 
 // Any inter: one output per lane from a 4-byte (gate, up) pair.
-__global__ __launch_bounds__(kThreads) void silu_and_mul_interleaved_scalar_kernel(
+__global__ __launch_bounds__(256) void silu_and_mul_interleaved_scalar_kernel(
     const f16x2* __restrict__ gate_up, int64_t total, _Float16* __restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
-  const f16x2 p = gate_up[i];  // row-major [rows, inter] pairs: same flat index
+  const f16x2 p = gate_up[i];  // pairs are row-major [rows, inter]: same flat index
   out[i] = static_cast<_Float16>(silu_f16(static_cast<float>(p[0])) * static_cast<float>(p[1]));
 }
 
-__global__ __launch_bounds__(kThreads) void resolve_input_ids_kernel(
+template <int BS, bool NT>
+void launch_swiglu_bs(bool interleaved, uint64_t blocks, const u32x4* gu, uint32_t vecs,
+                      uint32_t total, u32x4* o, hipStream_t stream) {
+  if (interleaved) {
+    silu_and_mul_interleaved_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, total, o);
+  } else {
+    silu_and_mul_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, vecs, total, o);
+  }
+}
+
+void launch_swiglu(bool interleaved, const u32x4* gu, uint32_t vecs, uint32_t total, u32x4* o,
+                   hipStream_t stream) {
+  const FlatPolicy p = pick_flat(64, "RLK_TUNE_SWIGLU_BS", "RLK_TUNE_SWIGLU_NT");
+  const uint64_t blocks = (total + p.bs - 1) / p.bs;
+#define RLK_SWIGLU_BS(B)                                                               \
+  p.nt ? launch_swiglu_bs<B, true>(interleaved, blocks, gu, vecs, total, o, stream)    \
+       : launch_swiglu_bs<B, false>(interleaved, blocks, gu, vecs, total, o, stream)
+  switch (p.bs) {
+    case 128: RLK_SWIGLU_BS(128); break;
+    case 256: RLK_SWIGLU_BS(256); break;
+    default: RLK_SWIGLU_BS(64); break;
+  }
+#undef RLK_SWIGLU_BS
+}
+
+__global__ __launch_bounds__(256) void resolve_input_ids_kernel(
     int32_t* __restrict__ ids, const int32_t* __restrict__ src,
     const int32_t* __restrict__ prev_sampled, int n) {
-  const int i = blockIdx.x * kThreads + threadIdx.x;
+  const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) {
     const int s = src[i];
     if (s >= 0) ids[i] = prev_sampled[s];
@@ -342,37 +359,29 @@ extern "C" int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta,
   if (hidden <= 0 || hidden % 8 != 0)
     return fail(RLK_EINVAL, "fused_add_rmsnorm: hidden size must be a multiple of 8 (got %d)",
                 hidden);
-  const int vecs = hidden / 8;
-  auto* res = reinterpret_cast<u32x4*>(residual);
-  const auto* del = reinterpret_cast<const u32x4*>(delta);
-  const auto* w = reinterpret_cast<const u32x4*>(weight);
-  auto* o = reinterpret_cast<u32x4*>(out);
-  const float hidden_f = static_cast<float>(hidden);
-  // Lanes per row: one wave64 per row once there are enough rows to fill the
-  // chip; a whole 256-lane block per row for small (decode) batches so that a
-  // row's loads spread over four SIMDs.
-  int tpr = rows >= 2048 ? 64 : 256;
+  NormArgs a;
+  a.res = reinterpret_cast<u32x4*>(residual);
+  a.del = reinterpret_cast<const u32x4*>(delta);
+  a.w = reinterpret_cast<const u32x4*>(weight);
+  a.rows = rows;
+  a.vecs = hidden / 8;
+  a.hidden = static_cast<float>(hidden);
+  a.eps = eps;
+  a.out = reinterpret_cast<u32x4*>(out);
+  // Lanes per row: enough for one 16-byte vector per lane up to 512 lanes
+  // (eight waves); wider rows keep several vectors per lane in registers.
+  // Non-temporal accesses measured faster at every batch size.
+  int tpr = 64;
+  while (tpr < 512 && tpr < a.vecs) tpr *= 2;
   tpr = tune_knob("RLK_TUNE_NORM_TPR", tpr);
-  bool launched = false;
-  int nv = round_up_nv((vecs + tpr - 1) / tpr);
-  if (nv > 0) {
-    switch (tpr) {
-      case 64: launched = launch_norm_t<64>(nv, res, del, w, rows, vecs, hidden_f, eps, o, stream); break;
-      case 128: launched = launch_norm_t<128>(nv, res, del, w, rows, vecs, hidden_f, eps, o, stream); break;
-      default: launched = launch_norm_t<256>(nv, res, del, w, rows, vecs, hidden_f, eps, o, stream); break;
-    }
-  }
+  const bool nt = tune_knob("RLK_TUNE_NORM_NT", 1) != 0;
+  bool launched = nt ? launch_norm_nt<true>(tpr, a, stream) : launch_norm_nt<false>(tpr, a, stream);
+  if (!launched) launched = launch_norm_nt<false>(512, a, stream);
   if (!launched) {
-    nv = round_up_nv((vecs + kThreads - 1) / kThreads);
-    if (nv > 0) {
-      launched = launch_norm_t<256>(nv, res, del, w, rows, vecs, hidden_f, eps, o, stream);
-    }
-  }
-  if (!launched) {
-    if (del != nullptr) {
-      add_rmsnorm_wide_kernel<true><<<rows, kThreads, 0, stream>>>(res, del, w, vecs, hidden_f, eps, o);
+    if (a.del != nullptr) {
+      add_rmsnorm_wide_kernel<true><<<rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, eps, a.out);
     } else {
-      add_rmsnorm_wide_kernel<false><<<rows, kThreads, 0, stream>>>(res, del, w, vecs, hidden_f, eps, o);
+      add_rmsnorm_wide_kernel<false><<<rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, eps, a.out);
     }
   }
   return launch_status("fused_add_rmsnorm");
@@ -384,18 +393,12 @@ extern "C" int rlk_silu_and_mul(const uint16_t* gate_up, int rows, int inter, ui
   if (inter <= 0 || inter % 8 != 0)
     return fail(RLK_EINVAL, "silu_and_mul: intermediate size must be a multiple of 8 (got %d)",
                 inter);
-  const int vecs = inter / 8;
-  const int nv = tune_knob("RLK_TUNE_SWIGLU_NV", pick_nv(rows, vecs, 2048));
-  const int chunks = (vecs + kThreads * nv - 1) / (kThreads * nv);
-  const int64_t blocks = static_cast<int64_t>(rows) * chunks;
-  if (blocks > 0x7fffffff) return fail(RLK_EINVAL, "silu_and_mul: too many rows (%d)", rows);
-  const auto* gu = reinterpret_cast<const u32x4*>(gate_up);
-  auto* o = reinterpret_cast<u32x4*>(out);
-  switch (nv) {
-    case 1: silu_and_mul_kernel<1><<<blocks, kThreads, 0, stream>>>(gu, vecs, chunks, o); break;
-    case 2: silu_and_mul_kernel<2><<<blocks, kThreads, 0, stream>>>(gu, vecs, chunks, o); break;
-    default: silu_and_mul_kernel<4><<<blocks, kThreads, 0, stream>>>(gu, vecs, chunks, o); break;
-  }
+  const uint32_t vecs = inter / 8;
+  const uint64_t total = static_cast<uint64_t>(rows) * vecs;
+  if (total > 0x7fffffffull)
+    return fail(RLK_EINVAL, "silu_and_mul: %d rows exceed one launch; split the call", rows);
+  launch_swiglu(false, reinterpret_cast<const u32x4*>(gate_up), vecs,
+                static_cast<uint32_t>(total), reinterpret_cast<u32x4*>(out), stream);
   return launch_status("silu_and_mul");
 }
 
@@ -403,25 +406,18 @@ extern "C" int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, i
                                             uint16_t* out, hipStream_t stream) {
   if (rows <= 0) return RLK_OK;
   if (inter <= 0) return fail(RLK_EINVAL, "silu_and_mul_interleaved: bad intermediate size %d", inter);
+  const uint64_t pairs = static_cast<uint64_t>(rows) * inter;
+  if (pairs > 0x7fffffffull)
+    return fail(RLK_EINVAL, "silu_and_mul_interleaved: %d rows exceed one launch; split the call",
+                rows);
   if (inter % 8 == 0) {
-    const int vecs = inter / 8;
-    const int nv = tune_knob("RLK_TUNE_SWIGLU_NV", pick_nv(rows, vecs, 2048));
-    const int chunks = (vecs + kThreads * nv - 1) / (kThreads * nv);
-    const int64_t blocks = static_cast<int64_t>(rows) * chunks;
-    if (blocks > 0x7fffffff) return fail(RLK_EINVAL, "silu_and_mul_interleaved: too many rows");
-    const auto* gu = reinterpret_cast<const u32x4*>(gate_up);
-    auto* o = reinterpret_cast<u32x4*>(out);
-    switch (nv) {
-      case 1: silu_and_mul_interleaved_kernel<1><<<blocks, kThreads, 0, stream>>>(gu, vecs, chunks, o); break;
-      case 2: silu_and_mul_interleaved_kernel<2><<<blocks, kThreads, 0, stream>>>(gu, vecs, chunks, o); break;
-      default: silu_and_mul_interleaved_kernel<4><<<blocks, kThreads, 0, stream>>>(gu, vecs, chunks, o); break;
-    }
+    launch_swiglu(true, reinterpret_cast<const u32x4*>(gate_up), inter / 8,
+                  static_cast<uint32_t>(pairs / 8), reinterpret_cast<u32x4*>(out), stream);
   } else {
-    const int64_t total = static_cast<int64_t>(rows) * inter;
-    const int64_t blocks = (total + kThreads - 1) / kThreads;
-    if (blocks > 0x7fffffff) return fail(RLK_EINVAL, "silu_and_mul_interleaved: too many rows");
-    silu_and_mul_interleaved_scalar_kernel<<<blocks, kThreads, 0, stream>>>(
-        reinterpret_cast<const f16x2*>(gate_up), total, reinterpret_cast<_Float16*>(out));
+    const uint64_t blocks = (pairs + 255) / 256;
+    silu_and_mul_interleaved_scalar_kernel<<<blocks, 256, 0, stream>>>(
+        reinterpret_cast<const f16x2*>(gate_up), static_cast<int64_t>(pairs),
+        reinterpret_cast<_Float16*>(out));
   }
   return launch_status("silu_and_mul_interleaved");
 }
@@ -429,7 +425,6 @@ extern "C" int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, i
 extern "C" int rlk_resolve_input_ids(int32_t* input_ids, const int32_t* src,
                                      const int32_t* prev_sampled, int n, hipStream_t stream) {
   if (n <= 0) return RLK_OK;
-  resolve_input_ids_kernel<<<(n + kThreads - 1) / kThreads, kThreads, 0, stream>>>(
-      input_ids, src, prev_sampled, n);
+  resolve_input_ids_kernel<<<(n + 255) / 256, 256, 0, stream>>>(input_ids, src, prev_sampled, n);
   return launch_status("resolve_input_ids");
 }

@@ -31,8 +31,6 @@
 namespace rlk {
 namespace {
 
-constexpr int kThreads = 256;
-
 struct RopeArgs {
   _Float16* qkv;
   const int32_t* positions;
@@ -49,18 +47,16 @@ struct RopeArgs {
   int block_size;
 };
 
-template <int D, bool kInt8, int WPT>
-__global__ __launch_bounds__(kThreads) void rope_kv_kernel(RopeArgs a) {
+template <int D, bool kInt8, int WPT, bool NT>
+__global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int kHalf = D / 2;
   constexpr int kLPH = kHalf / 8;            // lanes per head
   constexpr int kHeadsPerWave = kWave / kLPH;
-  constexpr int kTokPerBlock = kThreads / (kWave * WPT);
   constexpr int kGroups = kHeadsPerWave * WPT;  // heads of one token in flight
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTokPerBlock + wave / WPT;
-  if (t >= a.num_tokens) return;  // uniform per wave
-  const int hg = (wave % WPT) * kHeadsPerWave + lane / kLPH;
+  const int64_t t = blockIdx.x;  // one token per workgroup of WPT waves
+  const int hg = wave * kHeadsPerWave + lane / kLPH;
   const int p0 = (lane % kLPH) * 8;  // first pair index owned by this lane
   const int heads = a.hq + 2 * a.hkv;
   const int pos = a.positions[t];
@@ -81,8 +77,8 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(RopeArgs a) {
   }
   for (int h = hg; h < heads; h += kGroups) {  // all lanes of a head share h
     _Float16* hp = row + h * D;
-    f32x8 x0 = unpack8(load16(hp + p0));
-    f32x8 x1 = unpack8(load16(hp + kHalf + p0));
+    f32x8 x0 = unpack8(ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0)));
+    f32x8 x1 = unpack8(ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0)));
     if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
       const f32x8 y0 = x0 * c - x1 * s;
       const f32x8 y1 = x1 * c + x0 * s;
@@ -90,8 +86,8 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(RopeArgs a) {
       x1 = round_f16(y1);
     }
     if (h < a.hq) {  // query: back in place
-      store16(hp + p0, pack8(x0));
-      store16(hp + kHalf + p0, pack8(x1));
+      st16<NT>(reinterpret_cast<u32x4*>(hp + p0), pack8(x0));
+      st16<NT>(reinterpret_cast<u32x4*>(hp + kHalf + p0), pack8(x1));
       continue;
     }
     if (slot < 0) continue;
@@ -100,8 +96,8 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(RopeArgs a) {
     const int64_t cell = (static_cast<int64_t>(blk) * a.hkv + kvh) * a.block_size + off;
     if constexpr (!kInt8) {
       _Float16* dst = static_cast<_Float16*>(is_v ? a.v : a.k) + cell * D;
-      store16(dst + p0, pack8(x0));
-      store16(dst + kHalf + p0, pack8(x1));
+      st16<NT>(reinterpret_cast<u32x4*>(dst + p0), pack8(x0));
+      st16<NT>(reinterpret_cast<u32x4*>(dst + kHalf + p0), pack8(x1));
     } else {
       float amax = 0.f;
 #pragma unroll
@@ -116,21 +112,33 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(RopeArgs a) {
         q1[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x1[j] * inv, -127.f), 127.f)));
       }
       int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
-      *reinterpret_cast<u32x2*>(dst + p0) = __builtin_bit_cast(u32x2, q0);
-      *reinterpret_cast<u32x2*>(dst + kHalf + p0) = __builtin_bit_cast(u32x2, q1);
+      st8<NT>(reinterpret_cast<u32x2*>(dst + p0), __builtin_bit_cast(u32x2, q0));
+      st8<NT>(reinterpret_cast<u32x2*>(dst + kHalf + p0), __builtin_bit_cast(u32x2, q1));
       if (p0 == 0) (is_v ? a.v_scale : a.k_scale)[cell] = scale;
     }
   }
 }
 
-template <int D, bool kInt8>
+template <int D, bool kInt8, bool NT>
 void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
-  const int tok_per_block = kThreads / (kWave * wpt);
-  const int blocks = (a.num_tokens + tok_per_block - 1) / tok_per_block;
   switch (wpt) {
-    case 1: rope_kv_kernel<D, kInt8, 1><<<blocks, kThreads, 0, stream>>>(a); break;
-    case 2: rope_kv_kernel<D, kInt8, 2><<<blocks, kThreads, 0, stream>>>(a); break;
-    default: rope_kv_kernel<D, kInt8, 4><<<blocks, kThreads, 0, stream>>>(a); break;
+    case 1: rope_kv_kernel<D, kInt8, 1, NT><<<a.num_tokens, kWave, 0, stream>>>(a); break;
+    case 2: rope_kv_kernel<D, kInt8, 2, NT><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
+    case 3: rope_kv_kernel<D, kInt8, 3, NT><<<a.num_tokens, 3 * kWave, 0, stream>>>(a); break;
+    case 4: rope_kv_kernel<D, kInt8, 4, NT><<<a.num_tokens, 4 * kWave, 0, stream>>>(a); break;
+    case 5: rope_kv_kernel<D, kInt8, 5, NT><<<a.num_tokens, 5 * kWave, 0, stream>>>(a); break;
+    case 6: rope_kv_kernel<D, kInt8, 6, NT><<<a.num_tokens, 6 * kWave, 0, stream>>>(a); break;
+    case 7: rope_kv_kernel<D, kInt8, 7, NT><<<a.num_tokens, 7 * kWave, 0, stream>>>(a); break;
+    default: rope_kv_kernel<D, kInt8, 8, NT><<<a.num_tokens, 8 * kWave, 0, stream>>>(a); break;
+  }
+}
+
+template <int D>
+void launch_dt(const RopeArgs& a, bool int8, bool nt, int wpt, hipStream_t stream) {
+  if (int8) {
+    nt ? launch_d<D, true, true>(a, wpt, stream) : launch_d<D, true, false>(a, wpt, stream);
+  } else {
+    nt ? launch_d<D, false, true>(a, wpt, stream) : launch_d<D, false, false>(a, wpt, stream);
   }
 }
 
@@ -166,15 +174,21 @@ extern "C" int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions,
   a.hq = num_heads;
   a.hkv = kv->num_kv_heads;
   a.block_size = kv->block_size;
-  // Waves per token: several for decode-sized batches (more heads in flight
-  // per token, more CUs busy), one once the batch alone fills the chip.
-  int wpt = num_tokens >= 2048 ? 1 : (num_tokens >= 512 ? 2 : 4);
-  wpt = tune_knob("RLK_TUNE_ROPE_WPT", wpt);
+  // One token per workgroup of `wpt` waves; a wave covers 64 / (D / 16)
+  // heads of the token at once, so wpt = ceil(heads / heads_per_wave) (at most
+  // 8) handles every head of the token in one pass: 6 waves for Llama-3.1-8B
+  // (48 heads of 128), 5 for Qwen2-7B (36 heads).  Non-temporal accesses
+  // measured faster at every batch size.
   const bool int8 = kv->dtype == RLK_KV_INT8;
+  const int heads = num_heads + 2 * kv->num_kv_heads;
+  const int heads_per_wave = kWave / (kv->head_dim / 16);
+  int wpt = (heads + heads_per_wave - 1) / heads_per_wave;
+  wpt = tune_knob("RLK_TUNE_ROPE_WPT", wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
+  const bool nt = tune_knob("RLK_TUNE_ROPE_NT", 1) != 0;
   if (kv->head_dim == 128) {
-    int8 ? launch_d<128, true>(a, wpt, stream) : launch_d<128, false>(a, wpt, stream);
+    launch_dt<128>(a, int8, nt, wpt, stream);
   } else {
-    int8 ? launch_d<64, true>(a, wpt, stream) : launch_d<64, false>(a, wpt, stream);
+    launch_dt<64>(a, int8, nt, wpt, stream);
   }
   return launch_status("rope_and_write_kv");
 }

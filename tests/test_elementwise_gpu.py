@@ -128,7 +128,7 @@ def test_rmsnorm_reference_case(torch_cuda):
 
 
 @pytest.mark.parametrize("rows,hidden", [(32, 4096), (1, 2048), (7, 8), (3, 520), (2049, 4096),
-                                         (33, 3584), (300, 8192), (5, 16384), (2, 40960),
+                                         (33, 3584), (300, 8192), (5, 16384), (2, 40960), (1, 73728),
                                          (4100, 64), (2050, 3584)])
 @pytest.mark.parametrize("delta", [True, False])
 def test_rmsnorm_shapes(torch_cuda, rows, hidden, delta):
