@@ -129,6 +129,17 @@ def copy_baseline(torch, nbytes=1 << 30, reps=20):
     return round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
 
 
+def launch_floor_us(torch, K, calls=1000):
+    """Per-launch time of a one-workgroup kernel (resolve_input_ids on one
+    id) replayed back to back in a graph: the dispatch floor every call pays."""
+    ids = torch.zeros(1, dtype=torch.int32, device="cuda")
+    src = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    g = capture(torch, lambda: [K.resolve_input_ids(ids, src, ids, 1) for _ in range(calls)])
+    ms = time_graph(torch, g, 5) / calls
+    del g
+    return round(ms * 1e3, 3)
+
+
 def capture(torch, fn):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
@@ -267,18 +278,26 @@ def main():
 
     result = {}
     if args.only is None:
-        graphs = [capture(torch, lambda r=r: data.step(r)) for r in range(data.R)]
-        for i in range(args.warmup):
-            graphs[i % data.R].replay()
+        # K steps = (K // R) replays of a graph holding all R rotating steps,
+        # plus one graph of the remaining K % R steps; warmup (W steps) likewise.
+        full = capture(torch, lambda: [data.step(r) for r in range(data.R)])
+        part = lambda n: capture(torch, lambda: [data.step(r) for r in range(n)]) if n else None  # noqa: E731
+        rem, wrem = part(args.steps % data.R), part(args.warmup % data.R)
+        for _ in range(args.warmup // data.R):
+            full.replay()
+        if wrem is not None:
+            wrem.replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        for i in range(args.steps):
-            graphs[i % data.R].replay()
+        for _ in range(args.steps // data.R):
+            full.replay()
+        if rem is not None:
+            rem.replay()
         end.record()
         torch.cuda.synchronize()
         ms_step = start.elapsed_time(end) / args.steps
-        del graphs
+        del full, rem, wrem
         value = step_bytes / (ms_step * 1e-3) / 1e9
         log(f"{w.key} step: {ms_step * 1e3:.2f} us, {value:.1f} GB/s")
         result.update(ms_per_step=round(ms_step, 5), value=round(value, 2))
@@ -308,7 +327,8 @@ def main():
             torch.cuda.empty_cache()
 
     copy = copy_baseline(torch)
-    log(f"device copy baseline: {copy} GB/s")
+    floor = launch_floor_us(torch, K)
+    log(f"device copy baseline: {copy} GB/s; one-workgroup launch floor {floor} us")
 
     cpu = None
     if not args.no_cpu:
@@ -334,6 +354,7 @@ def main():
         "kernels": kern,
         "prefill": extra,
         "copy_baseline_gb_per_s": copy,
+        "launch_floor_us": floor,
     }
     print(json.dumps(line))
 

@@ -110,13 +110,14 @@ __global__ __launch_bounds__(TPR) void add_rmsnorm_kernel(
   const int64_t row = blockIdx.x;
   u32x4* res = residual + row * vecs;
 
-  u32x4 rv[NV], dv[NV];
+  u32x4 rv[NV], dv[NV], wv[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = lt + k * TPR;
     const bool ok = i < vecs;
     rv[k] = ok ? ld16<NT>(res + i) : u32x4{0, 0, 0, 0};
     if constexpr (kDelta) dv[k] = ok ? ld16<NT>(delta + row * vecs + i) : u32x4{0, 0, 0, 0};
+    wv[k] = ok ? weight[i] : u32x4{0, 0, 0, 0};  // shared by all rows: cached load, issued early
   }
   f32x8 x[NV];
   float ss = 0.f;
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(TPR) void add_rmsnorm_kernel(
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = lt + k * TPR;
-    if (i < vecs) st16<NT>(o + i, pack8(round_f16(x[k] * inv) * unpack8(weight[i])));
+    if (i < vecs) st16<NT>(o + i, pack8(round_f16(x[k] * inv) * unpack8(wv[k])));
   }
 }
 

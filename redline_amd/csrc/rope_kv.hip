@@ -59,6 +59,15 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
   const int hg = wave * kHeadsPerWave + lane / kLPH;
   const int p0 = (lane % kLPH) * 8;  // first pair index owned by this lane
   const int heads = a.hq + 2 * a.hkv;
+  _Float16* row = a.qkv + t * heads * D;
+  // The activations do not depend on the metadata: issue their loads for the
+  // first head before the positions -> cos/sin and slot -> cell chain, so the
+  // two latencies overlap instead of adding up.
+  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+  if (hg < heads) {
+    v0 = ld16<NT>(reinterpret_cast<const u32x4*>(row + hg * D + p0));
+    v1 = ld16<NT>(reinterpret_cast<const u32x4*>(row + hg * D + kHalf + p0));
+  }
   const int pos = a.positions[t];
   const int slot = a.slots[t];
 
@@ -69,7 +78,6 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
   const f32x8 c = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const f32x8 s = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
 
-  _Float16* row = a.qkv + t * heads * D;
   int blk = 0, off = 0;
   if (slot >= 0) {
     blk = slot / a.block_size;
@@ -77,8 +85,12 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
   }
   for (int h = hg; h < heads; h += kGroups) {  // all lanes of a head share h
     _Float16* hp = row + h * D;
-    f32x8 x0 = unpack8(ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0)));
-    f32x8 x1 = unpack8(ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0)));
+    if (h != hg) {
+      v0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
+      v1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
+    }
+    f32x8 x0 = unpack8(v0);
+    f32x8 x1 = unpack8(v1);
     if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
       const f32x8 y0 = x0 * c - x1 * s;
       const f32x8 y1 = x1 * c + x0 * s;

@@ -1,0 +1,294 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something it does not share code or
+formula with: the reference's own outputs (golden vectors written by the
+compiled reference host core), the KATs of the reference's tests, closed forms
+and invariants, and float64 mathematics.  Rounding points are pinned by
+"tie-masked exactness": the float64 value of each fp16 rounding step is
+computed independently and, wherever it is not within a sliver of an fp16
+rounding tie (where fp32 evaluation order may legitimately decide), the oracle
+must agree bit for bit — so a dropped or extra rounding, a wrong sign, a
+swapped operand or a different rounding rule fails.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import randn_f16
+
+F16_ULP_TOL = 2e-3  # fraction of an fp16 ulp around a tie that is masked
+
+
+def f16_tie_distance(x):
+    """Distance (in fp16 ulps) of float64 values to the nearest fp16 rounding tie."""
+    x = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(x, 2.0 ** -14)))
+    ulp = 2.0 ** (e - 10)
+    q = x / ulp
+    return np.abs(q - np.floor(q) - 0.5)
+
+
+def safe(*xs):
+    m = np.ones(np.shape(xs[0]), bool)
+    for x in xs:
+        m &= f16_tie_distance(x) > F16_ULP_TOL
+    return m
+
+
+def to16(x64):
+    return np.asarray(x64, np.float64).astype(np.float16)
+
+
+# ------------------------------------------------------------------ fp16 bits
+
+def test_f2h_matches_reference_outputs(golden):
+    g = golden("half_f2h.npz")
+    got = oracle.f2h(g["x"])
+    assert np.array_equal(got, g["y"])
+
+
+def test_f2h_kats_and_numpy():
+    # tests/cpp/test_core.cpp:97-112
+    assert oracle.f2h(np.array([1.0, -2.0, 1e6, 1.0009765625, 1.00048828125], np.float32)).tolist() \
+        == [0x3C00, 0xC000, 0x7C00, 0x3C01, 0x3C00]
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(20000) * np.exp(rng.uniform(-20, 12, 20000))).astype(np.float32)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(oracle.f2h(x), x.astype(np.float16).view(np.uint16))
+
+
+def test_h2f_exhaustive():
+    h = oracle.lib().orc_h2f
+    allh = np.arange(65536, dtype=np.uint16)
+    want = allh.view(np.float16).astype(np.float32)
+    got = np.array([h(int(v)) for v in allh], np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+
+
+@pytest.mark.skipif(not oracle.has_ref(), reason="compiled reference core not present")
+def test_f2h_exhaustive_against_compiled_reference():
+    R = oracle.ref()
+    rng = np.random.default_rng(1)
+    x = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = x[~np.isnan(x)]
+    want = np.empty(x.size, np.uint16)
+    R.ref_float_to_half_many(oracle.p(x), x.size, oracle.p(want))
+    assert np.array_equal(oracle.f2h(x), want)
+
+
+# --------------------------------------------------------------- RoPE tables
+
+def test_rope_tables_match_reference(golden):
+    g = golden("rope_tables.npz")
+    pos = g["positions"]
+    for i, (theta, D, sc, f, lo, hi, old) in enumerate(g["cases"]):
+        c, s = oracle.rope_cos_sin_tables(theta, int(D), int(pos.max()) + 1, int(sc), f, lo, hi,
+                                          int(old))
+        assert np.array_equal(c[pos].view(np.uint32), g[f"cos_{i}"].view(np.uint32)), i
+        assert np.array_equal(s[pos].view(np.uint32), g[f"sin_{i}"].view(np.uint32)), i
+
+
+def test_rope_tables_closed_form():
+    c, s = oracle.rope_cos_sin_tables(1e4, 64, 100)
+    assert np.all(c[0] == 1) and np.all(s[0] == 0)
+    inv = 1.0 / 1e4 ** (np.arange(32) * 2 / 64)
+    ang = np.arange(100)[:, None] * inv[None, :]
+    assert np.max(np.abs(c - np.cos(ang))) < 2e-5  # fp32 angle at p <= 99
+    assert np.max(np.abs(s - np.sin(ang))) < 2e-5
+
+
+# ----------------------------------------------------------------- embedding
+
+def test_embedding_is_a_row_copy():
+    rng = np.random.default_rng(2)
+    table = rng.integers(-2048, 2048, (300, 64)).astype(np.float16)  # exact integers
+    ids = rng.integers(0, 300, 77).astype(np.int32)
+    assert np.array_equal(oracle.embedding_lookup(ids, table, 64), table[ids])
+    assert np.array_equal(oracle.gather_rows(table, ids, 64), table[ids])
+    prev = rng.integers(0, 1000, 8).astype(np.int32)
+    src = np.array([-1, 0, 7, -1, 3], np.int32)
+    ids5 = np.array([5, 6, 7, 8, 9], np.int32)
+    assert oracle.resolve_input_ids(ids5, src, prev).tolist() == [5, prev[0], prev[7], 8, prev[3]]
+
+
+# -------------------------------------------------------------- RMSNorm
+
+def test_rmsnorm_rounding_points_float64():
+    """out = fp16(fp16(r * inv) * w), r = fp16(res + delta), inv from the
+    float64 mean square (elementwise.cu:45,52,61; test_kernels.cu:26-39)."""
+    rng = np.random.default_rng(3)
+    rows, H = 64, 512
+    res, d = randn_f16(rng, (rows, H)), randn_f16(rng, (rows, H))
+    w = (1 + 0.2 * rng.standard_normal(H)).astype(np.float16)
+    new_res, out = oracle.fused_add_rmsnorm(res, d, w, 1e-5)
+    r64 = res.astype(np.float64) + d.astype(np.float64)
+    m = safe(r64)
+    assert np.array_equal(new_res[m], to16(r64)[m])
+    r = new_res.astype(np.float64)
+    inv = 1.0 / np.sqrt((r * r).mean(1, keepdims=True) + 1e-5)
+    t = r * inv
+    y = to16(t).astype(np.float64) * w.astype(np.float64)
+    m = safe(t, y)
+    assert m.mean() > 0.98
+    assert np.array_equal(out[m], to16(y)[m])
+    # dropping the intermediate rounding would change many results
+    assert np.mean(to16(t * w) != to16(y)) > 0.01
+
+
+def test_rmsnorm_null_delta_and_constant_rows():
+    rng = np.random.default_rng(4)
+    res = randn_f16(rng, (3, 256))
+    w = np.full(256, 2.0, np.float16)
+    r1, out1 = oracle.fused_add_rmsnorm(res, None, w, 1e-5)
+    assert np.array_equal(r1, res)  # residual untouched
+    z = np.zeros_like(res)
+    _, out0 = oracle.fused_add_rmsnorm(res, z, w, 1e-5)
+    assert np.array_equal(out1, out0)  # adding zero == no delta
+    c = np.repeat(np.array([[0.5], [-3.0], [100.0]], np.float16), 256, 1)
+    _, oc = oracle.fused_add_rmsnorm(c, None, w, 1e-5)
+    cf = np.array([0.5, -3.0, 100.0])
+    want = to16(to16(cf / np.sqrt(cf * cf + 1e-5)).astype(np.float64) * 2.0)
+    assert np.array_equal(oc, np.repeat(want[:, None], 256, 1))
+
+
+# ----------------------------------------------------------------- SwiGLU
+
+def test_swiglu_rounding_points_float64():
+    """out = fp16(fp16(silu(g)) * u) (elementwise.cu:66-82), silu from float64."""
+    rng = np.random.default_rng(5)
+    rows, I = 16, 1024
+    gu = randn_f16(rng, (rows, 2 * I), 2.0)
+    out = oracle.silu_and_mul(gu, I)
+    g, u = gu[:, :I].astype(np.float64), gu[:, I:].astype(np.float64)
+    s = g / (1 + np.exp(-g))
+    y = to16(s).astype(np.float64) * u
+    m = safe(s, y)
+    assert m.mean() > 0.98
+    assert np.array_equal(out[m], to16(y)[m])
+    # interleaved layout of the same numbers gives the same outputs
+    inter = np.empty_like(gu)
+    inter[:, 0::2], inter[:, 1::2] = gu[:, :I], gu[:, I:]
+    assert np.array_equal(oracle.silu_and_mul(inter, I, interleaved=True), out)
+
+
+def test_swiglu_special_values():
+    g = np.array([0, 30, -30, -100, 1, -1], np.float16)
+    u = np.array([3, 1, 1, 1, 2, 2], np.float16)
+    out = oracle.silu_and_mul(np.concatenate([g, u])[None], 6)[0].astype(np.float64)
+    assert out[0] == 0 and out[1] == 30 and abs(out[2]) < 1e-6 and out[3] == 0
+    assert out[4] == float(to16(to16(1 / (1 + np.exp(-1.0))) * 2.0))
+
+
+# ---------------------------------------------------------------- RoPE + KV
+
+def _rope(qkv, pos, slots, hq, hkv, D, nblocks, int8, theta=1e4, bs=16):
+    cos, sin = oracle.rope_cos_sin_tables(theta, D, int(pos.max()) + 1)
+    kc = np.zeros((nblocks, hkv, bs, D), np.int8 if int8 else np.float16)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((nblocks, hkv, bs), np.float32) if int8 else None
+    vs = np.zeros_like(ks) if int8 else None
+    out = qkv.copy()
+    oracle.rope_and_write_kv(out, pos, slots, hq, hkv, D, cos, sin, kc, vc, ks, vs, bs, int8)
+    return out, kc, vc, ks, vs, cos, sin
+
+
+def _rotate64(x, pos, cos, sin):
+    """float64 rotate-half on [..., D] with the fp32 table values."""
+    h = x.shape[-1] // 2
+    c, s = cos[pos].astype(np.float64), sin[pos].astype(np.float64)
+    x0, x1 = x[..., :h], x[..., h:]
+    return np.concatenate([x0 * c - x1 * s, x1 * c + x0 * s], -1)
+
+
+def test_rope_fp16_against_float64_rotation():
+    rng = np.random.default_rng(6)
+    T, hq, hkv, D = 40, 4, 2, 128
+    qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
+    pos = rng.integers(0, 500, T).astype(np.int32)
+    slots = rng.permutation(np.arange(16, 16 * 8)).astype(np.int32)[:T]
+    out, kc, vc, _, _, cos, sin = _rope(qkv, pos, slots, hq, hkv, D, 8, False)
+    heads = qkv.reshape(T, -1, D).astype(np.float64)
+    rot = np.stack([_rotate64(heads[t], pos[t], cos, sin) for t in range(T)])
+    o = out.reshape(T, -1, D)
+    m = safe(rot[:, :hq])
+    assert np.array_equal(o[:, :hq][m], to16(rot[:, :hq])[m])          # q roped in place
+    assert np.array_equal(o[:, hq:], qkv.reshape(T, -1, D)[:, hq:])    # k, v sections untouched
+    blk, off = slots // 16, slots % 16
+    for t in range(T):
+        for h in range(hkv):
+            kk = kc[blk[t], h, off[t]]
+            m = safe(rot[t, hq + h])
+            assert np.array_equal(kk[m], to16(rot[t, hq + h])[m])
+            assert np.array_equal(vc[blk[t], h, off[t]], heads[t, hq + hkv + h].astype(np.float16))
+    # untouched cells stay zero
+    written = np.zeros((8, 16), bool)
+    written[blk, off] = True
+    assert not np.any(kc.transpose(0, 2, 1, 3)[~written])
+
+
+def test_rope_slot_kats_and_skip():
+    # tests/cpp/test_core.cpp:365-367: slots 13*4+1, 20*4+3, 22*4+0 at block size 4
+    rng = np.random.default_rng(7)
+    hq, hkv, D = 2, 1, 64
+    qkv = randn_f16(rng, (4, (hq + 2 * hkv) * D))
+    pos = np.array([9, 3, 8, 0], np.int32)
+    slots = np.array([13 * 4 + 1, 20 * 4 + 3, 22 * 4 + 0, -1], np.int32)
+    out, kc, vc, _, _, _, _ = _rope(qkv, pos, slots, hq, hkv, D, 24, False, bs=4)
+    for t, (b, o) in enumerate([(13, 1), (20, 3), (22, 0)]):
+        assert np.array_equal(vc[b, 0, o], qkv[t, (hq + hkv) * D:].astype(np.float16))
+    nz = {(b, o) for b, o in zip(*np.nonzero(np.any(vc[:, 0] != 0, -1)))}
+    assert nz == {(13, 1), (20, 3), (22, 0)}  # slot -1 wrote nothing
+    # position 0 is the identity rotation
+    assert np.array_equal(out[3], qkv[3])
+
+
+def test_rope_int8_codes_and_scales():
+    """INT8 (rope_kv.cu:71-85): scale = amax/127 over the fp16-rounded head,
+    codes = round-half-even(x / scale) clamped to +/-127; checked against
+    float64 wherever x/scale is not within a sliver of a .5 tie; the
+    reference test bound |code * scale - x| <= 0.51 scale; amax 0 -> scale 1."""
+    rng = np.random.default_rng(8)
+    T, hq, hkv, D = 64, 2, 2, 128
+    qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
+    qkv.reshape(T, -1, D)[:, hq:, 5] *= 8  # per-head outlier channel
+    qkv.reshape(T, -1, D)[3, hq + 1] = 0   # an all-zero k head
+    pos = rng.integers(0, 300, T).astype(np.int32)
+    slots = (np.arange(T) + 16).astype(np.int32)
+    out16, kc16, vc16, _, _, _, _ = _rope(qkv, pos, slots, hq, hkv, D, 6, False)
+    out8, kc8, vc8, ks, vs, _, _ = _rope(qkv, pos, slots, hq, hkv, D, 6, True)
+    assert np.array_equal(out16, out8)
+    blk, off = slots // 16, slots % 16
+    for cache16, cache8, scales in ((kc16, kc8, ks), (vc16, vc8, vs)):
+        x = cache16[blk, :, off].astype(np.float64)            # [T, hkv, D] fp16 values
+        q = cache8[blk, :, off].astype(np.float64)
+        sc = scales[blk, :, off].astype(np.float64)[..., None]
+        amax = np.abs(x).max(-1, keepdims=True)
+        want_sc = np.where(amax > 0, (amax.astype(np.float32) / np.float32(127)), 1.0)
+        assert np.array_equal(sc, want_sc)
+        assert np.all(np.abs(q * sc - x) <= 0.51 * sc)
+        r = x / sc
+        far = np.abs(np.abs(r - np.floor(r)) - 0.5) > 1e-4
+        assert np.array_equal(q[far], np.clip(np.rint(r[far]), -127, 127))
+        assert np.all(np.abs(q).max(-1)[amax[..., 0] > 0] == 127)
+    assert ks[blk[3], 1, off[3]] == 1.0 and not np.any(kc8[blk[3], 1, off[3]])
+
+
+def test_rope_int8_ties_round_half_even():
+    """A V head (no rotation) with amax = 127/64 has scale exactly 2^-6, so
+    values (n + 0.5)/64 sit exactly on ties: __float2int_rn rounds them to
+    even (rope_kv.cu:80,82)."""
+    hq, hkv, D = 1, 1, 128
+    n = np.arange(D) % 126
+    v = ((n + 0.5) / 64).astype(np.float16)
+    v[0] = np.float16(127 / 64)
+    v[1::2] *= -1
+    qkv = np.zeros((1, (hq + 2 * hkv) * D), np.float16)
+    qkv[0, (hq + hkv) * D:] = v
+    _, _, vc, _, vs, _, _ = _rope(qkv, np.array([0], np.int32), np.array([16], np.int32),
+                                  hq, hkv, D, 2, True)
+    assert vs[1, 0, 0] == np.float32(2.0 ** -6)
+    want = np.rint(v.astype(np.float64) * 64)  # numpy rint: half to even
+    assert np.array_equal(vc[1, 0, 0].astype(np.float64), want)
+    assert np.any(np.abs(v.astype(np.float64) * 64 % 1) == 0.5)

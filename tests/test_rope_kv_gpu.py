@@ -248,3 +248,20 @@ def test_rope_other_block_sizes(torch_cuda, bs):
     slots = rng.permutation(np.arange(bs, 40 * bs)).astype(np.int32)[:T]
     run_case(torch, qkv, pos, slots, hq, hkv, D, 40, True, bs=bs, max_pos=512)
     run_case(torch, qkv, pos, slots, hq, hkv, D, 40, False, bs=bs, max_pos=512)
+
+
+def test_rope_int8_exact_ties(torch_cuda):
+    """Values exactly on .5 code ties (scale 2^-6) round half to even, as the
+    oracle (pinned against numpy's rint) does."""
+    say("rope int8 exact ties")
+    hq, hkv, D = 1, 1, 128
+    n = np.arange(D) % 126
+    v = ((n + 0.5) / 64).astype(np.float16)
+    v[0] = np.float16(127 / 64)
+    v[1::2] *= -1
+    qkv = np.zeros((1, (hq + 2 * hkv) * D), np.float16)
+    qkv[0, (hq + hkv) * D:] = v
+    cache, _, _ = run_case(torch_cuda, qkv, np.array([0], np.int32), np.array([16], np.int32),
+                           hq, hkv, D, 2, True)
+    _, vq, _, vs = cache.tensors(0)
+    assert np.array_equal(vq[1, 0, 0].cpu().numpy().astype(np.float64), np.rint(v.astype(np.float64) * 64))
