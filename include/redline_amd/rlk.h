@@ -46,7 +46,7 @@ extern "C" {
 typedef struct rlk_kv_layer_view {
   void* k;
   void* v;
-  float* k_scale;
+  float* k_scale; /* fp16 cells instead with RLK_SCALE_F16 (rlk_rope_and_write_kv_ex) */
   float* v_scale;
   int block_size;
   int num_kv_heads;
@@ -112,6 +112,34 @@ int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_t
                           int num_tokens, int num_heads, const float* cos_table,
                           const float* sin_table, const rlk_kv_layer_view* kv,
                           hipStream_t stream);
+
+/* Extension with no counterpart in the reference interface: options of
+ * rlk_rope_and_write_kv_ex.
+ *   qkv_bias     fp16 [(Hq + 2*Hkv) * D] added to every head before the
+ *                rotation (x = fp16(x + b)), the Qwen2 attention bias that the
+ *                reference adds in its QKV GEMM epilogue
+ *                (src/cuda/gemm/linear.cpp:108); NULL = no bias.  The k and v
+ *                sections of qkv are left as they were (only the cache sees the
+ *                biased k/v); the q section receives bias + RoPE.
+ *   scale_dtype  RLK_SCALE_F32: fp32 per-cell scales (the reference layout,
+ *                kv_cache.cpp:45-48).  RLK_SCALE_F16: scales stored as fp16 and
+ *                codes quantised against the stored (fp16-rounded) scale; the
+ *                k_scale / v_scale pointers then address uint16_t cells.
+ *                Codes may differ by 1 from the fp32-scale codes. */
+#define RLK_SCALE_F32 0
+#define RLK_SCALE_F16 1
+
+typedef struct rlk_rope_kv_options {
+  const uint16_t* qkv_bias;
+  int scale_dtype;
+} rlk_rope_kv_options;
+
+/* rlk_rope_and_write_kv with options (NULL options = the plain entry point). */
+int rlk_rope_and_write_kv_ex(uint16_t* qkv, const int32_t* positions,
+                             const int32_t* slot_mapping, int num_tokens, int num_heads,
+                             const float* cos_table, const float* sin_table,
+                             const rlk_kv_layer_view* kv, const rlk_rope_kv_options* options,
+                             hipStream_t stream);
 
 /* ------------------------------------------------------ host-side helpers */
 

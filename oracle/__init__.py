@@ -47,6 +47,8 @@ def lib() -> C.CDLL:
         L.orc_silu_and_mul_interleaved.argtypes = [_P, _I, _I, _P]
         L.orc_rope_and_write_kv.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P,
                                             _I, _I]
+        L.orc_rope_and_write_kv_ex.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
+                                               _P, _I, _I, _P, _I]
         L.orc_layer_step.argtypes = [_P, _P, _I, _I, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P,
                                      _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P]
         _o = L
@@ -152,8 +154,10 @@ def silu_and_mul(gate_up, inter, interleaved=False):
 
 
 def rope_and_write_kv(qkv, positions, slots, hq, hkv, d, cos_t, sin_t, k_cache, v_cache,
-                      k_scale=None, v_scale=None, block_size=16, int8=False):
-    """Updates qkv (fp16 [T, (hq+2hkv)*d]) and the caches in place."""
+                      k_scale=None, v_scale=None, block_size=16, int8=False, bias=None,
+                      scale16=False):
+    """Updates qkv (fp16 [T, (hq+2hkv)*d]) and the caches in place.  `bias`
+    (fp16 [(hq+2hkv)*d]) and `scale16` select the extension semantics."""
     q = _u16(qkv)
     assert q.flags.c_contiguous
     positions = np.ascontiguousarray(positions, np.int32)
@@ -161,7 +165,9 @@ def rope_and_write_kv(qkv, positions, slots, hq, hkv, d, cos_t, sin_t, k_cache, 
     T = positions.size
     kc = k_cache.view(np.uint16) if k_cache.dtype == np.float16 else k_cache
     vc = v_cache.view(np.uint16) if v_cache.dtype == np.float16 else v_cache
-    lib().orc_rope_and_write_kv(p(q), p(positions), p(slots), T, hq, hkv, d,
-                                p(np.ascontiguousarray(cos_t, np.float32)),
-                                p(np.ascontiguousarray(sin_t, np.float32)), p(kc), p(vc),
-                                p(k_scale), p(v_scale), block_size, int(int8))
+    b = None if bias is None else _u16(bias)
+    lib().orc_rope_and_write_kv_ex(p(q), p(positions), p(slots), T, hq, hkv, d,
+                                   p(np.ascontiguousarray(cos_t, np.float32)),
+                                   p(np.ascontiguousarray(sin_t, np.float32)), p(kc), p(vc),
+                                   p(k_scale), p(v_scale), block_size, int(int8), p(b),
+                                   int(scale16))

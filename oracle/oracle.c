@@ -24,6 +24,9 @@
  *   orc_silu_and_mul(_interl.) scipy expit-based float64 silu within fp16
  *                              rounding, special values (0, large +/-), layout
  *                              equivalence of split vs interleaved.
+ *   orc_rope_and_write_kv_ex   bias: equivalence with the plain function on
+ *                              fp16(qkv + bias); fp16 scale: scale == fp16(amax/127)
+ *                              and tie-masked float64 codes against the stored scale.
  *   orc_rope_and_write_kv      pos 0 identity, V passthrough, rotation by angle
  *                              against float64 rotation matrix, norm
  *                              preservation, slot/cell address KATs from
@@ -193,10 +196,11 @@ void orc_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, 
  *   INT8: amax over the head's fp16-rounded values, scale = amax > 0 ?
  *   amax / 127 : 1, inv = 1 / scale, code = rint(clamp(x * inv, -127, 127))
  *   (rope_kv.cu:71-85), scales fp32 per cell. */
-void orc_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_t* slots,
-                           int T, int Hq, int Hkv, int D, const float* cos_t, const float* sin_t,
-                           void* k_cache, void* v_cache, float* k_scale, float* v_scale, int bs,
-                           int int8) {
+void orc_rope_and_write_kv_ex(uint16_t* qkv, const int32_t* positions, const int32_t* slots,
+                              int T, int Hq, int Hkv, int D, const float* cos_t,
+                              const float* sin_t, void* k_cache, void* v_cache, void* k_scale,
+                              void* v_scale, int bs, int int8, const uint16_t* bias,
+                              int scale16) {
   const int half = D / 2, heads = Hq + 2 * Hkv;
   float x[256];
   for (int t = 0; t < T; ++t) {
@@ -205,6 +209,8 @@ void orc_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_
     for (int h = 0; h < heads; ++h) {
       uint16_t* v = row + (size_t)h * D;
       for (int i = 0; i < D; ++i) x[i] = orc_h2f(v[i]);
+      if (bias) /* extension: QKV bias added before the rotation, fp16-rounded */
+        for (int i = 0; i < D; ++i) x[i] = rnd16(x[i] + orc_h2f(bias[h * D + i]));
       if (h < Hq + Hkv) {
         for (int i = 0; i < half; ++i) {
           const float c = cos_t[(size_t)pos * half + i], s = sin_t[(size_t)pos * half + i];
@@ -230,14 +236,29 @@ void orc_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_
       } else {
         float amax = 0.0f;
         for (int i = 0; i < D; ++i) amax = fmaxf(amax, fabsf(x[i]));
-        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        /* extension: fp16-stored scale, codes quantised against the stored
+         * value (the reference's host quantiser convention,
+         * src/cpu/random_model.cpp:107-108) */
+        if (scale16) scale = rnd16(scale);
         const float inv = 1.0f / scale;
         int8_t* dst = (int8_t*)(is_v ? v_cache : k_cache) + cell * D;
         for (int i = 0; i < D; ++i) dst[i] = (int8_t)rintf(fminf(fmaxf(x[i] * inv, -127.0f), 127.0f));
-        (is_v ? v_scale : k_scale)[cell] = scale;
+        if (scale16)
+          ((uint16_t*)(is_v ? v_scale : k_scale))[cell] = orc_f2h(scale);
+        else
+          ((float*)(is_v ? v_scale : k_scale))[cell] = scale;
       }
     }
   }
+}
+
+void orc_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_t* slots, int T,
+                           int Hq, int Hkv, int D, const float* cos_t, const float* sin_t,
+                           void* k_cache, void* v_cache, float* k_scale, float* v_scale, int bs,
+                           int int8) {
+  orc_rope_and_write_kv_ex(qkv, positions, slots, T, Hq, Hkv, D, cos_t, sin_t, k_cache, v_cache,
+                           k_scale, v_scale, bs, int8, NULL, 0);
 }
 
 /* One layer's hot path on one batch, as a single call for CPU timing:

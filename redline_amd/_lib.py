@@ -42,6 +42,15 @@ class KVLayerView(C.Structure):
     ]
 
 
+RLK_SCALE_F32, RLK_SCALE_F16 = 0, 1
+
+
+class RopeKVOptions(C.Structure):
+    """Mirror of rlk_rope_kv_options (extension of rope_and_write_kv)."""
+
+    _fields_ = [("qkv_bias", C.c_void_p), ("scale_dtype", C.c_int)]
+
+
 class BatchShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in (
         "num_tokens", "num_seqs", "num_logit_rows", "num_decode_items",
@@ -70,6 +79,8 @@ _SIGNATURES = {
     "rlk_gather_rows": (_I, [_P, _P, _I, _I, _P, _P]),
     "rlk_resolve_input_ids": (_I, [_P, _P, _P, _I, _P]),
     "rlk_rope_and_write_kv": (_I, [_P, _P, _P, _I, _I, _P, _P, C.POINTER(KVLayerView), _P]),
+    "rlk_rope_and_write_kv_ex": (_I, [_P, _P, _P, _I, _I, _P, _P, C.POINTER(KVLayerView),
+                                      C.POINTER(RopeKVOptions), _P]),
     "rlk_float_to_half_bits": (C.c_uint16, [C.c_float]),
     "rlk_half_bits_to_float": (C.c_float, [C.c_uint16]),
     "rlk_rope_inv_freq": (_I, [C.c_double, _I, _I, C.c_double, C.c_double, C.c_double, _I, _P]),

@@ -39,17 +39,20 @@ struct RopeArgs {
   const float* sin_t;
   void* k;
   void* v;
-  float* k_scale;
-  float* v_scale;
+  void* k_scale;  // float[cells], or fp16[cells] when scale16
+  void* v_scale;
+  const _Float16* bias;  // [heads * D] added before the rotation, or null
+  int scale16;
   int num_tokens;
   int hq;
   int hkv;
   int block_size;
 };
 
-template <int D, bool kInt8, int WPT, bool NT>
+template <int D, bool kInt8, int WPT>
 __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
+  constexpr bool NT = true;  // streaming accesses: measured faster at every batch size
   constexpr int kHalf = D / 2;
   constexpr int kLPH = kHalf / 8;            // lanes per head
   constexpr int kHeadsPerWave = kWave / kLPH;
@@ -91,6 +94,10 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
     }
     f32x8 x0 = unpack8(v0);
     f32x8 x1 = unpack8(v1);
+    if (a.bias != nullptr) {  // extension: QKV bias, fp16-rounded sum
+      x0 = round_f16(x0 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + p0)));
+      x1 = round_f16(x1 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0)));
+    }
     if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
       const f32x8 y0 = x0 * c - x1 * s;
       const f32x8 y1 = x1 * c + x0 * s;
@@ -115,7 +122,8 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fmaxf(__builtin_fabsf(x0[j]), __builtin_fabsf(x1[j])));
       amax = group_max<kLPH>(amax);
-      const float scale = amax > 0.f ? amax / 127.f : 1.f;
+      float scale = amax > 0.f ? amax / 127.f : 1.f;
+      if (a.scale16) scale = round_f16(scale);  // extension: quantise against the stored fp16 scale
       const float inv = 1.f / scale;
       i8x8 q0, q1;
 #pragma unroll
@@ -126,32 +134,35 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
       int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
       st8<NT>(reinterpret_cast<u32x2*>(dst + p0), __builtin_bit_cast(u32x2, q0));
       st8<NT>(reinterpret_cast<u32x2*>(dst + kHalf + p0), __builtin_bit_cast(u32x2, q1));
-      if (p0 == 0) (is_v ? a.v_scale : a.k_scale)[cell] = scale;
+      if (p0 == 0) {
+        void* sp = is_v ? a.v_scale : a.k_scale;
+        if (a.scale16) {
+          static_cast<_Float16*>(sp)[cell] = static_cast<_Float16>(scale);
+        } else {
+          static_cast<float*>(sp)[cell] = scale;
+        }
+      }
     }
   }
 }
 
-template <int D, bool kInt8, bool NT>
+template <int D, bool kInt8>
 void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
   switch (wpt) {
-    case 1: rope_kv_kernel<D, kInt8, 1, NT><<<a.num_tokens, kWave, 0, stream>>>(a); break;
-    case 2: rope_kv_kernel<D, kInt8, 2, NT><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
-    case 3: rope_kv_kernel<D, kInt8, 3, NT><<<a.num_tokens, 3 * kWave, 0, stream>>>(a); break;
-    case 4: rope_kv_kernel<D, kInt8, 4, NT><<<a.num_tokens, 4 * kWave, 0, stream>>>(a); break;
-    case 5: rope_kv_kernel<D, kInt8, 5, NT><<<a.num_tokens, 5 * kWave, 0, stream>>>(a); break;
-    case 6: rope_kv_kernel<D, kInt8, 6, NT><<<a.num_tokens, 6 * kWave, 0, stream>>>(a); break;
-    case 7: rope_kv_kernel<D, kInt8, 7, NT><<<a.num_tokens, 7 * kWave, 0, stream>>>(a); break;
-    default: rope_kv_kernel<D, kInt8, 8, NT><<<a.num_tokens, 8 * kWave, 0, stream>>>(a); break;
+    case 1: rope_kv_kernel<D, kInt8, 1><<<a.num_tokens, kWave, 0, stream>>>(a); break;
+    case 2: rope_kv_kernel<D, kInt8, 2><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
+    case 3: rope_kv_kernel<D, kInt8, 3><<<a.num_tokens, 3 * kWave, 0, stream>>>(a); break;
+    case 4: rope_kv_kernel<D, kInt8, 4><<<a.num_tokens, 4 * kWave, 0, stream>>>(a); break;
+    case 5: rope_kv_kernel<D, kInt8, 5><<<a.num_tokens, 5 * kWave, 0, stream>>>(a); break;
+    case 6: rope_kv_kernel<D, kInt8, 6><<<a.num_tokens, 6 * kWave, 0, stream>>>(a); break;
+    case 7: rope_kv_kernel<D, kInt8, 7><<<a.num_tokens, 7 * kWave, 0, stream>>>(a); break;
+    default: rope_kv_kernel<D, kInt8, 8><<<a.num_tokens, 8 * kWave, 0, stream>>>(a); break;
   }
 }
 
 template <int D>
-void launch_dt(const RopeArgs& a, bool int8, bool nt, int wpt, hipStream_t stream) {
-  if (int8) {
-    nt ? launch_d<D, true, true>(a, wpt, stream) : launch_d<D, true, false>(a, wpt, stream);
-  } else {
-    nt ? launch_d<D, false, true>(a, wpt, stream) : launch_d<D, false, false>(a, wpt, stream);
-  }
+void launch_dt(const RopeArgs& a, bool int8, int wpt, hipStream_t stream) {
+  int8 ? launch_d<D, true>(a, wpt, stream) : launch_d<D, false>(a, wpt, stream);
 }
 
 }  // namespace
@@ -159,19 +170,21 @@ void launch_dt(const RopeArgs& a, bool int8, bool nt, int wpt, hipStream_t strea
 
 using namespace rlk;
 
-extern "C" int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions,
-                                     const int32_t* slot_mapping, int num_tokens, int num_heads,
-                                     const float* cos_table, const float* sin_table,
-                                     const rlk_kv_layer_view* kv, hipStream_t stream) {
+namespace {
+
+int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_mapping,
+                int num_tokens, int num_heads, const float* cos_table, const float* sin_table,
+                const rlk_kv_layer_view* kv, const uint16_t* bias, int scale16,
+                hipStream_t stream, const char* what) {
   if (num_tokens <= 0) return RLK_OK;
-  if (kv == nullptr) return fail(RLK_EINVAL, "rope_and_write_kv: null KV layer view");
+  if (kv == nullptr) return fail(RLK_EINVAL, "%s: null KV layer view", what);
   if (kv->head_dim != 64 && kv->head_dim != 128)
     return fail(RLK_EUNSUPPORTED, "unsupported head_dim %d (supported: 64, 128)", kv->head_dim);
   if (kv->dtype != RLK_KV_FP16 && kv->dtype != RLK_KV_INT8)
-    return fail(RLK_EINVAL, "rope_and_write_kv: unknown KV dtype %d", kv->dtype);
+    return fail(RLK_EINVAL, "%s: unknown KV dtype %d", what, kv->dtype);
   if (num_heads < 0 || kv->num_kv_heads < 0 || kv->block_size <= 0)
-    return fail(RLK_EINVAL, "rope_and_write_kv: bad head counts (%d, %d) or block size %d",
-                num_heads, kv->num_kv_heads, kv->block_size);
+    return fail(RLK_EINVAL, "%s: bad head counts (%d, %d) or block size %d", what, num_heads,
+                kv->num_kv_heads, kv->block_size);
   RopeArgs a;
   a.qkv = reinterpret_cast<_Float16*>(qkv);
   a.positions = positions;
@@ -182,6 +195,8 @@ extern "C" int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions,
   a.v = kv->v;
   a.k_scale = kv->k_scale;
   a.v_scale = kv->v_scale;
+  a.bias = reinterpret_cast<const _Float16*>(bias);
+  a.scale16 = scale16;
   a.num_tokens = num_tokens;
   a.hq = num_heads;
   a.hkv = kv->num_kv_heads;
@@ -189,18 +204,39 @@ extern "C" int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions,
   // One token per workgroup of `wpt` waves; a wave covers 64 / (D / 16)
   // heads of the token at once, so wpt = ceil(heads / heads_per_wave) (at most
   // 8) handles every head of the token in one pass: 6 waves for Llama-3.1-8B
-  // (48 heads of 128), 5 for Qwen2-7B (36 heads).  Non-temporal accesses
-  // measured faster at every batch size.
-  const bool int8 = kv->dtype == RLK_KV_INT8;
+  // (48 heads of 128), 5 for Qwen2-7B (36 heads).
   const int heads = num_heads + 2 * kv->num_kv_heads;
   const int heads_per_wave = kWave / (kv->head_dim / 16);
   int wpt = (heads + heads_per_wave - 1) / heads_per_wave;
   wpt = tune_knob("RLK_TUNE_ROPE_WPT", wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
-  const bool nt = tune_knob("RLK_TUNE_ROPE_NT", 1) != 0;
+  const bool int8 = kv->dtype == RLK_KV_INT8;
   if (kv->head_dim == 128) {
-    launch_dt<128>(a, int8, nt, wpt, stream);
+    launch_dt<128>(a, int8, wpt, stream);
   } else {
-    launch_dt<64>(a, int8, nt, wpt, stream);
+    launch_dt<64>(a, int8, wpt, stream);
   }
-  return launch_status("rope_and_write_kv");
+  return launch_status(what);
+}
+
+}  // namespace
+
+extern "C" int rlk_rope_and_write_kv(uint16_t* qkv, const int32_t* positions,
+                                     const int32_t* slot_mapping, int num_tokens, int num_heads,
+                                     const float* cos_table, const float* sin_table,
+                                     const rlk_kv_layer_view* kv, hipStream_t stream) {
+  return rope_launch(qkv, positions, slot_mapping, num_tokens, num_heads, cos_table, sin_table,
+                     kv, nullptr, 0, stream, "rope_and_write_kv");
+}
+
+extern "C" int rlk_rope_and_write_kv_ex(uint16_t* qkv, const int32_t* positions,
+                                        const int32_t* slot_mapping, int num_tokens,
+                                        int num_heads, const float* cos_table,
+                                        const float* sin_table, const rlk_kv_layer_view* kv,
+                                        const rlk_rope_kv_options* options, hipStream_t stream) {
+  const uint16_t* bias = options != nullptr ? options->qkv_bias : nullptr;
+  const int scale_dtype = options != nullptr ? options->scale_dtype : RLK_SCALE_F32;
+  if (scale_dtype != RLK_SCALE_F32 && scale_dtype != RLK_SCALE_F16)
+    return fail(RLK_EINVAL, "rope_and_write_kv_ex: unknown scale dtype %d", scale_dtype);
+  return rope_launch(qkv, positions, slot_mapping, num_tokens, num_heads, cos_table, sin_table,
+                     kv, bias, scale_dtype == RLK_SCALE_F16, stream, "rope_and_write_kv_ex");
 }

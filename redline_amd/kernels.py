@@ -18,8 +18,12 @@ from ._lib import KVLayerView, check, lib
 
 __all__ = [
     "embedding_lookup", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
-    "gather_rows", "resolve_input_ids", "rope_and_write_kv", "KVDType", "KVCache",
+    "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
+    "KVCache", "SCALE_F32", "SCALE_F16",
 ]
+
+SCALE_F32 = _lib.RLK_SCALE_F32
+SCALE_F16 = _lib.RLK_SCALE_F16
 
 
 class KVDType:
@@ -123,6 +127,21 @@ def rope_and_write_kv(qkv, positions, slot_mapping, num_tokens, num_heads, cos_t
         C.byref(kv), _stream(stream)))
 
 
+def rope_and_write_kv_ex(qkv, positions, slot_mapping, num_tokens, num_heads, cos_table, sin_table,
+                         kv: KVLayerView, qkv_bias=None, scale_dtype=SCALE_F32, stream=None):
+    """Extension: optional QKV bias added before RoPE, optional fp16 INT8 scales."""
+    if num_tokens > 0:
+        _need(positions, num_tokens, "positions"); _need(slot_mapping, num_tokens, "slot_mapping")
+        _need(qkv, num_tokens * (num_heads + 2 * kv.num_kv_heads) * kv.head_dim, "qkv")
+        _need(qkv_bias, (num_heads + 2 * kv.num_kv_heads) * kv.head_dim, "qkv_bias")
+    opt = _lib.RopeKVOptions(_ptr(qkv_bias, torch.float16, "qkv_bias", True), scale_dtype)
+    check(lib().rlk_rope_and_write_kv_ex(
+        _ptr(qkv, torch.float16, "qkv"), _ptr(positions, torch.int32, "positions"),
+        _ptr(slot_mapping, torch.int32, "slot_mapping"), num_tokens, num_heads,
+        _ptr(cos_table, torch.float32, "cos_table"), _ptr(sin_table, torch.float32, "sin_table"),
+        C.byref(kv), C.byref(opt), _stream(stream)))
+
+
 class KVCache:
     """Paged KV cache in one zeroed device allocation, laid out per layer as
     K, V (then k_scale, v_scale for INT8), each [num_blocks, Hkv, bs, D]
@@ -131,7 +150,7 @@ class KVCache:
     that padded rows write into."""
 
     def __init__(self, num_layers, num_blocks, num_kv_heads, head_dim, block_size=16,
-                 dtype=KVDType.kFP16, device="cuda"):
+                 dtype=KVDType.kFP16, device="cuda", scale_dtype=SCALE_F32):
         if num_blocks <= 1 or block_size <= 0 or num_layers <= 0:
             raise _lib.Error(_lib.RLK_EINVAL, "bad KV cache config")
         self.num_layers, self.num_blocks = num_layers, num_blocks
@@ -139,7 +158,9 @@ class KVCache:
             num_kv_heads, head_dim, block_size, dtype)
         cells = num_blocks * num_kv_heads * block_size
         elem = 2 if dtype == KVDType.kFP16 else 1
-        per_layer = 2 * cells * head_dim * elem + (2 * cells * 4 if dtype == KVDType.kINT8 else 0)
+        sbytes = 2 if scale_dtype == SCALE_F16 else 4
+        sdt = torch.float16 if scale_dtype == SCALE_F16 else torch.float32
+        per_layer = 2 * cells * head_dim * elem + (2 * cells * sbytes if dtype == KVDType.kINT8 else 0)
         self.storage = torch.zeros(per_layer * num_layers, dtype=torch.uint8, device=device)
         self._views, self._tensors = [], []
         shape = (num_blocks, num_kv_heads, block_size, head_dim)
@@ -151,8 +172,8 @@ class KVCache:
             v = self.storage[off:off + kb].view(tdt).view(shape); off += kb
             ks = vs = None
             if dtype == KVDType.kINT8:
-                ks = self.storage[off:off + cells * 4].view(torch.float32).view(shape[:3]); off += cells * 4
-                vs = self.storage[off:off + cells * 4].view(torch.float32).view(shape[:3]); off += cells * 4
+                ks = self.storage[off:off + cells * sbytes].view(sdt).view(shape[:3]); off += cells * sbytes
+                vs = self.storage[off:off + cells * sbytes].view(sdt).view(shape[:3]); off += cells * sbytes
             view = KVLayerView(k.data_ptr(), v.data_ptr(), ks.data_ptr() if ks is not None else None,
                                vs.data_ptr() if vs is not None else None, block_size, num_kv_heads,
                                head_dim, dtype)

@@ -292,3 +292,61 @@ def test_rope_int8_ties_round_half_even():
     want = np.rint(v.astype(np.float64) * 64)  # numpy rint: half to even
     assert np.array_equal(vc[1, 0, 0].astype(np.float64), want)
     assert np.any(np.abs(v.astype(np.float64) * 64 % 1) == 0.5)
+
+
+def test_rope_bias_extension_equivalence():
+    """With a QKV bias the result equals the plain function applied to
+    fp16(qkv + bias) (the reference adds the bias in its QKV GEMM epilogue,
+    linear.cpp:108), except that qkv's k/v sections stay unbiased."""
+    rng = np.random.default_rng(9)
+    T, hq, hkv, D = 20, 4, 2, 128
+    qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
+    bias = randn_f16(rng, ((hq + 2 * hkv) * D,), 0.02)
+    pos = rng.integers(0, 200, T).astype(np.int32)
+    slots = (np.arange(T) + 16).astype(np.int32)
+    cos, sin = oracle.rope_cos_sin_tables(1e6, D, 200)
+    kc_a, vc_a = np.zeros((4, hkv, 16, D), np.float16), np.zeros((4, hkv, 16, D), np.float16)
+    a = qkv.copy()
+    oracle.rope_and_write_kv(a, pos, slots, hq, hkv, D, cos, sin, kc_a, vc_a, bias=bias)
+    biased = (qkv.astype(np.float32) + bias.astype(np.float32)).astype(np.float16)
+    kc_b, vc_b = np.zeros_like(kc_a), np.zeros_like(vc_a)
+    b = biased.copy()
+    oracle.rope_and_write_kv(b, pos, slots, hq, hkv, D, cos, sin, kc_b, vc_b)
+    assert np.array_equal(a[:, :hq * D], b[:, :hq * D])
+    assert np.array_equal(a[:, hq * D:], qkv[:, hq * D:])
+    assert np.array_equal(kc_a, kc_b) and np.array_equal(vc_a, vc_b)
+
+
+def test_rope_fp16_scale_extension():
+    """scale16 = fp16(amax/127); codes = rint(x / scale16) (tie-masked float64),
+    within 1 of the fp32-scale codes; |code*scale16 - x| <= 0.51*scale16 +
+    the clamp at 127 when rounding the scale down pushes amax/scale16 > 127."""
+    rng = np.random.default_rng(10)
+    T, hq, hkv, D = 48, 2, 2, 128
+    qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
+    pos = rng.integers(0, 100, T).astype(np.int32)
+    slots = (np.arange(T) + 16).astype(np.int32)
+    cos, sin = oracle.rope_cos_sin_tables(1e4, D, 100)
+    shape = (5, hkv, 16, D)
+    k16 = np.zeros(shape, np.float16)
+    v16 = np.zeros_like(k16)
+    oracle.rope_and_write_kv(qkv.copy(), pos, slots, hq, hkv, D, cos, sin, k16, v16)
+    k8, v8 = np.zeros(shape, np.int8), np.zeros(shape, np.int8)
+    ks, vs = np.zeros(shape[:3], np.uint16), np.zeros(shape[:3], np.uint16)
+    oracle.rope_and_write_kv(qkv.copy(), pos, slots, hq, hkv, D, cos, sin, k8, v8, ks, vs,
+                             int8=True, scale16=True)
+    k8f, v8f = np.zeros(shape, np.int8), np.zeros(shape, np.int8)
+    ksf, vsf = np.zeros(shape[:3], np.float32), np.zeros(shape[:3], np.float32)
+    oracle.rope_and_write_kv(qkv.copy(), pos, slots, hq, hkv, D, cos, sin, k8f, v8f, ksf, vsf,
+                             int8=True)
+    blk, off = slots // 16, slots % 16
+    for c16, c8, sc, c8f in ((k16, k8, ks, k8f), (v16, v8, vs, v8f)):
+        x = c16[blk, :, off].astype(np.float64)
+        q = c8[blk, :, off].astype(np.float64)
+        s = sc[blk, :, off].view(np.float16).astype(np.float64)[..., None]
+        amax = np.abs(x).max(-1, keepdims=True)
+        assert np.array_equal(s, to16(np.float32(amax) / np.float32(127)).astype(np.float64))
+        r = x / s
+        far = np.abs(np.abs(r - np.floor(r)) - 0.5) > 1e-4
+        assert np.array_equal(q[far], np.clip(np.rint(r[far]), -127, 127))
+        assert np.max(np.abs(q - c8f[blk, :, off])) <= 1

@@ -265,3 +265,76 @@ def test_rope_int8_exact_ties(torch_cuda):
                            hq, hkv, D, 2, True)
     _, vq, _, vs = cache.tensors(0)
     assert np.array_equal(vq[1, 0, 0].cpu().numpy().astype(np.float64), np.rint(v.astype(np.float64) * 64))
+
+
+@pytest.mark.parametrize("int8,scale16", [(False, False), (True, False), (True, True)])
+def test_rope_extension_bias_and_fp16_scale(torch_cuda, int8, scale16):
+    """rlk_rope_and_write_kv_ex on the Qwen2-7B workload (C5, bias before
+    RoPE): bit-exact with the oracle's extension, including fp16 scales."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    w = make_workload("C5")
+    m = w.model
+    say(f"rope ex C5 int8={int8} scale16={scale16}")
+    meta, shape, lay, _ = build_batch(w)
+    T = w.num_tokens
+    pos = meta[lay["positions"]:lay["positions"] + T].copy()
+    slots = meta[lay["slot_mapping"]:lay["slot_mapping"] + T].copy()
+    rng = np.random.default_rng(13)
+    qkv = randn_f16(rng, (T, m.qkv_cols))
+    bias = randn_f16(rng, (m.qkv_cols,), 0.02)
+    D = m.head_dim
+    cos, sin = ra.rope_cos_sin_tables(m.theta, D, w.max_pos)
+    sdt = K.SCALE_F16 if scale16 else K.SCALE_F32
+    cache = K.KVCache(1, w.num_blocks, m.hkv, D, 16, K.KVDType.kINT8 if int8 else K.KVDType.kFP16,
+                      scale_dtype=sdt)
+    d_qkv, d_meta = dev(torch, qkv), dev(torch, meta)
+    K.rope_and_write_kv_ex(d_qkv, d_meta[lay["positions"]:], d_meta[lay["slot_mapping"]:], T, m.hq,
+                           dev(torch, cos), dev(torch, sin), cache.layer(0), dev(torch, bias), sdt)
+    shape4 = (w.num_blocks, m.hkv, 16, D)
+    kc = np.zeros(shape4, np.int8 if int8 else np.float16)
+    vc = np.zeros_like(kc)
+    ks = np.zeros(shape4[:3], np.uint16 if scale16 else np.float32) if int8 else None
+    vs = np.zeros_like(ks) if int8 else None
+    want = qkv.copy()
+    oracle.rope_and_write_kv(want, pos, slots, m.hq, m.hkv, D, cos, sin, kc, vc, ks, vs, 16, int8,
+                             bias=bias, scale16=scale16)
+    assert_bits_equal(d_qkv.cpu().numpy(), want, "qkv")
+    blk, off = slots // 16, slots % 16
+    cells = ((blk[:, None] * m.hkv + np.arange(m.hkv)[None, :]) * 16 + off[:, None]).reshape(-1)
+    d_cells = dev(torch, cells.astype(np.int64))
+    k, v, k_s, v_s = cache.tensors(0)
+    for gpu, cpu in ((k, kc), (v, vc)):
+        assert_bits_equal(gpu.reshape(-1, D).index_select(0, d_cells).cpu().numpy(),
+                          cpu.reshape(-1, D)[cells], "cache")
+    if int8:
+        for gpu, cpu in ((k_s, ks), (v_s, vs)):
+            got = gpu.reshape(-1).index_select(0, d_cells).cpu().numpy()
+            assert_bits_equal(got.view(cpu.dtype), cpu.reshape(-1)[cells], "scales")
+
+
+def test_rope_extension_null_options_is_plain(torch_cuda):
+    torch = torch_cuda
+    import ctypes as C
+    from redline_amd import _lib, kernels as K
+    say("rope ex null options")
+    rng = np.random.default_rng(14)
+    hq, hkv, D = 4, 2, 64
+    qkv = randn_f16(rng, (5, (hq + 2 * hkv) * D))
+    pos = np.arange(5, dtype=np.int32)
+    slots = np.arange(16, 21, dtype=np.int32)
+    cos, sin = ra.rope_cos_sin_tables(1e4, D, 8)
+    outs = []
+    for use_ex in (False, True):
+        cache = K.KVCache(1, 2, hkv, D)
+        d = dev(torch, qkv)
+        args = (d.data_ptr(), dev(torch, pos).data_ptr(), dev(torch, slots).data_ptr(), 5, hq,
+                dev(torch, cos).data_ptr(), dev(torch, sin).data_ptr(), C.byref(cache.layer(0)))
+        stream = torch.cuda.current_stream().cuda_stream
+        st = (_lib.lib().rlk_rope_and_write_kv_ex(*args, None, stream) if use_ex
+              else _lib.lib().rlk_rope_and_write_kv(*args, stream))
+        assert st == 0
+        torch.cuda.synchronize()
+        outs.append((d.cpu().numpy(), cache.tensors(0)[0].cpu().numpy()))
+    assert_bits_equal(outs[0][0], outs[1][0], "qkv")
+    assert_bits_equal(outs[0][1], outs[1][1], "k cache")
