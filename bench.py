@@ -118,6 +118,26 @@ class LayerData:
         }
 
 
+def measured_traffic(workload, kernel_prefix):
+    """HBM bytes per launch of a kernel as measured by the rocprofv3 FETCH_SIZE
+    / WRITE_SIZE runs summarised in profiles/hbm_traffic_C2_C5.md (None when
+    that summary has no row for it)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_C2_C5.md")
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0] == workload and cells[1].startswith("`" + kernel_prefix):
+            return round(float(cells[4]) * 1e6)
+    return None
+
+
+KERNEL_SYMBOL = {"embedding_lookup": "gather_rows_kernel", "fused_add_rmsnorm": "add_rmsnorm_kernel",
+                 "rope_and_write_kv": "rope_kv_kernel", "silu_and_mul": "silu_and_mul_kernel"}
+
+
 def copy_baseline(torch, nbytes=1 << 30, reps=20):
     """A plain device-to-device copy (torch) of `nbytes`: the practical
     streaming ceiling, read + write bytes counted."""
@@ -184,6 +204,33 @@ def per_kernel(torch, data, reps, only=None):
     return out
 
 
+SWEEP_KNOBS = {
+    "embedding_lookup": {"RLK_TUNE_GATHER_BS": [64, 128, 256], "RLK_TUNE_GATHER_NT": [0, 1]},
+    "fused_add_rmsnorm": {"RLK_TUNE_NORM_TPR": [64, 128, 256, 512], "RLK_TUNE_NORM_NT": [0, 1]},
+    "silu_and_mul": {"RLK_TUNE_SWIGLU_BS": [64, 128, 256], "RLK_TUNE_SWIGLU_NT": [0, 1]},
+    "rope_and_write_kv": {"RLK_TUNE_ROPE_WPT": [1, 2, 4, 5, 6, 8]},
+}
+
+
+def sweep(torch, data, reps, only=None):
+    """Times each kernel under every combination of its launch-policy knobs
+    (the RLK_TUNE_* environment overrides the launchers read per call)."""
+    import itertools
+    for kern, knobs in SWEEP_KNOBS.items():
+        if only and kern != only:
+            continue
+        names = list(knobs)
+        for vals in itertools.product(*knobs.values()):
+            for n, v in zip(names, vals):
+                os.environ[n] = str(v)
+            r = per_kernel(torch, data, reps, kern)[kern]
+            print(json.dumps({"workload": data.w.key, "kernel": kern, "knobs": dict(zip(names, vals)),
+                              "us_per_call": r["us_per_call"], "gb_per_s": r["gb_per_s"]}),
+                  flush=True)
+        for n in names:
+            del os.environ[n]
+
+
 def cpu_baseline(torch, data, seconds=10.0):
     """The CPU oracle (oracle/oracle.c, single thread) on the same step:
     a bounded number of full steps over one input set, copied to host."""
@@ -237,6 +284,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--sweep", action="store_true",
+                    help="launch-policy sweep: time every kernel under each setting of its "
+                         "RLK_TUNE_* overrides on the workload, one JSON line per setting")
     ap.add_argument("--profile-calls", type=int, default=0,
                     help="counter-collection mode: N eager calls of each kernel (rotating sets) "
                          "plus N copies of 256 MiB for calibration, then exit")
@@ -257,6 +307,10 @@ def main():
     data = LayerData(torch, K, w)
     nb = data.bytes()
     step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
+
+    if args.sweep:
+        sweep(torch, data, args.reps, args.only)
+        return
 
     if args.profile_calls:
         fns = {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
@@ -314,7 +368,10 @@ def main():
     dk = kern[dominant]
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": dk["gb_per_s"],
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_of_hbm_peak"],
-                "traffic": None, "bytes_per_launch": nb[dominant]}
+                "traffic": measured_traffic(w.key, KERNEL_SYMBOL[dominant]),
+                "traffic_source": "profiles/hbm_traffic_C2_C5.md (rocprofv3 FETCH_SIZE x2.0 + "
+                                  "WRITE_SIZE x1.0, calibrated on a 256 MiB copy)",
+                "bytes_per_launch": nb[dominant]}
 
     extra = {}
     if not args.no_extra:
