@@ -19,12 +19,22 @@
 
 #include "redline_amd/rlk.h"
 
+// Inside a Redline build (src/ on the include path) the engine's own
+// redline::Error is used; standalone, an identical class is declared here.
+#if __has_include("core/common.h")
+#include "core/common.h"
+#else
 namespace redline {
 
 class Error : public std::runtime_error {
  public:
   explicit Error(const std::string& msg) : std::runtime_error(msg) {}
 };
+
+}  // namespace redline
+#endif
+
+namespace redline {
 
 enum class KVDType { kFP16 = RLK_KV_FP16, kINT8 = RLK_KV_INT8 };
 
