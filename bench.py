@@ -231,6 +231,59 @@ def sweep(torch, data, reps, only=None):
             del os.environ[n]
 
 
+def attention_bench(torch, K, w, int8, reps, rotations=3, seed=0, eager_calls=0):
+    """Decode attention over the workload's decode items: per-call time and
+    GB/s (K/V rows read once per GQA group), rotating over `rotations`
+    batches drawn from one KV pool filled at random."""
+    from redline_amd.configs import build_batch, bytes_decode_attention
+    m = w.model
+    D = m.head_dim
+    cache = K.KVCache(1, w.num_blocks, m.hkv, D, w.block_size,
+                      K.KVDType.kINT8 if int8 else K.KVDType.kFP16)
+    k, v, ks, vs = cache.tensors(0)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    if int8:
+        k.copy_(torch.randint(-127, 128, k.shape, generator=g, device="cuda", dtype=torch.int8))
+        v.copy_(torch.randint(-127, 128, v.shape, generator=g, device="cuda", dtype=torch.int8))
+        ks.fill_(0.01)
+        vs.fill_(0.01)
+    else:
+        k.normal_(generator=g)
+        v.normal_(generator=g)
+    calls, nbytes = [], 0
+    for r in range(rotations):
+        meta, shape, lay, tables = build_batch(w, np.random.default_rng(seed * 100 + r + 7))
+        T, nd = w.num_tokens, shape.num_decode_items
+        d_meta = torch.from_numpy(meta[:lay["total_words"]]).cuda()
+        qkv = torch.randn((T, m.qkv_cols), generator=g, device="cuda").half()
+        out = torch.empty((T, m.hq * D), dtype=torch.float16, device="cuda")
+        parts = (shape.max_context + K.kDecodePartitionSize - 1) // K.kDecodePartitionSize
+        ws = K.DecodeWorkspace(nd, m.hq, parts, D)
+        sl = lambda name, n: d_meta[lay[name]:lay[name] + n]  # noqa: E731
+        p = K.attention_params(qkv, m.qkv_cols, out, m.hq, D ** -0.5, cache.layer(0),
+                               d_meta[lay["block_tables"]:], max(len(t) for t in tables),
+                               sl("positions", T))
+        wk = K.decode_work(sl("decode_token", nd), sl("decode_seq", nd), nd, parts, ws)
+        pos = meta[lay["positions"]:lay["positions"] + T]
+        toks = meta[lay["decode_token"]:lay["decode_token"] + nd]
+        nbytes += bytes_decode_attention(pos[toks] + 1, m.hq, m.hkv, D, int8)
+        calls.append((p, wk, qkv, out, ws, d_meta))
+    if eager_calls:  # counter-collection mode: plain launches, no timing
+        for i in range(eager_calls):
+            K.paged_attention_decode(calls[i % rotations][0], calls[i % rotations][1])
+        torch.cuda.synchronize()
+        return None
+    gph = capture(torch, lambda: [K.paged_attention_decode(c[0], c[1]) for c in calls])
+    ms = time_graph(torch, gph, reps) / rotations
+    del gph
+    gbs = nbytes / rotations / (ms * 1e-3) / 1e9
+    log(f"  {w.key} paged_attention_decode {'INT8' if int8 else 'FP16'} KV: {ms * 1e3:8.2f} us "
+        f"{gbs:8.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)")
+    return {"us_per_call": round(ms * 1e3, 3), "gb_per_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_call": int(nbytes / rotations)}
+
+
 def cpu_baseline(torch, data, seconds=10.0):
     """The CPU oracle (oracle/oracle.c, single thread) on the same step:
     a bounded number of full steps over one input set, copied to host."""
@@ -281,9 +334,12 @@ def main():
     ap.add_argument("--workload", default="C2")
     ap.add_argument("--reps", type=int, default=20, help="graph replays per kernel timing")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C3-C5 per-kernel figures")
+    ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention figures")
     ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--rotations", type=int, default=None,
+                    help="rotating input sets (default: enough to exceed 2x the Infinity Cache)")
     ap.add_argument("--sweep", action="store_true",
                     help="launch-policy sweep: time every kernel under each setting of its "
                          "RLK_TUNE_* overrides on the workload, one JSON line per setting")
@@ -304,7 +360,7 @@ def main():
 
     w = make_workload(args.workload)
     log(f"setting up {w.key} ({w.model.name}, T={w.num_tokens})")
-    data = LayerData(torch, K, w)
+    data = LayerData(torch, K, w, rotations=args.rotations)
     nb = data.bytes()
     step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
 
@@ -320,6 +376,9 @@ def main():
                 continue
             for i in range(args.profile_calls):
                 fns[name](i % data.R)
+        if args.only in (None, "paged_attention_decode"):
+            for int8 in (False, True):
+                attention_bench(torch, K, w, int8, 0, eager_calls=args.profile_calls)
         src = torch.empty(128 << 20, dtype=torch.float16, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(args.profile_calls):
@@ -383,6 +442,12 @@ def main():
             del dx
             torch.cuda.empty_cache()
 
+    attention = {}
+    if not args.no_attention:
+        for int8 in (False, True):
+            attention["int8_kv" if int8 else "fp16_kv"] = attention_bench(torch, K, w, int8, args.reps)
+            torch.cuda.empty_cache()
+
     copy = copy_baseline(torch)
     floor = launch_floor_us(torch, K)
     log(f"device copy baseline: {copy} GB/s; one-workgroup launch floor {floor} us")
@@ -410,6 +475,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kern,
         "prefill": extra,
+        "decode_attention": attention,
         "copy_baseline_gb_per_s": copy,
         "launch_floor_us": floor,
     }

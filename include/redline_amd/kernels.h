@@ -59,6 +59,38 @@ static_assert(offsetof(KVLayerView, dtype) == offsetof(rlk_kv_layer_view, dtype)
               "KVLayerView layout");
 
 namespace kernels {
+
+// Attention interface structs: field order of the reference's
+// (src/cuda/kernels/kernels.h:91-117).
+struct AttentionParams {
+  const half* q = nullptr;  // query rows, stride q_stride elements per token
+  int q_stride = 0;
+  half* out = nullptr;      // [num_tokens, num_heads * head_dim]
+  int num_heads = 0;
+  float scale = 1.0f;
+  KVLayerView kv;
+  const int32_t* block_tables = nullptr;  // [num_seqs, max_blocks_per_seq]
+  int max_blocks_per_seq = 0;
+  const int32_t* positions = nullptr;     // [num_tokens]
+};
+
+struct DecodeAttentionWork {
+  const int32_t* item_token = nullptr;  // [num_items]
+  const int32_t* item_seq = nullptr;    // [num_items]
+  int num_items = 0;
+  int max_partitions = 1;   // grid size; partitions beyond the context exit early
+  float* ws_out = nullptr;  // [num_items, num_heads, max_partitions, head_dim]
+  float* ws_max = nullptr;  // [num_items, num_heads, max_partitions]
+  float* ws_sum = nullptr;
+};
+constexpr int kDecodePartitionSize = RLK_DECODE_PARTITION_SIZE;
+
+static_assert(sizeof(AttentionParams) == sizeof(rlk_attention_params), "AttentionParams layout");
+static_assert(offsetof(AttentionParams, positions) == offsetof(rlk_attention_params, positions),
+              "AttentionParams layout");
+static_assert(sizeof(DecodeAttentionWork) == sizeof(rlk_decode_attention_work),
+              "DecodeAttentionWork layout");
+
 namespace detail {
 
 inline void check(int status) {
@@ -115,6 +147,14 @@ inline void rope_and_write_kv(half* qkv, const int32_t* positions, const int32_t
   detail::check(rlk_rope_and_write_kv(detail::bits(qkv), positions, slot_mapping, num_tokens,
                                       num_heads, cos_table, sin_table,
                                       reinterpret_cast<const rlk_kv_layer_view*>(&kv), stream));
+}
+
+// Paged decode attention (flash-decoding split-K over 256-key partitions).
+inline void paged_attention_decode(const AttentionParams& p, const DecodeAttentionWork& w,
+                                   hipStream_t stream) {
+  detail::check(rlk_paged_attention_decode(reinterpret_cast<const rlk_attention_params*>(&p),
+                                           reinterpret_cast<const rlk_decode_attention_work*>(&w),
+                                           stream));
 }
 
 }  // namespace kernels

@@ -141,6 +141,49 @@ int rlk_rope_and_write_kv_ex(uint16_t* qkv, const int32_t* positions,
                              const rlk_kv_layer_view* kv, const rlk_rope_kv_options* options,
                              hipStream_t stream);
 
+/* -------------------------------------------------------------- attention */
+
+/* Keys per split-K partition of the decode attention (the reference's
+ * kDecodePartitionSize, kernels.h:116); it fixes the workspace layout. */
+#define RLK_DECODE_PARTITION_SIZE 256
+
+/* Field order and types of redline::kernels::AttentionParams
+ * (src/cuda/kernels/kernels.h:91-101). */
+typedef struct rlk_attention_params {
+  const uint16_t* q;     /* query rows, q_stride elements per token (fp16) */
+  int q_stride;
+  uint16_t* out;         /* [num_tokens, num_heads * head_dim] fp16 */
+  int num_heads;
+  float scale;           /* softmax scale, applied to q */
+  rlk_kv_layer_view kv;
+  const int32_t* block_tables; /* [num_seqs, max_blocks_per_seq] */
+  int max_blocks_per_seq;
+  const int32_t* positions;    /* [num_tokens] */
+} rlk_attention_params;
+
+/* Field order and types of redline::kernels::DecodeAttentionWork
+ * (kernels.h:106-115). */
+typedef struct rlk_decode_attention_work {
+  const int32_t* item_token; /* [num_items] query token of each decode item */
+  const int32_t* item_seq;   /* [num_items] its sequence (row of block_tables) */
+  int num_items;
+  int max_partitions;        /* grid size; partitions beyond a context exit early */
+  float* ws_out;             /* [num_items, num_heads, max_partitions, head_dim] */
+  float* ws_max;             /* [num_items, num_heads, max_partitions] */
+  float* ws_sum;
+} rlk_decode_attention_work;
+
+/* Decode attention: item i's query token t attends to positions
+ * [0, positions[t]] of its sequence through the paged cache (FP16, or INT8
+ * with fp32 scales); all G = num_heads / num_kv_heads query heads of a kv head
+ * share each K/V read; contexts longer than one partition are split and merged
+ * through the caller's workspace.  Replaces kernels::paged_attention_decode,
+ * src/cuda/kernels/attention.cu:70-210,362-398.
+ * num_items <= 0: no-op.  head_dim not in {64, 128} or G > 8: RLK_EUNSUPPORTED.
+ * max_partitions > 1 needs ws_out / ws_max / ws_sum. */
+int rlk_paged_attention_decode(const rlk_attention_params* params,
+                               const rlk_decode_attention_work* work, hipStream_t stream);
+
 /* ------------------------------------------------------ host-side helpers */
 
 /* IEEE fp16 <-> fp32 with round-to-nearest-even.

@@ -49,6 +49,8 @@ def lib() -> C.CDLL:
                                             _I, _I]
         L.orc_rope_and_write_kv_ex.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
                                                _P, _I, _I, _P, _I]
+        L.orc_paged_attention_decode.argtypes = [_P, _I, _P, _I, C.c_float, _P, _P, _P, _P, _I,
+                                                 _I, _I, _I, _P, _I, _P, _P, _P, _I]
         L.orc_layer_step.argtypes = [_P, _P, _I, _I, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P,
                                      _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P]
         _o = L
@@ -171,3 +173,23 @@ def rope_and_write_kv(qkv, positions, slots, hq, hkv, d, cos_t, sin_t, k_cache, 
                                    p(np.ascontiguousarray(sin_t, np.float32)), p(kc), p(vc),
                                    p(k_scale), p(v_scale), block_size, int(int8), p(b),
                                    int(scale16))
+
+
+def paged_attention_decode(q, q_stride, num_heads, scale, k_cache, v_cache, k_scale, v_scale,
+                           block_tables, positions, item_token, item_seq, num_tokens,
+                           int8=False):
+    """Returns out fp16 [num_tokens, num_heads * D]; rows of tokens that are not
+    decode items are zero.  Caches are [num_blocks, Hkv, bs, D]."""
+    nb, hkv, bs, D = k_cache.shape
+    out = np.zeros((num_tokens, num_heads * D), np.uint16)
+    kc = k_cache.view(np.uint16) if k_cache.dtype == np.float16 else np.ascontiguousarray(k_cache)
+    vc = v_cache.view(np.uint16) if v_cache.dtype == np.float16 else np.ascontiguousarray(v_cache)
+    bt = np.ascontiguousarray(block_tables, np.int32)
+    it = np.ascontiguousarray(item_token, np.int32)
+    lib().orc_paged_attention_decode(
+        p(_u16(q)), q_stride, p(out), num_heads, scale, p(kc), p(vc),
+        p(None if k_scale is None else np.ascontiguousarray(k_scale, np.float32)),
+        p(None if v_scale is None else np.ascontiguousarray(v_scale, np.float32)), bs, hkv, D,
+        int(int8), p(bt), bt.shape[1], p(np.ascontiguousarray(positions, np.int32)), p(it),
+        p(np.ascontiguousarray(item_seq, np.int32)), it.size)
+    return out.view(np.float16)

@@ -27,6 +27,10 @@
  *   orc_rope_and_write_kv_ex   bias: equivalence with the plain function on
  *                              fp16(qkv + bias); fp16 scale: scale == fp16(amax/127)
  *                              and tie-masked float64 codes against the stored scale.
+ *   orc_paged_attention_decode scipy softmax attention in float64 over the
+ *                              gathered cache, q = 0 -> mean of V, a dominant key
+ *                              -> its V, invariance under physical block moves,
+ *                              INT8 == FP16 path on the dequantised cache.
  *   orc_rope_and_write_kv      pos 0 identity, V passthrough, rotation by angle
  *                              against float64 rotation matrix, norm
  *                              preservation, slot/cell address KATs from
@@ -36,6 +40,7 @@
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------ fp16 bits */
@@ -259,6 +264,59 @@ void orc_rope_and_write_kv(uint16_t* qkv, const int32_t* positions, const int32_
                            int int8) {
   orc_rope_and_write_kv_ex(qkv, positions, slots, T, Hq, Hkv, D, cos_t, sin_t, k_cache, v_cache,
                            k_scale, v_scale, bs, int8, NULL, 0);
+}
+
+/* Paged decode attention (attention.cu:70-210): item i's token t attends to
+ * positions [0, positions[t]] of sequence item_seq[i] through the block table;
+ * query head h uses kv head h / (num_heads / Hkv).  Evaluated in double:
+ * s_j = (q * scale) . k_j (k dequantised as code * k_scale for INT8),
+ * p = softmax(s), out = fp16(sum_j p_j v_j).  The kernel's split-K partition
+ * merge is an exact identity of this formula and has no counterpart here. */
+void orc_paged_attention_decode(const uint16_t* q, int q_stride, uint16_t* out, int num_heads,
+                                float scale, const void* k_cache, const void* v_cache,
+                                const float* k_scale, const float* v_scale, int bs, int Hkv,
+                                int D, int int8, const int32_t* block_tables, int max_blocks,
+                                const int32_t* positions, const int32_t* item_token,
+                                const int32_t* item_seq, int num_items) {
+  const int G = num_heads / Hkv;
+  for (int it = 0; it < num_items; ++it) {
+    const int t = item_token[it], seq = item_seq[it];
+    const int ctx = positions[t] + 1;
+    const int32_t* table = block_tables + (size_t)seq * max_blocks;
+    double* s = (double*)malloc(sizeof(double) * (size_t)ctx);
+    double acc[256];
+    for (int h = 0; h < num_heads; ++h) {
+      const int kvh = h / G;
+      const uint16_t* qh = q + (size_t)t * q_stride + (size_t)h * D;
+      double mx = -INFINITY;
+      for (int j = 0; j < ctx; ++j) {
+        const size_t cell = ((size_t)table[j / bs] * Hkv + kvh) * bs + j % bs;
+        double dot = 0.0;
+        for (int d = 0; d < D; ++d) {
+          const double kv = int8 ? (double)((const int8_t*)k_cache)[cell * D + d] * k_scale[cell]
+                                 : (double)orc_h2f(((const uint16_t*)k_cache)[cell * D + d]);
+          dot += (double)orc_h2f(qh[d]) * (double)scale * kv;
+        }
+        s[j] = dot;
+        if (dot > mx) mx = dot;
+      }
+      double den = 0.0;
+      for (int d = 0; d < D; ++d) acc[d] = 0.0;
+      for (int j = 0; j < ctx; ++j) {
+        const double e = exp(s[j] - mx);
+        den += e;
+        const size_t cell = ((size_t)table[j / bs] * Hkv + kvh) * bs + j % bs;
+        for (int d = 0; d < D; ++d) {
+          const double vv = int8 ? (double)((const int8_t*)v_cache)[cell * D + d] * v_scale[cell]
+                                 : (double)orc_h2f(((const uint16_t*)v_cache)[cell * D + d]);
+          acc[d] += e * vv;
+        }
+      }
+      for (int d = 0; d < D; ++d)
+        out[(size_t)t * num_heads * D + (size_t)h * D + d] = orc_f2h((float)(acc[d] / den));
+    }
+    free(s);
+  }
 }
 
 /* One layer's hot path on one batch, as a single call for CPU timing:

@@ -51,6 +51,26 @@ class RopeKVOptions(C.Structure):
     _fields_ = [("qkv_bias", C.c_void_p), ("scale_dtype", C.c_int)]
 
 
+RLK_DECODE_PARTITION_SIZE = 256
+
+
+class AttentionParams(C.Structure):
+    """Mirror of rlk_attention_params / kernels::AttentionParams (kernels.h:91-101)."""
+
+    _fields_ = [("q", C.c_void_p), ("q_stride", C.c_int), ("out", C.c_void_p),
+                ("num_heads", C.c_int), ("scale", C.c_float), ("kv", KVLayerView),
+                ("block_tables", C.c_void_p), ("max_blocks_per_seq", C.c_int),
+                ("positions", C.c_void_p)]
+
+
+class DecodeAttentionWork(C.Structure):
+    """Mirror of rlk_decode_attention_work / kernels::DecodeAttentionWork."""
+
+    _fields_ = [("item_token", C.c_void_p), ("item_seq", C.c_void_p), ("num_items", C.c_int),
+                ("max_partitions", C.c_int), ("ws_out", C.c_void_p), ("ws_max", C.c_void_p),
+                ("ws_sum", C.c_void_p)]
+
+
 class BatchShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in (
         "num_tokens", "num_seqs", "num_logit_rows", "num_decode_items",
@@ -81,6 +101,8 @@ _SIGNATURES = {
     "rlk_rope_and_write_kv": (_I, [_P, _P, _P, _I, _I, _P, _P, C.POINTER(KVLayerView), _P]),
     "rlk_rope_and_write_kv_ex": (_I, [_P, _P, _P, _I, _I, _P, _P, C.POINTER(KVLayerView),
                                       C.POINTER(RopeKVOptions), _P]),
+    "rlk_paged_attention_decode": (_I, [C.POINTER(AttentionParams),
+                                        C.POINTER(DecodeAttentionWork), _P]),
     "rlk_float_to_half_bits": (C.c_uint16, [C.c_float]),
     "rlk_half_bits_to_float": (C.c_float, [C.c_uint16]),
     "rlk_rope_inv_freq": (_I, [C.c_double, _I, _I, C.c_double, C.c_double, C.c_double, _I, _P]),

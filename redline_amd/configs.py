@@ -161,3 +161,13 @@ def bytes_rope_kv(T, hq, hkv, D, int8=False):
     q_write = 2 * hq * D
     kv_write = (2 * hkv * D + 8 * hkv) if int8 else 4 * hkv * D
     return T * (qkv_read + q_write + kv_write + 4 * D + 8)
+
+
+def bytes_decode_attention(contexts, hq, hkv, D, int8=False):
+    """K and V rows of every attended key (plus their scales for INT8), the
+    query heads read and the output written; split-K partials are workspace
+    traffic and not counted."""
+    ctx = int(np.sum(contexts))
+    elem = 1 if int8 else 2
+    kv = ctx * hkv * (2 * D * elem + (8 if int8 else 0))
+    return kv + len(contexts) * hq * D * 2 * 2 + ctx // 16 * 4

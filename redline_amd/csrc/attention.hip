@@ -1,0 +1,378 @@
+// Paged decode attention over the block-structured KV cache, for gfx950.
+//
+// Flash-decoding split-K with the reference's work decomposition and
+// workspace layout (src/cuda/kernels/attention.cu:70-210 in Neil456/Redline):
+// a workgroup handles one (decode item, kv head, 256-key partition) and all G
+// query heads of that kv head's GQA group, so every K/V byte is read once per
+// group; partitions are merged by a small reduction kernel when a context
+// spans more than one.
+//
+// The in-workgroup mapping is wave64-first (8 waves per workgroup):
+//   * every key of the partition is resolved once to its cache cell (block
+//     table lookup) into LDS, so K/V addresses are one LDS read each;
+//   * a K or V row of D elements is D/8 lanes x 8 elements: one 16-byte load
+//     per lane for fp16 rows, one 8-byte load for int8 rows; a wave covers
+//     64/(D/8) keys per pass and each wave requests all of its K and V rows
+//     for the partition before consuming the first (loads past the context
+//     re-read the last valid row and are masked, so none is conditional);
+//   * q . k runs on fp16 pairs with v_dot2_f32_f16 (fp32 accumulate) and the
+//     D/8 lanes of a key finish the dot with DPP row operations (quad_perm,
+//     row_half_mirror, row_mirror): no LDS traffic; scores go to LDS;
+//   * the softmax statistics of all G heads are reduced together (wave
+//     butterflies, one LDS exchange);
+//   * P . V keeps the row mapping, each lane accumulating its 8 output dims
+//     for the G heads; key slots are folded with xor shuffles inside the wave
+//     and across the 8 waves through LDS.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "device.hpp"
+#include "redline_amd/rlk.h"
+#include "status.hpp"
+
+namespace rlk {
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kPart = RLK_DECODE_PARTITION_SIZE;  // keys per partition
+
+struct AttnArgs {
+  rlk_attention_params p;
+  rlk_decode_attention_work w;
+
+};
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+template <bool kInt8>
+struct Row;
+
+template <>
+struct Row<false> {  // 8 fp16 elements, 16 bytes
+  using Raw = u32x4;
+  __device__ static Raw load(const void* base, int64_t cell, int D, int e0) {
+    return ld16<true>(reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + cell * D + e0));
+  }
+  __device__ static f16x8v halves(Raw r) { return __builtin_bit_cast(f16x8v, r); }
+  __device__ static f32x8 floats(Raw r) { return unpack8(r); }
+};
+
+template <>
+struct Row<true> {  // 8 int8 codes, 8 bytes
+  using Raw = u32x2;
+  __device__ static Raw load(const void* base, int64_t cell, int D, int e0) {
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(base) + cell * D + e0));
+  }
+  // |code| <= 127 is exact in fp16
+  __device__ static f16x8v halves(Raw r) {
+    return __builtin_convertvector(__builtin_bit_cast(i8x8, r), f16x8v);
+  }
+  __device__ static f32x8 floats(Raw r) {
+    return __builtin_convertvector(__builtin_bit_cast(i8x8, r), f32x8);
+  }
+};
+
+// v + the value of the lane picked by DPP control CTRL (within 16-lane rows).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                           0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N (8 or 16) lanes, every lane receiving it: four
+// (three) DPP-modified adds, no LDS traffic.
+template <int N>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]: pairs
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]: quads
+  v = dpp_add<0x141>(v);  // row_half_mirror: groups of 8
+  if constexpr (N == 16) v = dpp_add<0x140>(v);  // row_mirror: groups of 16
+  return v;
+}
+
+// One workgroup = one (item, kv head, 256-key partition), 8 waves.  Each
+// wave owns kPasses passes of kKPP keys; all of its K and V rows are
+// requested before the first is used, so a workgroup keeps its whole
+// partition (256 keys x 2 rows) in flight at once.
+template <int D, int G, bool kInt8>
+__global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_kernel(AttnArgs args) {
+  constexpr int kLPK = D / 8;             // lanes per key row (16 or 8)
+  constexpr int kKPP = kWave / kLPK;      // keys per wave pass
+  constexpr int kKPB = kKPP * kWaves;     // keys per workgroup pass
+  constexpr int kPasses = kPart / kKPB;   // passes over a full partition (8 or 4)
+  using R = Row<kInt8>;
+  const rlk_attention_params& p = args.p;
+  const rlk_decode_attention_work& w = args.w;
+
+  __shared__ float scores[G][kPart];
+  __shared__ float red[kWaves][G][D];
+  __shared__ float stat[kWaves][G];
+  __shared__ int cell_s[kPart];  // cache cell of each key of the partition
+
+  const int part = blockIdx.x, kvh = blockIdx.y, item = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int token = w.item_token[item];
+  const int seq = w.item_seq[item];
+  const int ctx = p.positions[token] + 1;
+  const int num_parts = (ctx + kPart - 1) / kPart;
+  if (part >= num_parts) return;  // uniform over the workgroup
+  const int start = part * kPart;
+  const int n = min(kPart, ctx - start);
+  const int slot = lane / kLPK;         // key slot of this lane within a wave pass
+  const int e0 = (lane % kLPK) * 8;     // first element of the row owned by this lane
+
+  // Resolve every key of the partition to its cache cell once (one block-
+  // table lookup and division per key instead of one per key and pass); the
+  // K/V addresses below are then one LDS read each.  Table rows are padded
+  // with block 0, so every entry read inside the row is valid.
+  {
+    const int bs = p.kv.block_size;
+    const int pos = start + tid;
+    const int bi = pos / bs;
+    if (tid < kPart && bi < p.max_blocks_per_seq) {
+      const int blk = p.block_tables[static_cast<int64_t>(seq) * p.max_blocks_per_seq + bi];
+      cell_s[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - bi * bs);
+    }
+  }
+  // q of the G heads, this lane's 8 elements, kept in fp16 pairs for
+  // v_dot2_f32_f16 (the softmax scale is applied to the fp32 dot).
+  f16x8v q[G];
+  {
+    const _Float16* qrow = reinterpret_cast<const _Float16*>(p.q) +
+                           static_cast<int64_t>(token) * p.q_stride + (kvh * G) * D + e0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) q[g] = __builtin_bit_cast(f16x8v, load16(qrow + g * D));
+  }
+  __syncthreads();
+
+  // Key j of pass u for this lane; slots past the context re-read the last
+  // valid row (a cache hit) and are masked out of the results, which keeps
+  // every load unconditional.
+  auto key_of = [&](int pass) { return (pass * kWaves + wave) * kKPP + slot; };
+  auto cell_of = [&](int j) -> int64_t { return cell_s[min(j, n - 1)]; };
+
+  // ---- all K and V rows of this wave in flight at once
+  typename R::Raw kr[kPasses], vr[kPasses];
+  float ksc[kPasses], vsc[kPasses];
+#pragma unroll
+  for (int u = 0; u < kPasses; ++u) {
+    const int64_t cell = cell_of(key_of(u));
+    kr[u] = R::load(p.kv.k, cell, D, e0);
+    vr[u] = R::load(p.kv.v, cell, D, e0);
+    ksc[u] = kInt8 ? p.kv.k_scale[cell] : 1.f;
+    vsc[u] = kInt8 ? p.kv.v_scale[cell] : 1.f;
+  }
+  // Keep the scheduler from consuming a row right after its own load (which
+  // would wait for each load in turn) and from converting V rows early.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- phase 1: scores[g][j] = scale * (q_g . k_j) * k_scale_j
+#pragma unroll
+  for (int u = 0; u < kPasses; ++u) {
+    const f16x8v k = R::halves(kr[u]);
+    const int j = key_of(u);
+    float dot[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d2 = 0.f;
+#pragma unroll
+      for (int x = 0; x < 8; x += 2) {
+        const f16x2 a = {q[g][x], q[g][x + 1]};
+        const f16x2 b = {k[x], k[x + 1]};
+        d2 = __builtin_amdgcn_fdot2(a, b, d2, false);
+      }
+      dot[g] = group_sum_dpp<kLPK>(d2);
+    }
+    if (j < n && lane % kLPK == 0) {
+      const float sc = p.scale * ksc[u];
+#pragma unroll
+      for (int g = 0; g < G; ++g) scores[g][j] = dot[g] * sc;
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax statistics per head: thread t < 256 owns key t
+  float m[G], l[G];
+  {
+    float sv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      sv[g] = tid < n ? scores[g][tid] : -FLT_MAX;
+      float v = sv[g];
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+      if (lane == 0) stat[wave][g] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float v = stat[0][g];
+#pragma unroll
+      for (int ww = 1; ww < kWaves; ++ww) v = fmaxf(v, stat[ww][g]);
+      m[g] = v;
+    }
+    __syncthreads();  // stat is reused below
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float e = tid < n ? __expf(sv[g] - m[g]) : 0.f;
+      if (tid < n) scores[g][tid] = e;
+      float v = e;
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+      if (lane == 0) stat[wave][g] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float v = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) v += stat[ww][g];
+      l[g] = v;
+    }
+  }
+
+  // ---- phase 2: o[g][e0..e0+7] += p_gj * v_scale_j * v_j
+  f32x8 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < kPasses; ++u) {
+    const int j = key_of(u);
+    const float live = j < n ? vsc[u] : 0.f;
+    const f32x8 v = R::floats(vr[u]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] += (scores[g][min(j, n - 1)] * live) * v;
+  }
+  // fold the key slots of the wave (lanes e0-equal, slot-different)
+#pragma unroll
+  for (int o = kLPK; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[g][x] += __shfl_xor(acc[g][x], o, kWave);
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int x = 0; x < 8; ++x) red[wave][g][e0 + x] = acc[g][x];
+  }
+  __syncthreads();
+
+  for (int i = tid; i < G * D; i += kThreads) {
+    const int g = i / D, d = i % D;
+    float o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) o += red[ww][g][d];
+    o /= l[g];
+    const int h = kvh * G + g;
+    if (num_parts == 1) {
+      reinterpret_cast<_Float16*>(p.out)[static_cast<int64_t>(token) * p.num_heads * D + h * D + d] =
+          static_cast<_Float16>(o);
+    } else {
+      const int64_t row = (static_cast<int64_t>(item) * p.num_heads + h) * w.max_partitions + part;
+      w.ws_out[row * D + d] = o;
+      if (d == 0) {
+        w.ws_max[row] = m[g];
+        w.ws_sum[row] = l[g];
+      }
+    }
+  }
+}
+
+// Merges the split-K partials of one (item, head): one lane per output dim
+// (the merge rule of attention.cu:193-210).  Weight of partition i:
+// exp(m_i - max_j m_j) * l_i.
+template <int D>
+__global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
+  const rlk_attention_params& p = args.p;
+  const rlk_decode_attention_work& w = args.w;
+  const int item = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int token = w.item_token[item];
+  const int ctx = p.positions[token] + 1;
+  const int num_parts = (ctx + kPart - 1) / kPart;
+  if (num_parts <= 1) return;
+  const int64_t base = (static_cast<int64_t>(item) * p.num_heads + h) * w.max_partitions;
+  float mx = -FLT_MAX;
+  for (int i = 0; i < num_parts; ++i) mx = fmaxf(mx, w.ws_max[base + i]);
+  float total = 0.f, o = 0.f;
+  for (int i = 0; i < num_parts; ++i) {
+    const float wgt = __expf(w.ws_max[base + i] - mx) * w.ws_sum[base + i];
+    total += wgt;
+    o += wgt * w.ws_out[(base + i) * D + d];
+  }
+  reinterpret_cast<_Float16*>(p.out)[static_cast<int64_t>(token) * p.num_heads * D + h * D + d] =
+      static_cast<_Float16>(o / total);
+}
+
+template <int D, int G>
+void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
+  const dim3 grid(a.w.max_partitions, a.p.kv.num_kv_heads, a.w.num_items);
+  if (int8) {
+    decode_attention_kernel<D, G, true><<<grid, kThreads, 0, stream>>>(a);
+  } else {
+    decode_attention_kernel<D, G, false><<<grid, kThreads, 0, stream>>>(a);
+  }
+}
+
+template <int D>
+bool launch_d(const AttnArgs& a, int G, bool int8, hipStream_t stream) {
+  switch (G) {
+    case 1: launch_g<D, 1>(a, int8, stream); break;
+    case 2: launch_g<D, 2>(a, int8, stream); break;
+    case 3: launch_g<D, 3>(a, int8, stream); break;
+    case 4: launch_g<D, 4>(a, int8, stream); break;
+    case 5: launch_g<D, 5>(a, int8, stream); break;
+    case 6: launch_g<D, 6>(a, int8, stream); break;
+    case 7: launch_g<D, 7>(a, int8, stream); break;
+    case 8: launch_g<D, 8>(a, int8, stream); break;
+    default: return false;
+  }
+  if (a.w.max_partitions > 1)
+    decode_reduce_kernel<D><<<dim3(a.w.num_items, a.p.num_heads), D, 0, stream>>>(a);
+  return true;
+}
+
+}  // namespace
+}  // namespace rlk
+
+using namespace rlk;
+
+extern "C" int rlk_paged_attention_decode(const rlk_attention_params* p,
+                                          const rlk_decode_attention_work* w,
+                                          hipStream_t stream) {
+  if (p == nullptr || w == nullptr)
+    return fail(RLK_EINVAL, "paged_attention_decode: null params or work");
+  if (w->num_items <= 0) return RLK_OK;
+  const int hkv = p->kv.num_kv_heads;
+  if (hkv <= 0 || p->num_heads <= 0 || p->num_heads % hkv != 0)
+    return fail(RLK_EINVAL, "num_heads must be a multiple of num_kv_heads (%d, %d)", p->num_heads,
+                hkv);
+  if (p->kv.head_dim != 64 && p->kv.head_dim != 128)
+    return fail(RLK_EUNSUPPORTED, "unsupported head_dim %d", p->kv.head_dim);
+  if (p->kv.dtype != RLK_KV_FP16 && p->kv.dtype != RLK_KV_INT8)
+    return fail(RLK_EINVAL, "paged_attention_decode: unknown KV dtype %d", p->kv.dtype);
+  if (w->num_items > 65535 || p->kv.num_kv_heads > 65535)
+    return fail(RLK_EINVAL, "paged_attention_decode: %d items exceed one launch; split the call",
+                w->num_items);
+  if (w->max_partitions < 1 || p->kv.block_size <= 0)
+    return fail(RLK_EINVAL, "paged_attention_decode: bad max_partitions %d or block size %d",
+                w->max_partitions, p->kv.block_size);
+  if (w->max_partitions > 1 && (w->ws_out == nullptr || w->ws_max == nullptr || w->ws_sum == nullptr))
+    return fail(RLK_EINVAL, "paged_attention_decode: split-K workspace is required when "
+                            "max_partitions > 1");
+  AttnArgs a;
+  a.p = *p;
+  a.w = *w;
+  const int G = p->num_heads / hkv;
+  const bool int8 = p->kv.dtype == RLK_KV_INT8;
+  const bool ok = p->kv.head_dim == 128 ? launch_d<128>(a, G, int8, stream)
+                                        : launch_d<64>(a, G, int8, stream);
+  if (!ok) return fail(RLK_EUNSUPPORTED, "unsupported GQA group size %d", G);
+  return launch_status("paged_attention_decode");
+}

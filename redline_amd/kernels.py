@@ -19,8 +19,11 @@ from ._lib import KVLayerView, check, lib
 __all__ = [
     "embedding_lookup", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
     "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
-    "KVCache", "SCALE_F32", "SCALE_F16",
+    "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "attention_params",
+    "decode_work", "DecodeWorkspace", "kDecodePartitionSize",
 ]
+
+kDecodePartitionSize = _lib.RLK_DECODE_PARTITION_SIZE
 
 SCALE_F32 = _lib.RLK_SCALE_F32
 SCALE_F16 = _lib.RLK_SCALE_F16
@@ -140,6 +143,43 @@ def rope_and_write_kv_ex(qkv, positions, slot_mapping, num_tokens, num_heads, co
         _ptr(slot_mapping, torch.int32, "slot_mapping"), num_tokens, num_heads,
         _ptr(cos_table, torch.float32, "cos_table"), _ptr(sin_table, torch.float32, "sin_table"),
         C.byref(kv), C.byref(opt), _stream(stream)))
+
+
+def attention_params(q, q_stride, out, num_heads, scale, kv: KVLayerView, block_tables,
+                     max_blocks_per_seq, positions) -> _lib.AttentionParams:
+    """kernels::AttentionParams from torch tensors (q may be a view into qkv)."""
+    return _lib.AttentionParams(
+        _ptr(q, torch.float16, "q"), q_stride, _ptr(out, torch.float16, "out"), num_heads,
+        float(scale), kv, _ptr(block_tables, torch.int32, "block_tables"), max_blocks_per_seq,
+        _ptr(positions, torch.int32, "positions"))
+
+
+def decode_work(item_token, item_seq, num_items, max_partitions, workspace=None):
+    """kernels::DecodeAttentionWork; `workspace` is a DecodeWorkspace (needed
+    when max_partitions > 1)."""
+    ws = workspace
+    return _lib.DecodeAttentionWork(
+        _ptr(item_token, torch.int32, "item_token"), _ptr(item_seq, torch.int32, "item_seq"),
+        num_items, max_partitions,
+        None if ws is None else ws.out.data_ptr(), None if ws is None else ws.max.data_ptr(),
+        None if ws is None else ws.sum.data_ptr())
+
+
+class DecodeWorkspace:
+    """Split-K partials of the decode attention, sized like the reference
+    model's workspace (src/cuda/model/llama.cpp:37-40)."""
+
+    def __init__(self, max_items, num_heads, max_partitions, head_dim, device="cuda"):
+        rows = max_items * num_heads * max_partitions
+        self.out = torch.empty(rows * head_dim, dtype=torch.float32, device=device)
+        self.max = torch.empty(rows, dtype=torch.float32, device=device)
+        self.sum = torch.empty(rows, dtype=torch.float32, device=device)
+
+
+def paged_attention_decode(params: _lib.AttentionParams, work: _lib.DecodeAttentionWork,
+                           stream=None):
+    """Flash-decoding paged attention (kernels::paged_attention_decode)."""
+    check(lib().rlk_paged_attention_decode(C.byref(params), C.byref(work), _stream(stream)))
 
 
 class KVCache:

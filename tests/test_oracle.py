@@ -350,3 +350,111 @@ def test_rope_fp16_scale_extension():
         far = np.abs(np.abs(r - np.floor(r)) - 0.5) > 1e-4
         assert np.array_equal(q[far], np.clip(np.rint(r[far]), -127, 127))
         assert np.max(np.abs(q - c8f[blk, :, off])) <= 1
+
+
+# ------------------------------------------------------- paged decode attention
+
+def _attn_case(rng, lens, hq, hkv, D, bs=16, int8=False):
+    """Random paged caches for sequences of the given context lengths; one
+    decode item per sequence at its last position."""
+    nblk = 1 + sum((L + bs - 1) // bs for L in lens)
+    ids = rng.permutation(np.arange(1, nblk)).astype(np.int32)
+    maxb = max((L + bs - 1) // bs for L in lens)
+    tables = np.zeros((len(lens), maxb), np.int32)
+    nxt = 0
+    for i, L in enumerate(lens):
+        nb = (L + bs - 1) // bs
+        tables[i, :nb] = ids[nxt:nxt + nb]
+        nxt += nb
+    shape = (nblk, hkv, bs, D)
+    if int8:
+        kc = rng.integers(-127, 128, shape).astype(np.int8)
+        vc = rng.integers(-127, 128, shape).astype(np.int8)
+        ks = (rng.random(shape[:3]) * 0.02 + 0.001).astype(np.float32)
+        vs = (rng.random(shape[:3]) * 0.02 + 0.001).astype(np.float32)
+    else:
+        kc, vc = randn_f16(rng, shape), randn_f16(rng, shape)
+        ks = vs = None
+    T = len(lens)
+    q = randn_f16(rng, (T, hq * D))
+    pos = np.array([L - 1 for L in lens], np.int32)
+    return q, kc, vc, ks, vs, tables, pos
+
+
+def _dequant(c, s):
+    return c.astype(np.float64) if s is None else c.astype(np.float64) * s[..., None]
+
+
+def _attn_numpy(q, kc, vc, ks, vs, tables, pos, hq, hkv, D, scale, bs=16):
+    from scipy.special import softmax
+    G = hq // hkv
+    K, V = _dequant(kc, ks), _dequant(vc, vs)
+    out = np.zeros((len(pos), hq * D))
+    for i, p_ in enumerate(pos):
+        js = np.arange(p_ + 1)
+        blk = tables[i, js // bs]
+        for h in range(hq):
+            k = K[blk, h // G, js % bs]
+            v = V[blk, h // G, js % bs]
+            s = (q[i, h * D:(h + 1) * D].astype(np.float64) * np.float64(np.float32(scale))) @ k.T
+            out[i, h * D:(h + 1) * D] = softmax(s) @ v
+    return out
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_attention_against_scipy_softmax(int8):
+    rng = np.random.default_rng(20)
+    hq, hkv, D = 8, 2, 64
+    lens = [1, 37, 300, 16]
+    q, kc, vc, ks, vs, tables, pos = _attn_case(rng, lens, hq, hkv, D, int8=int8)
+    scale = 1 / np.sqrt(D)
+    got = oracle.paged_attention_decode(q, hq * D, hq, scale, kc, vc, ks, vs, tables, pos,
+                                        np.arange(4), np.arange(4), 4, int8)
+    want = _attn_numpy(q, kc, vc, ks, vs, tables, pos, hq, hkv, D, scale)
+    m = safe(want)
+    assert np.array_equal(got[m], to16(want)[m])
+
+
+def test_attention_closed_forms_and_paging_invariance():
+    rng = np.random.default_rng(21)
+    hq, hkv, D = 4, 1, 128
+    q, kc, vc, ks, vs, tables, pos = _attn_case(rng, [50, 200], hq, hkv, D)
+    # q = 0: uniform weights, the output is the mean of the V rows
+    z = np.zeros_like(q)
+    out = oracle.paged_attention_decode(z, hq * D, hq, 0.1, kc, vc, None, None, tables, pos,
+                                        np.arange(2), np.arange(2), 2)
+    for i, L in enumerate([50, 200]):
+        js = np.arange(L)
+        mean = vc[tables[i, js // 16], 0, js % 16].astype(np.float64).mean(0)
+        for h in range(hq):
+            assert np.array_equal(out[i, h * D:(h + 1) * D], to16(mean))
+    # a key aligned with q and a large scale: the output is that key's V row
+    k_pos = 33
+    blk, off = tables[1, k_pos // 16], k_pos % 16
+    kc2 = kc.copy()
+    kc2[blk, 0, off] = q[1, :D]
+    out = oracle.paged_attention_decode(q, hq * D, hq, 50.0, kc2, vc, None, None, tables, pos,
+                                        np.arange(2), np.arange(2), 2)
+    assert np.array_equal(out[1, :D], vc[blk, 0, off])
+    # moving every block to another physical slot (and fixing the tables)
+    # leaves the result unchanged
+    perm = rng.permutation(kc.shape[0])
+    inv = np.argsort(perm)
+    a = oracle.paged_attention_decode(q, hq * D, hq, 0.09, kc, vc, None, None, tables, pos,
+                                      np.arange(2), np.arange(2), 2)
+    b = oracle.paged_attention_decode(q, hq * D, hq, 0.09, kc[perm], vc[perm], None, None,
+                                      inv[tables].astype(np.int32), pos, np.arange(2),
+                                      np.arange(2), 2)
+    assert np.array_equal(a, b)
+
+
+def test_attention_int8_equals_dequantised_fp64():
+    """INT8 attention equals the attention of the dequantised cache (codes x scale)."""
+    rng = np.random.default_rng(22)
+    hq, hkv, D = 4, 2, 64
+    q, kc, vc, ks, vs, tables, pos = _attn_case(rng, [90], hq, hkv, D, int8=True)
+    got = oracle.paged_attention_decode(q, hq * D, hq, 0.125, kc, vc, ks, vs, tables, pos,
+                                        np.arange(1), np.arange(1), 1, True)
+    want = _attn_numpy(q, kc, vc, ks, vs, tables, pos, hq, hkv, D, 0.125)
+    m = safe(want)
+    assert m.mean() > 0.98 and np.array_equal(got[m], to16(want)[m])

@@ -327,9 +327,12 @@ def test_rope_extension_null_options_is_plain(torch_cuda):
     outs = []
     for use_ex in (False, True):
         cache = K.KVCache(1, 2, hkv, D)
-        d = dev(torch, qkv)
-        args = (d.data_ptr(), dev(torch, pos).data_ptr(), dev(torch, slots).data_ptr(), 5, hq,
-                dev(torch, cos).data_ptr(), dev(torch, sin).data_ptr(), C.byref(cache.layer(0)))
+        # keep every device tensor referenced until the kernel has run (a
+        # temporary freed after .data_ptr() can be handed to the next one)
+        d, d_pos, d_slots = dev(torch, qkv), dev(torch, pos), dev(torch, slots)
+        d_cos, d_sin = dev(torch, cos), dev(torch, sin)
+        args = (d.data_ptr(), d_pos.data_ptr(), d_slots.data_ptr(), 5, hq, d_cos.data_ptr(),
+                d_sin.data_ptr(), C.byref(cache.layer(0)))
         stream = torch.cuda.current_stream().cuda_stream
         st = (_lib.lib().rlk_rope_and_write_kv_ex(*args, None, stream) if use_ex
               else _lib.lib().rlk_rope_and_write_kv(*args, stream))
