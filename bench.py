@@ -284,6 +284,57 @@ def attention_bench(torch, K, w, int8, reps, rotations=3, seed=0, eager_calls=0)
             "bytes_per_call": int(nbytes / rotations)}
 
 
+def gemv_bytes(m, n, k, g):
+    """Algorithmic bytes of one INT4 GEMV with SwiGLU epilogue: codes, fp16
+    scales and offsets, activations read once, fp16 [m, n/2] written."""
+    return n * k // 2 + 2 * n * (k // g) * 2 + m * k * 2 + m * (n // 2) * 2
+
+
+def gemv_bench(torch, K, m, reps, n=2 * 14336, k=4096, g=128, unfused=True, eager_calls=0):
+    """INT4 gate_up projection of Llama-3.1-8B (rows interleaved) at decode
+    batch m with the fused SwiGLU epilogue, rotating over enough weight sets to
+    exceed 2x the Infinity Cache; with `unfused`, also the reference's path for
+    a weight without the fused epilogue: GEMV to fp16 [m, n] + silu_and_mul_interleaved."""
+    nb = gemv_bytes(m, n, k, g)
+    R = max(2, -(-(640 << 20) // nb))
+    gen = torch.Generator(device="cuda").manual_seed(m)
+    sets = []
+    for _ in range(R):
+        w = torch.randint(0, 256, (n, k // 2), generator=gen, device="cuda", dtype=torch.uint8)
+        sc = (torch.rand((n, k // g), generator=gen, device="cuda") * 0.016 + 0.004).half()
+        of = (-7.5 * sc.float()).half()
+        x = torch.randn((m, k), generator=gen, device="cuda").half()
+        sets.append((x, w, sc, of, torch.empty((m, n // 2), dtype=torch.float16, device="cuda")))
+    fused = lambda c: K.gemv_w4a16_swiglu(c[0], m, c[1], c[2], c[3], g, n, k, c[4])  # noqa: E731
+    if eager_calls:
+        for i in range(eager_calls):
+            fused(sets[i % R])
+        torch.cuda.synchronize()
+        return None
+    gph = capture(torch, lambda: [fused(c) for c in sets])
+    ms = time_graph(torch, gph, reps) / R
+    del gph
+    gbs = nb / (ms * 1e-3) / 1e9
+    out = {"m": m, "n": n, "k": k, "group_size": g, "us_per_call": round(ms * 1e3, 3),
+           "gb_per_s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "bytes_per_call": nb, "rotating_input_sets": R}
+    msg = f"  gemv_w4a16_swiglu m={m:2d}: {ms * 1e3:8.2f} us {gbs:8.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:5.1f}%)"
+    if unfused:
+        scratch = torch.empty((m, n), dtype=torch.float16, device="cuda")
+
+        def two(c):
+            K.gemv_w4a16(c[0], m, c[1], c[2], c[3], g, None, n, k, scratch)
+            K.silu_and_mul_interleaved(scratch, m, n // 2, c[4])
+        gph = capture(torch, lambda: [two(c) for c in sets])
+        ms2 = time_graph(torch, gph, reps) / R
+        del gph
+        out["unfused_us_per_call"] = round(ms2 * 1e3, 3)
+        msg += f"; unfused gemv + silu_and_mul_interleaved {ms2 * 1e3:8.2f} us"
+    log(msg)
+    del sets
+    return out
+
+
 def cpu_baseline(torch, data, seconds=10.0):
     """The CPU oracle (oracle/oracle.c, single thread) on the same step:
     a bounded number of full steps over one input set, copied to host."""
@@ -336,6 +387,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3-C5 per-kernel figures")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention figures")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the INT4 GEMV + SwiGLU figures")
     ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--rotations", type=int, default=None,
@@ -358,6 +410,18 @@ def main():
     from redline_amd.configs import make_workload
     torch.cuda.set_device(0)
 
+    if args.only == "gemv_w4a16_swiglu" and not args.profile_calls:
+        res = []
+        for m in (1, 8, 16, 32):
+            for cfg in (range(8) if args.sweep else [None]):
+                if cfg is not None:
+                    os.environ["RLK_TUNE_W4_CFG"] = str(cfg)
+                r = gemv_bench(torch, K, m, args.reps, unfused=not args.sweep)
+                r["cfg"] = cfg
+                print(json.dumps(r), flush=True)
+                res.append(r)
+        return
+
     w = make_workload(args.workload)
     log(f"setting up {w.key} ({w.model.name}, T={w.num_tokens})")
     data = LayerData(torch, K, w, rotations=args.rotations)
@@ -379,6 +443,9 @@ def main():
         if args.only in (None, "paged_attention_decode"):
             for int8 in (False, True):
                 attention_bench(torch, K, w, int8, 0, eager_calls=args.profile_calls)
+        if args.only in (None, "gemv_w4a16_swiglu"):
+            for m in (1, 8, 16, 32):
+                gemv_bench(torch, K, m, 0, eager_calls=args.profile_calls)
         src = torch.empty(128 << 20, dtype=torch.float16, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(args.profile_calls):
@@ -442,6 +509,12 @@ def main():
             del dx
             torch.cuda.empty_cache()
 
+    gemv = []
+    if not args.no_gemv:
+        for m in (1, 8, 16, 32):
+            gemv.append(gemv_bench(torch, K, m, args.reps))
+            torch.cuda.empty_cache()
+
     attention = {}
     if not args.no_attention:
         for int8 in (False, True):
@@ -476,6 +549,7 @@ def main():
         "kernels": kern,
         "prefill": extra,
         "decode_attention": attention,
+        "gemv_w4a16_swiglu": gemv,
         "copy_baseline_gb_per_s": copy,
         "launch_floor_us": floor,
     }

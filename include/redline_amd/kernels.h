@@ -157,5 +157,27 @@ inline void paged_attention_decode(const AttentionParams& p, const DecodeAttenti
                                            stream));
 }
 
+// INT4 weight-only GEMV (kernels.h:156-171 of the reference).  The reference
+// serves m <= kGemvW4MaxM = 16 per launch; this library serves up to
+// kGemvW4MaxM here (32) in one launch.
+constexpr int kGemvW4MaxM = RLK_GEMV_W4_MAX_M;
+
+inline void gemv_w4a16(const half* x, int m, const uint8_t* w, const half* scales,
+                       const half* offsets, int group_size, const half* bias, int n, int k, void* y,
+                       bool y_fp32, hipStream_t stream) {
+  detail::check(rlk_gemv_w4a16(detail::bits(x), m, w, detail::bits(scales), detail::bits(offsets),
+                               group_size, detail::bits(bias), n, k, y, y_fp32 ? 1 : 0, stream));
+}
+
+// Same kernel for a [gate; up] weight whose rows are interleaved (gate_i, up_i):
+// writes silu(gate) * up, fp16 [m, n / 2], from the GEMV epilogue.
+inline void gemv_w4a16_swiglu(const half* x, int m, const uint8_t* w, const half* scales,
+                              const half* offsets, int group_size, int n, int k, half* y,
+                              hipStream_t stream) {
+  detail::check(rlk_gemv_w4a16_swiglu(detail::bits(x), m, w, detail::bits(scales),
+                                      detail::bits(offsets), group_size, n, k, detail::bits(y),
+                                      stream));
+}
+
 }  // namespace kernels
 }  // namespace redline

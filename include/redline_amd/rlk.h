@@ -86,6 +86,32 @@ int rlk_silu_and_mul(const uint16_t* gate_up, int rows, int inter, uint16_t* out
 int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, uint16_t* out,
                                  hipStream_t stream);
 
+/* ---------------------------------------------- INT4 weight-only GEMV (decode)
+ *
+ * y[m, n] = x[m, k] . W[n, k]^T (+ bias[n]) with W group-quantised INT4:
+ *   W[r][c] = q * scales[r][c / g] + offsets[r][c / g],
+ *   q = code c of row r: byte c / 2 of the row, low nibble for even c.
+ * w is [n, k/2] bytes; scales and offsets fp16 [n, k/g]; x fp16 [m, k].
+ * m <= 0: no-op.  m > RLK_GEMV_W4_MAX_M: RLK_EUNSUPPORTED (the reference
+ * serves m <= 16, kernels.h:161; this build serves m <= 32 in one launch).
+ * k and group_size multiples of 32 with k % group_size == 0, else RLK_EINVAL;
+ * x and w 16-byte aligned. */
+#define RLK_GEMV_W4_MAX_M 32
+
+/* y fp16 [m, n], or fp32 when y_fp32 != 0; bias fp16 [n] or NULL.
+ * Replaces kernels::gemv_w4a16, gemv_weight_only.cu:222-232 (kernels.h:164-168). */
+int rlk_gemv_w4a16(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
+                   const uint16_t* offsets, int group_size, const uint16_t* bias, int n, int k,
+                   void* y, int y_fp32, hipStream_t stream);
+
+/* SwiGLU in the GEMV epilogue: rows (2i, 2i + 1) of w are (gate_i, up_i), the
+ * loader's INT4 gate_up layout (weights.cpp:157-167); y fp16 [m, n/2] =
+ * fp16(fp16(silu(fp16(gate))) * fp16(up)).  n must be even.
+ * Replaces kernels::gemv_w4a16_swiglu, gemv_weight_only.cu:234-241 (kernels.h:169-171). */
+int rlk_gemv_w4a16_swiglu(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
+                          const uint16_t* offsets, int group_size, int n, int k, uint16_t* y,
+                          hipStream_t stream);
+
 /* dst[i, :] = src[idx[i], :].  Replaces kernels::gather_rows,
  * elementwise.cu:147-153.  n <= 0: no-op.  cols % 8 != 0: RLK_EINVAL. */
 int rlk_gather_rows(const uint16_t* src, const int32_t* idx, int n, int cols, uint16_t* dst,

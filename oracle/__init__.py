@@ -51,6 +51,8 @@ def lib() -> C.CDLL:
                                                _P, _I, _I, _P, _I]
         L.orc_paged_attention_decode.argtypes = [_P, _I, _P, _I, C.c_float, _P, _P, _P, _P, _I,
                                                  _I, _I, _I, _P, _I, _P, _P, _P, _I]
+        L.orc_gemv_w4a16.argtypes = [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P]
+        L.orc_gemv_w4a16_swiglu.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P]
         L.orc_layer_step.argtypes = [_P, _P, _I, _I, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P,
                                      _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P]
         _o = L
@@ -152,6 +154,31 @@ def silu_and_mul(gate_up, inter, interleaved=False):
     out = np.empty((rows, inter), np.uint16)
     fn = lib().orc_silu_and_mul_interleaved if interleaved else lib().orc_silu_and_mul
     fn(p(gu), rows, inter, p(out))
+    return out.view(np.float16)
+
+
+def gemv_w4a16(x, w, scales, offsets, group_size, bias=None):
+    """float64 y [m, n] of x [m, k] fp16 times the group-dequantised INT4 W [n, k/2]."""
+    x = _u16(x)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, np.uint8)
+    n = w.shape[0]
+    assert w.shape[1] * 2 == k
+    y = np.empty((m, n), np.float64)
+    lib().orc_gemv_w4a16(p(x), m, p(w), p(_u16(scales)), p(_u16(offsets)), group_size,
+                         p(None if bias is None else _u16(bias)), n, k, p(y))
+    return y
+
+
+def gemv_w4a16_swiglu(x, w, scales, offsets, group_size):
+    """fp16 [m, n/2]: SwiGLU of the interleaved (gate, up) rows of the INT4 GEMV."""
+    x = _u16(x)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, np.uint8)
+    n = w.shape[0]
+    out = np.empty((m, n // 2), np.uint16)
+    lib().orc_gemv_w4a16_swiglu(p(x), m, p(w), p(_u16(scales)), p(_u16(offsets)), group_size, n,
+                                k, p(out))
     return out.view(np.float16)
 
 

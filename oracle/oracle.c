@@ -31,6 +31,12 @@
  *                              gathered cache, q = 0 -> mean of V, a dominant key
  *                              -> its V, invariance under physical block moves,
  *                              INT8 == FP16 path on the dequantised cache.
+ *   orc_gemv_w4a16(_swiglu)    numpy float64 matmul against a weight matrix built
+ *                              first and then packed (nibble order KAT from
+ *                              tests/cuda/test_gemm.cu:40-45), q = 0 -> offset
+ *                              * sum(x), one-hot x -> the dequantised column,
+ *                              SwiGLU == orc_silu_and_mul_interleaved of the
+ *                              fp16-rounded GEMV output.
  *   orc_rope_and_write_kv      pos 0 identity, V passthrough, rotation by angle
  *                              against float64 rotation matrix, norm
  *                              preservation, slot/cell address KATs from
@@ -188,6 +194,56 @@ void orc_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, 
     for (int i = 0; i < inter; ++i)
       out[(size_t)r * inter + i] = swiglu1(orc_h2f(g[2 * i]), orc_h2f(g[2 * i + 1]));
   }
+}
+
+/* ------------------------------------------------------ INT4 weight-only GEMV */
+
+/* y[m, n] = x[m, k] . W[n, k]^T (+ bias) with W dequantised group-wise:
+ *   W[r][c] = q * scale[r][c / g] + offset[r][c / g],  q = nibble c of row r,
+ * nibble c held in byte c / 2 of the row, low nibble for even c
+ * (gemv_weight_only.cu:103-160, packing tests/cuda/test_gemm.cu:40-45,
+ * python/redline/quantize.py:4,84-86).  The reference evaluates the group sum as
+ * s * sum(x q) + o * sum(x) in fp32; here every product and sum is float64, so
+ * y is the exact value the kernels approximate. */
+void orc_gemv_w4a16(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
+                    const uint16_t* offsets, int group_size, const uint16_t* bias, int n, int k,
+                    double* y) {
+  const int groups = k / group_size;
+  double* xs = (double*)malloc(sizeof(double) * (size_t)k);
+  for (int i = 0; i < m; ++i) {
+    for (int c = 0; c < k; ++c) xs[c] = orc_h2f(x[(size_t)i * k + c]);
+    for (int r = 0; r < n; ++r) {
+      const uint8_t* row = w + (size_t)r * (k / 2);
+      double acc = bias ? orc_h2f(bias[r]) : 0.0;
+      for (int gi = 0; gi < groups; ++gi) {
+        const double s = orc_h2f(scales[(size_t)r * groups + gi]);
+        const double o = orc_h2f(offsets[(size_t)r * groups + gi]);
+        for (int c = gi * group_size; c < (gi + 1) * group_size; ++c) {
+          const int q = (c & 1) ? (row[c / 2] >> 4) : (row[c / 2] & 15);
+          acc += xs[c] * (q * s + o);
+        }
+      }
+      y[(size_t)i * n + r] = acc;
+    }
+  }
+  free(xs);
+}
+
+/* The SwiGLU epilogue over interleaved (gate_i, up_i) rows 2i, 2i + 1, fp16
+ * out [m, n / 2], with the rounding points of the unfused path: gate and up
+ * rounded to fp16 as GEMM outputs, then silu rounded, then the product
+ * (gemv_weight_only.cu:46-63, row interleave weights.cpp:157-167). */
+void orc_gemv_w4a16_swiglu(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
+                           const uint16_t* offsets, int group_size, int n, int k, uint16_t* y) {
+  double* acc = (double*)malloc(sizeof(double) * (size_t)m * n);
+  orc_gemv_w4a16(x, m, w, scales, offsets, group_size, NULL, n, k, acc);
+  for (int i = 0; i < m; ++i)
+    for (int j = 0; j < n / 2; ++j) {
+      const float g = rnd16((float)acc[(size_t)i * n + 2 * j]);
+      const float u = rnd16((float)acc[(size_t)i * n + 2 * j + 1]);
+      y[(size_t)i * (n / 2) + j] = swiglu1(g, u);
+    }
+  free(acc);
 }
 
 /* ------------------------------------------------------------- rope / kv */

@@ -52,6 +52,7 @@ class RopeKVOptions(C.Structure):
 
 
 RLK_DECODE_PARTITION_SIZE = 256
+RLK_GEMV_W4_MAX_M = 32
 
 
 class AttentionParams(C.Structure):
@@ -103,6 +104,8 @@ _SIGNATURES = {
                                       C.POINTER(RopeKVOptions), _P]),
     "rlk_paged_attention_decode": (_I, [C.POINTER(AttentionParams),
                                         C.POINTER(DecodeAttentionWork), _P]),
+    "rlk_gemv_w4a16": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _I, _P]),
+    "rlk_gemv_w4a16_swiglu": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]),
     "rlk_float_to_half_bits": (C.c_uint16, [C.c_float]),
     "rlk_half_bits_to_float": (C.c_float, [C.c_uint16]),
     "rlk_rope_inv_freq": (_I, [C.c_double, _I, _I, C.c_double, C.c_double, C.c_double, _I, _P]),

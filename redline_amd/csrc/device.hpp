@@ -15,6 +15,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
@@ -35,6 +36,14 @@ __device__ __forceinline__ f32x8 round_f16(f32x8 f) {
 
 __device__ __forceinline__ float round_f16(float f) {
   return static_cast<float>(static_cast<_Float16>(f));
+}
+
+// silu(g) rounded to fp16 (elementwise.cu:77): the SwiGLU gate before it
+// multiplies up.  exp and the division use the hardware's fast exp2 /
+// reciprocal: the result is rounded to fp16 right after, far coarser than
+// their error.
+__device__ __forceinline__ float silu_f16(float g) {
+  return round_f16(__fdividef(g, 1.0f + __expf(-g)));
 }
 
 // Butterfly reductions over all 64 lanes of a wavefront; every lane gets the result.

@@ -244,13 +244,6 @@ bool launch_norm_nt(int tpr, const NormArgs& a, hipStream_t stream) {
 
 // ------------------------------------------------------------------ SwiGLU
 
-// silu(g) rounded to fp16 (elementwise.cu:77), then times up.  exp and the
-// division use the hardware's fast exp2 / reciprocal: the result is rounded
-// to fp16 right after, far coarser than their error.
-__device__ __forceinline__ float silu_f16(float g) {
-  return round_f16(__fdividef(g, 1.0f + __expf(-g)));
-}
-
 // Split layout: gate in [r, 0:I], up in [r, I:2I]; flat over the [rows, vecs]
 // output vectors (vecs = I / 8).
 template <int BS, bool NT>

@@ -1,0 +1,473 @@
+// Weight-only INT4 GEMV for decode on gfx950 matrix cores, with an optional
+// SwiGLU epilogue over interleaved (gate_i, up_i) weight rows.
+//
+// Reference behaviour: gemv_weight_only.cu:103-160 (y = s * sum(x q) + o *
+// sum(x) per 32-aligned group of K), :46-63 (SwiGLU rounding points), launchers
+// :222-241.
+//
+// Design.  At decode batch m <= 32 every weight byte is used 2m times, so a
+// vector-ALU GEMV with fp32 FMAs is compute-bound on this chip from m ~ 4 on.
+// The dot products run on MFMA (v_mfma_f32_16x16x32_f16) instead, with the
+// activations as the A operand (16 rows of x) and the weights as B (16 weight
+// rows, one per lane column):
+//   * each lane holds 8 codes of its weight row per step (4 bytes), turned
+//     into exact fp16 values 64 + q by OR-ing each nibble into the mantissa of
+//     64.0 -- one VALU op per two codes plus shifts, no converts;
+//   * an MFMA against an all-ones B gives sum(x) per activation row;
+//   * once per scale window (a K range inside one quantisation group) the fp32
+//     partial is folded in as acc += s * (x . (64 + q)) + (o - 64 s) * sum(x)
+//     -- the reference's s * sum(x q) + o * sum(x) -- so the codes are never
+//     rounded through a dequantised fp16 weight.  The output layout gives each
+//     lane one weight row, so s and o are per-lane scalars.
+// K order inside an MFMA is free as long as A and B agree: a lane takes 32
+// consecutive K (16 code bytes, one 16-byte load per row and chunk) and the
+// activations are permuted to the nibble order (0, 4, 1, 5, 2, 6, 3, 7) that
+// the code unpacking produces.
+//
+// Work split.  Activations are the expensive operand to fetch: every weight
+// tile needs all of x, and per-wave x loads (16 rows x 64 bytes per load
+// instruction) cost more than the weights themselves -- the load path pays per
+// cache line an instruction touches, not per byte.  So a workgroup stages x
+// once in LDS, already permuted, and all its waves read their A fragments
+// from there; the grid is sized to about one workgroup per compute unit, so x
+// is staged about once per CU.  Each wave owns one 16-row tile over the full K
+// (K-split ways S > 1 are a tuning option) and keeps a P-deep ring of
+// non-temporal weight loads in flight, started before the staging so that both
+// overlap.  Scales and offsets of the workgroup's rows are staged in LDS too,
+// for the same per-line reason.  When x does not fit the LDS budget, K is
+// walked in passes (x re-staged per pass, accumulators kept).  128-K chunks
+// (group_size % 128 == 0, the common case) are one scale window each; other
+// group sizes (32, 64, 96, ...) use 32-K chunks.
+#include <algorithm>
+
+#include "device.hpp"
+#include "redline_amd/rlk.h"
+#include "status.hpp"
+
+namespace rlk {
+namespace {
+
+struct W4Args {
+  const uint16_t* x;  // activations of this launch, [m, k]
+  const uint8_t* w;
+  const uint16_t* scales;
+  const uint16_t* offsets;
+  const uint16_t* bias;
+  void* y;            // [m, y_ld]
+  int m;              // activation rows (1 .. 16 MT)
+  int n, k, group_size, groups, nchunks;
+  int cpp;            // K chunks per x pass (a multiple of K-split ways x ring depth)
+  int npass;
+  int xstride;        // halves per staged x row
+  int y_ld;
+};
+
+constexpr int kModeF16 = 0, kModeF32 = 1, kModeSwiglu = 2;
+
+// Codes of one lane for one chunk: 32 K (16 bytes) for 128-K chunks, 8 K
+// (4 bytes) for 32-K chunks.  Weights are read exactly once: non-temporal.
+template <int KC>
+__device__ __forceinline__ u32x4 load_codes(const uint8_t* p) {
+  if constexpr (KC == 128) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  } else {
+    u32x4 v = {__builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p)), 0u, 0u, 0u};
+    return v;
+  }
+}
+
+// A value the compiler must keep in a VGPR without knowing it (the empty asm
+// emits no instruction).  With the code magic opaque, (x & mask) | magic is
+// selected as one v_and_or_b32 (mask in an SGPR); with both operands known
+// constants the compiler splits it into AND + OR, because gfx9 VOP3
+// encodings take no literal.  Writing the op itself as inline asm would hide
+// it from the compiler's hazard recognizer, which must pad a VALU write of an
+// MFMA source operand.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+  return (x & mask) | magic;
+}
+
+// The 8 codes of a word (nibble e = code of K offset e) as fp16 values
+// 64 + q, in the order (q0, q4, q1, q5, q2, q6, q3, q7): a nibble placed in
+// mantissa bits 4..7 of 64.0 (0x5400) reads 64 + q exactly.  The bias of 64
+// is removed through the offset term (o - 64 s), computed once per group in
+// fp32; it keeps the MFMA sums within a small factor of the unbiased ones.
+__device__ __forceinline__ f16x8 codes_f16(uint32_t word, uint32_t magic) {
+  constexpr uint32_t kMask = 0x00F000F0u;
+  const u32x4 r = {and_or(word << 4, kMask, magic), and_or(word, kMask, magic),
+                   and_or(word >> 4, kMask, magic), and_or(word >> 8, kMask, magic)};
+  return __builtin_bit_cast(f16x8, r);
+}
+constexpr float kCodeBias = 64.0f;
+
+// 8 consecutive activations permuted to the codes' order.
+__device__ __forceinline__ f16x8 x_perm(u32x4 v) {
+  const f16x8 h = __builtin_bit_cast(f16x8, v);
+  return __builtin_shufflevector(h, h, 0, 4, 1, 5, 2, 6, 3, 7);
+}
+
+// v / d for 0 <= v < 2^21 through a float reciprocal: (v + 1/2) / d lies at
+// least 1/(2d) away from an integer and the float error is below 2^-22 * v/d.
+__device__ __forceinline__ int quot(int v, float inv_d) {
+  return static_cast<int>((static_cast<float>(v) + 0.5f) * inv_d);
+}
+
+__device__ __forceinline__ float swap_adjacent_lanes(float v) {
+  // quad_perm (1, 0, 3, 2): each lane reads its odd/even neighbour
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF,
+                                                            0xF, false));
+}
+
+// Output of one 16x16 tile: lane (qd, r16) holds rows m = m0 + 4 qd + e of
+// weight row `row`.
+template <int MODE>
+__device__ __forceinline__ void store_tile(const W4Args& a, f32x4 v, int m0, int row, int r16) {
+  if constexpr (MODE == kModeSwiglu) {
+    // (gate, up) = rows (2i, 2i + 1) sit in lanes (r16, r16 + 1)
+    f32x4 up;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) up[e] = swap_adjacent_lanes(v[e]);
+    if ((r16 & 1) != 0 || row >= a.n) return;
+    uint16_t* y = static_cast<uint16_t*>(a.y) + row / 2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (m0 + e >= a.m) break;
+      const float g = round_f16(v[e]);
+      const float u = round_f16(up[e]);
+      y[static_cast<size_t>(m0 + e) * a.y_ld] =
+          __builtin_bit_cast(uint16_t, static_cast<_Float16>(silu_f16(g) * u));
+    }
+  } else {
+    if (row >= a.n) return;
+    const float b =
+        a.bias != nullptr ? static_cast<float>(__builtin_bit_cast(_Float16, a.bias[row])) : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (m0 + e >= a.m) break;
+      const size_t at = static_cast<size_t>(m0 + e) * a.y_ld + row;
+      if constexpr (MODE == kModeF32) {
+        static_cast<float*>(a.y)[at] = v[e] + b;
+      } else {
+        static_cast<uint16_t*>(a.y)[at] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[e] + b));
+      }
+    }
+  }
+}
+
+// A workgroup owns `wr` 16-row weight tiles (wr row waves, a runtime value)
+// times S K-split ways: wave w takes row slot w % wr and K part w / wr.
+// P: chunks in flight per wave; KC: K per chunk (128 or 32); MT: 16-row
+// activation tiles (m <= 16 MT).
+template <int S, int P, int KC, int MT, int MODE>
+__global__ __launch_bounds__(1024) void gemv_w4_kernel(W4Args a) {
+  constexpr int kSteps = KC / 32, kLaneK = KC / 4;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int threads = blockDim.x, wr = threads / (64 * S);
+  const int rows_wg = 16 * wr;
+  uint32_t* so_lds = reinterpret_cast<uint32_t*>(lds);  // [groups][rows_wg]: s | o << 16
+  uint16_t* x_lds = reinterpret_cast<uint16_t*>(lds + static_cast<size_t>(a.groups) * rows_wg * 4);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slot = wave % wr, part = wave / wr;
+  const int r16 = lane & 15, qd = lane >> 4;
+  const int row = blockIdx.x * wr * 16 + slot * 16 + r16;  // this lane's weight row
+  const int rowc = min(row, a.n - 1);                       // rows past n re-read the last one
+  const int last = a.nchunks - 1;
+
+  // The weight codes of this lane's row travel in a ring of P chunks; part
+  // `part` takes chunks part, part + S, part + 2S, ...  The ring is started
+  // before scales, offsets and x are staged, so that all are in flight together.
+  const uint8_t* wp = a.w + static_cast<size_t>(rowc) * (a.k / 2) + qd * (kLaneK / 2);
+  u32x4 wbuf[P];
+  auto fetch = [&](int p, int c) { wbuf[p] = load_codes<KC>(wp + static_cast<size_t>(c) * (KC / 2)); };
+#pragma unroll
+  for (int p = 0; p < P; ++p) fetch(p, min(part + S * p, last));
+
+  // Both staging loops keep kBatch loads in flight before their LDS writes
+  // (indices clamped so the loads are unconditional).  Scales and offsets go
+  // to LDS as [group][row]: per-lane loads of them would touch 16 rows' lines
+  // per instruction, as costly as a weight load.
+  constexpr int kBatch = 8;
+  const int staged = rows_wg * a.groups;
+  const float inv_groups = 1.0f / static_cast<float>(a.groups);
+  const int row_wg0 = blockIdx.x * rows_wg;
+  for (int i0 = tid; i0 < staged; i0 += threads * kBatch) {
+    uint32_t v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = min(i0 + u * threads, staged - 1);
+      const int r = quot(i, inv_groups), g = i - r * a.groups;
+      const size_t src = static_cast<size_t>(min(row_wg0 + r, a.n - 1)) * a.groups + g;
+      v[u] = a.scales[src] | (static_cast<uint32_t>(a.offsets[src]) << 16);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u * threads;
+      if (i < staged) {
+        const int r = quot(i, inv_groups), g = i - r * a.groups;
+        so_lds[g * rows_wg + r] = v[u];
+      }
+    }
+  }
+  auto stage_x = [&](int c0, int c1) {
+    const int vpr = (c1 - c0) * (KC / 8);  // 8-half vectors per row
+    const int total = a.m * vpr;
+    const float inv_vpr = 1.0f / static_cast<float>(vpr);
+    for (int v0 = tid; v0 < total; v0 += threads * kBatch) {
+      u32x4 val[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int v = min(v0 + u * threads, total - 1);
+        const int r = quot(v, inv_vpr), e = v - r * vpr;
+        val[u] = load16(a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(c0) * KC + e * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int v = v0 + u * threads;
+        if (v < total) {
+          const int r = quot(v, inv_vpr), e = v - r * vpr;
+          *reinterpret_cast<f16x8*>(x_lds + r * a.xstride + e * 8) = x_perm(val[u]);
+        }
+      }
+    }
+  };
+  stage_x(0, min(a.cpp, a.nchunks));
+
+  // A-fragment rows of this lane (activation rows past m repeat the last one)
+  const uint16_t* xl[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xl[mt] = x_lds + min(16 * mt + r16, a.m - 1) * a.xstride + qd * kLaneK;
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr f16x8 kOnes = {1, 1, 1, 1, 1, 1, 1, 1};
+  const uint32_t magic = opaque(0x54005400u);  // 64.0 in both halves
+
+  // Rounds of P chunks per part.  A pass holds cpp chunks, a multiple of S*P,
+  // so pass boundaries fall on round boundaries for every part alike.
+  const int rounds = (a.nchunks + S * P - 1) / (S * P);
+  int c0 = 0;  // first chunk of the staged pass
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int cb = rd * S * P;
+    if (cb % a.cpp == 0) {  // workgroup-uniform
+      if (cb > 0) {
+        __syncthreads();  // every wave is done with the previous pass's x
+        stage_x(cb, min(cb + a.cpp, a.nchunks));
+        c0 = cb;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int c = cb + part + S * p;
+      if (c < a.nchunks) {  // wave-uniform: only the last round has idle slots
+        f16x8 xa[MT][kSteps];
+        f32x4 xs[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < kSteps; ++j) {
+            xa[mt][j] = *reinterpret_cast<const f16x8*>(xl[mt] + (c - c0) * KC + 8 * j);
+            xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], kOnes, xs[mt], 0, 0, 0);
+          }
+        }
+        const uint32_t so = so_lds[(c * KC / a.group_size) * rows_wg + slot * 16 + r16];
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
+        const float of = fmaf(-kCodeBias, sc,
+                              static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16))));
+        f16x8 q[kSteps];
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j) q[j] = codes_f16(wbuf[p][j], magic);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < kSteps; ++j)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], q[j], d, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(of, xs[mt][e], fmaf(sc, d[e], acc[mt][e]));
+        }
+      }
+      // refill the slot with this part's chunk one round ahead
+      fetch(p, min(c + S * P, last));
+    }
+  }
+
+  if constexpr (S > 1) {
+    // K parts 1..S-1 hand their partial sums to part 0 through LDS (after the
+    // x region); part 0 adds them in part order, so the result is deterministic.
+    f32x4* red = reinterpret_cast<f32x4*>(x_lds + static_cast<size_t>(a.m) * a.xstride);
+    if (part > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        red[(((part - 1) * wr + slot) * MT + mt) * kWave + lane] = acc[mt];
+    }
+    __syncthreads();
+    if (part > 0) return;
+#pragma unroll
+    for (int q = 1; q < S; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] += red[(((q - 1) * wr + slot) * MT + mt) * kWave + lane];
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) store_tile<MODE>(a, acc[mt], 16 * mt + 4 * qd, row, r16);
+}
+
+// LDS a workgroup may take: the device allows 160 KiB per workgroup.
+constexpr size_t kLdsBudget = 160 * 1024;
+constexpr int kNoFit = 1;  // launch(): the policy's smallest x pass exceeds the LDS budget
+
+int compute_units() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+template <int S, int P, int KC, int MT, int MODE>
+int launch(W4Args a, int wr_max, hipStream_t stream) {
+  // Row waves per workgroup: enough that the grid is about one workgroup per
+  // compute unit, so x is staged about once per CU.
+  const int tiles = (a.n + 15) / 16;
+  const int cus = compute_units();
+  const int wr = std::max(1, std::min(std::min(wr_max, 16 / S), (tiles + cus - 1) / cus));
+  const size_t red_bytes = static_cast<size_t>(S - 1) * wr * MT * kWave * sizeof(f32x4);
+  const size_t so_bytes = static_cast<size_t>(a.groups) * 16 * wr * 4;
+  const size_t fixed = red_bytes + so_bytes;
+  const size_t min_x = static_cast<size_t>(a.m) * (S * P * KC + 8) * 2;
+  if (fixed + min_x > kLdsBudget) return kNoFit;
+  // chunks per x pass: as many as fit, balanced over the passes, a multiple of S*P
+  const size_t unit = static_cast<size_t>(S) * P;
+  const size_t fit =
+      ((kLdsBudget - fixed) / (2 * static_cast<size_t>(a.m)) - 8) / KC / unit * unit;
+  const int npass = static_cast<int>((a.nchunks + fit - 1) / fit);
+  const int per = (a.nchunks + npass - 1) / npass;
+  a.cpp = static_cast<int>((per + unit - 1) / unit * unit);
+  a.npass = (a.nchunks + a.cpp - 1) / a.cpp;
+  a.xstride = a.cpp * KC + 8;
+  const size_t lds = fixed + static_cast<size_t>(a.m) * a.xstride * 2;
+  auto kernel = gemv_w4_kernel<S, P, KC, MT, MODE>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess)
+      return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
+                  hipGetErrorString(e));
+  }
+  const int blocks = (tiles + wr - 1) / wr;
+  kernel<<<blocks, 64 * wr * S, lds, stream>>>(a);
+  return RLK_OK;
+}
+
+// Launch policies (K-split ways, chunks in flight per wave, most row waves per
+// workgroup); entry 0 -- no split, 8 chunks in flight -- is the default, the others are selectable for tuning
+// sweeps through RLK_TUNE_W4_CFG.  32-K chunks always use the default.
+template <int KC, int MT, int MODE>
+int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
+  int st = kNoFit;
+  if constexpr (KC == 128) {
+    switch (cfg) {
+      case 1: st = launch<2, 8, KC, MT, MODE>(a, 8, s); break;
+      case 2: st = launch<2, 4, KC, MT, MODE>(a, 8, s); break;
+      case 3: st = launch<4, 4, KC, MT, MODE>(a, 4, s); break;
+      case 4: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
+      case 5: st = launch<1, 8, KC, MT, MODE>(a, 4, s); break;
+      case 6: st = launch<4, 2, KC, MT, MODE>(a, 4, s); break;
+      case 7: st = launch<2, 8, KC, MT, MODE>(a, 2, s); break;
+      default: break;
+    }
+  }
+  (void)cfg;
+  // the default, then shallower rings when x passes do not fit
+  if (st == kNoFit) st = launch<1, 8, KC, MT, MODE>(a, 16, s);
+  if (st == kNoFit) st = launch<1, 4, KC, MT, MODE>(a, 16, s);
+  if (st == kNoFit) st = launch<1, 2, KC, MT, MODE>(a, 16, s);
+  if (st == kNoFit)
+    return fail(RLK_EUNSUPPORTED, "gemv_w4a16: k=%d does not fit the LDS budget", a.k);
+  return st;
+}
+
+template <int MODE>
+int dispatch(const W4Args& a, hipStream_t s) {
+  const bool wide = a.group_size % 128 == 0;
+  const int cfg = tune_knob("RLK_TUNE_W4_CFG", 0);
+  if (a.m <= 16)
+    return wide ? launch_cfg<128, 1, MODE>(a, cfg, s) : launch_cfg<32, 1, MODE>(a, cfg, s);
+  return wide ? launch_cfg<128, 2, MODE>(a, cfg, s) : launch_cfg<32, 2, MODE>(a, cfg, s);
+}
+
+int gemv_w4(const char* what, const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
+            const uint16_t* offsets, int group_size, const uint16_t* bias, int n, int k, void* y,
+            int mode, hipStream_t stream) {
+  if (m <= 0) return RLK_OK;
+  if (x == nullptr || w == nullptr || scales == nullptr || offsets == nullptr || y == nullptr)
+    return fail(RLK_EINVAL, "%s: null pointer argument", what);
+  if (m > RLK_GEMV_W4_MAX_M)
+    return fail(RLK_EUNSUPPORTED, "%s: unsupported m=%d (at most %d)", what, m, RLK_GEMV_W4_MAX_M);
+  if (n <= 0 || k <= 0 || group_size <= 0 || k % 32 != 0 || group_size % 32 != 0 ||
+      k % group_size != 0)
+    return fail(RLK_EINVAL, "%s needs K and group_size multiples of 32 (k=%d, group_size=%d)",
+                what, k, group_size);
+  if (k > (1 << 18))
+    return fail(RLK_EUNSUPPORTED, "%s: k=%d exceeds %d", what, k, 1 << 18);
+  if (mode == kModeSwiglu && n % 2 != 0)
+    return fail(RLK_EINVAL, "%s: bad shape (n=%d must be even: interleaved gate/up rows)", what, n);
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
+    return fail(RLK_EINVAL, "%s: x and w must be 16-byte aligned", what);
+  W4Args a;
+  a.x = x;
+  a.w = w;
+  a.scales = scales;
+  a.offsets = offsets;
+  a.bias = mode == kModeSwiglu ? nullptr : bias;
+  a.y = y;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.group_size = group_size;
+  a.groups = k / group_size;
+  a.nchunks = k / (group_size % 128 == 0 ? 128 : 32);
+  a.y_ld = mode == kModeSwiglu ? n / 2 : n;
+  int st;
+  switch (mode) {
+    case kModeF32: st = dispatch<kModeF32>(a, stream); break;
+    case kModeSwiglu: st = dispatch<kModeSwiglu>(a, stream); break;
+    default: st = dispatch<kModeF16>(a, stream); break;
+  }
+  return st != RLK_OK ? st : launch_status(what);
+}
+
+}  // namespace
+}  // namespace rlk
+
+using namespace rlk;
+
+extern "C" int rlk_gemv_w4a16(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
+                              const uint16_t* offsets, int group_size, const uint16_t* bias, int n,
+                              int k, void* y, int y_fp32, hipStream_t stream) {
+  return gemv_w4("gemv_w4a16", x, m, w, scales, offsets, group_size, bias, n, k, y,
+                 y_fp32 ? kModeF32 : kModeF16, stream);
+}
+
+extern "C" int rlk_gemv_w4a16_swiglu(const uint16_t* x, int m, const uint8_t* w,
+                                     const uint16_t* scales, const uint16_t* offsets,
+                                     int group_size, int n, int k, uint16_t* y,
+                                     hipStream_t stream) {
+  return gemv_w4("gemv_w4a16_swiglu", x, m, w, scales, offsets, group_size, nullptr, n, k, y,
+                 kModeSwiglu, stream);
+}

@@ -20,10 +20,12 @@ __all__ = [
     "embedding_lookup", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
     "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
     "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "attention_params",
-    "decode_work", "DecodeWorkspace", "kDecodePartitionSize",
+    "decode_work", "DecodeWorkspace", "kDecodePartitionSize", "gemv_w4a16", "gemv_w4a16_swiglu",
+    "kGemvW4MaxM",
 ]
 
 kDecodePartitionSize = _lib.RLK_DECODE_PARTITION_SIZE
+kGemvW4MaxM = _lib.RLK_GEMV_W4_MAX_M
 
 SCALE_F32 = _lib.RLK_SCALE_F32
 SCALE_F16 = _lib.RLK_SCALE_F16
@@ -97,6 +99,38 @@ def silu_and_mul_interleaved(gate_up, rows, inter, out, stream=None):
         _need(gate_up, rows * 2 * inter, "gate_up"); _need(out, rows * inter, "out")
     check(lib().rlk_silu_and_mul_interleaved(_ptr(gate_up, torch.float16, "gate_up"), rows, inter,
                                              _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def _gemv_w4_need(x, m, w, scales, offsets, group_size, n, k):
+    if m > 0 and k > 0 and group_size > 0 and k % group_size == 0:
+        _need(x, m * k, "x"); _need(w, n * k // 2, "w")
+        _need(scales, n * (k // group_size), "scales"); _need(offsets, n * (k // group_size), "offsets")
+
+
+def gemv_w4a16(x, m, w, scales, offsets, group_size, bias, n, k, y, y_fp32=False, stream=None):
+    """y[m, n] = x[m, k] . dequant(w)^T (+ bias): INT4 weight [n, k/2] uint8 with
+    fp16 scales/offsets [n, k/group_size]; y fp16, or fp32 with y_fp32."""
+    _gemv_w4_need(x, m, w, scales, offsets, group_size, n, k)
+    if m > 0:
+        _need(y, m * n, "y")
+    check(lib().rlk_gemv_w4a16(
+        _ptr(x, torch.float16, "x"), m, _ptr(w, torch.uint8, "w"),
+        _ptr(scales, torch.float16, "scales"), _ptr(offsets, torch.float16, "offsets"), group_size,
+        _ptr(bias, torch.float16, "bias", True), n, k,
+        _ptr(y, torch.float32 if y_fp32 else torch.float16, "y"), int(bool(y_fp32)),
+        _stream(stream)))
+
+
+def gemv_w4a16_swiglu(x, m, w, scales, offsets, group_size, n, k, y, stream=None):
+    """y[m, n/2] = silu(gate) * up from an INT4 weight whose rows are interleaved
+    (gate_i, up_i), in the GEMV epilogue."""
+    _gemv_w4_need(x, m, w, scales, offsets, group_size, n, k)
+    if m > 0:
+        _need(y, m * (n // 2), "y")
+    check(lib().rlk_gemv_w4a16_swiglu(
+        _ptr(x, torch.float16, "x"), m, _ptr(w, torch.uint8, "w"),
+        _ptr(scales, torch.float16, "scales"), _ptr(offsets, torch.float16, "offsets"), group_size,
+        n, k, _ptr(y, torch.float16, "y"), _stream(stream)))
 
 
 def gather_rows(src, idx, n, cols, dst, stream=None):

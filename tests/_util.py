@@ -51,3 +51,34 @@ def assert_bits_equal(got, want, what=""):
     if not np.array_equal(gv, wv):
         n = int(np.sum(g.reshape(-1) != w.reshape(-1)))
         raise AssertionError(f"{what}: {n} elements differ bitwise")
+
+
+def int4_linear(rng: np.random.Generator, n: int, k: int, group_size: int, dense: bool = True):
+    """A group-quantised INT4 weight in the reference's GEMV layout.
+
+    Returns (packed uint8 [n, k/2], scales fp16 [n, k/g], offsets fp16 [n, k/g],
+    float64 dequantised W [n, k], or None when not `dense`).  W is built from the codes before they are
+    packed (W = q * s + o), so it checks the packing rather than restating it.
+    Scales and offsets have the magnitudes a min/max quantiser gives a weight
+    of std ~0.05 (offset ~ -7.5 scale: W is roughly zero-mean)."""
+    groups = k // group_size
+    q = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    s = rng.uniform(0.004, 0.02, (n, groups)).astype(np.float16)
+    o = (-7.5 * s.astype(np.float64) * rng.uniform(0.9, 1.1, (n, groups))).astype(np.float16)
+    w = None
+    if dense:
+        s64 = np.repeat(s.astype(np.float64), group_size, axis=1)
+        o64 = np.repeat(o.astype(np.float64), group_size, axis=1)
+        w = q * s64 + o64
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return packed, s, o, w
+
+
+def interleave_rows(a: np.ndarray) -> np.ndarray:
+    """[gate; up] rows -> (gate_0, up_0, gate_1, up_1, ...), the loader's INT4
+    gate_up layout (src/cuda/model/weights.cpp:157-167)."""
+    half = a.shape[0] // 2
+    out = np.empty_like(a)
+    out[0::2] = a[:half]
+    out[1::2] = a[half:]
+    return out

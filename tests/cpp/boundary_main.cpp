@@ -34,6 +34,18 @@ int main() {
   kv.head_dim = 80;
   expect_throw("rope", [&] { kernels::rope_and_write_kv(nullptr, nullptr, nullptr, 1, 4, nullptr, nullptr, kv, nullptr); },
                "unsupported head_dim 80");
+  alignas(16) static unsigned char dummy[256];
+  const half* hx = reinterpret_cast<const half*>(dummy);
+  half* hy = reinterpret_cast<half*>(dummy);
+  expect_throw("gemv_w4 null", [&] { kernels::gemv_w4a16(nullptr, 1, dummy, hx, hx, 128, nullptr, 8, 256, hy, false, nullptr); },
+               "null pointer");
+  expect_throw("gemv_w4 k", [&] { kernels::gemv_w4a16(hx, 1, dummy, hx, hx, 128, nullptr, 8, 200, hy, false, nullptr); },
+               "multiples of 32");
+  expect_throw("gemv_w4 m", [&] { kernels::gemv_w4a16(hx, kernels::kGemvW4MaxM + 1, dummy, hx, hx, 128, nullptr, 8, 256, hy, true, nullptr); },
+               "unsupported m");
+  expect_throw("gemv_w4 swiglu n", [&] { kernels::gemv_w4a16_swiglu(hx, 2, dummy, hx, hx, 128, 7, 256, hy, nullptr); },
+               "even");
+  kernels::gemv_w4a16_swiglu(hx, 0, dummy, hx, hx, 128, 8, 256, hy, nullptr);
   // n <= 0 is a silent no-op, as in the reference.
   kernels::embedding_lookup(nullptr, nullptr, 0, 12, nullptr, nullptr);
   kernels::rope_and_write_kv(nullptr, nullptr, nullptr, 0, 4, nullptr, nullptr, kv, nullptr);

@@ -1,0 +1,161 @@
+"""Parity of the INT4 weight-only GEMV and its fused SwiGLU epilogue (through
+the C ABI) with the CPU oracle.
+
+The oracle evaluates x . dequant(W)^T in float64 (pinned in tests/test_oracle.py
+against a matmul over the weight built before packing, the reference's nibble
+order KAT and closed forms).  The kernel sums in fp32 on the matrix cores, so
+fp32 outputs are compared with the reference test's own bound (relative max
+error 1e-4, tests/cuda/test_gemm.cu:147-154), fp16 outputs at fp16 tolerance,
+and the SwiGLU output additionally with the reference's 6e-3 bound
+(test_gemm.cu:258-292).  Geometries: the reference test's (n = 97, k = 512,
+g = 64, m in 1, 3, 8, 13, 16; inter = 192, k = 256, g = 64), the 128-K chunk
+path (g a multiple of 128), m up to 32 (two activation tiles) and the
+Llama-3.1-8B gate_up projection (n = 2 x 14336, k = 4096, g = 128)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import redline_amd as ra
+from tests._util import (assert_close_f16, int4_linear, interleave_rows, randn_f16, rel_max_err,
+                         say)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available()
+    import redline_amd.kernels  # noqa: F401
+    return torch
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_gemv(torch, x, packed, s, o, g, bias=None, f32=False):
+    from redline_amd import kernels as K
+    m, k = x.shape
+    n = packed.shape[0]
+    y = torch.empty((m, n), dtype=torch.float32 if f32 else torch.float16, device="cuda")
+    K.gemv_w4a16(dev(torch, x), m, dev(torch, packed), dev(torch, s), dev(torch, o), g,
+                 None if bias is None else dev(torch, bias), n, k, y, f32)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def run_swiglu(torch, x, packed, s, o, g):
+    from redline_amd import kernels as K
+    m, k = x.shape
+    n = packed.shape[0]
+    y = torch.empty((m, n // 2), dtype=torch.float16, device="cuda")
+    K.gemv_w4a16_swiglu(dev(torch, x), m, dev(torch, packed), dev(torch, s), dev(torch, o), g, n,
+                        k, y)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("g", [64, 128, 256])
+@pytest.mark.parametrize("m", [1, 3, 8, 13, 16, 20, 32])
+def test_gemv_w4_reference_geometry(torch_cuda, g, m):
+    """gemv_weight_only_matches_cpu: odd n exercises the row tail; bias; fp32 and fp16 out."""
+    torch = torch_cuda
+    say(f"gemv_w4 n=97 k=512 g={g} m={m}")
+    rng = np.random.default_rng(100 * g + m)
+    n, k = 97, 512
+    packed, s, o, _ = int4_linear(rng, n, k, g)
+    x = randn_f16(rng, (m, k))
+    bias = randn_f16(rng, (n,), 0.1)
+    want = oracle.gemv_w4a16(x, packed, s, o, g, bias)
+    got32 = run_gemv(torch, x, packed, s, o, g, bias, f32=True)
+    assert rel_max_err(got32, want) <= 1e-4
+    np.testing.assert_allclose(got32, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+    got16 = run_gemv(torch, x, packed, s, o, g, bias, f32=False)
+    assert_close_f16(got16, want.astype(np.float16), what="gemv fp16")
+
+
+@pytest.mark.parametrize("g,k", [(64, 256), (128, 512), (32, 96)])
+@pytest.mark.parametrize("m", [1, 3, 8, 16, 20, 32])
+def test_gemv_w4_swiglu_interleaved_rows(torch_cuda, g, k, m):
+    """gemv_w4a16_swiglu_interleaved_rows: [gate; up] quantised, rows interleaved
+    as the loader stores them; compared with the oracle's fused epilogue and
+    with silu(gate) * up of the float64 projection (the reference's bound)."""
+    torch = torch_cuda
+    say(f"gemv_w4_swiglu inter=192 k={k} g={g} m={m}")
+    rng = np.random.default_rng(1200 + m + g)
+    inter = 192
+    packed, s, o, w = int4_linear(rng, 2 * inter, k, g)
+    pi, si, oi = interleave_rows(packed), interleave_rows(s), interleave_rows(o)
+    x = randn_f16(rng, (m, k))
+    got = run_swiglu(torch, x, pi, si, oi, g)
+    want = oracle.gemv_w4a16_swiglu(x, pi, si, oi, g)
+    assert_close_f16(got, want, what="swiglu")
+    y = x.astype(np.float64) @ w.T
+    gate, up = y[:, :inter], y[:, inter:]
+    exact = gate / (1 + np.exp(-gate)) * up
+    assert rel_max_err(got, exact) <= 6e-3
+
+
+@pytest.mark.parametrize("m", [1, 8, 32])
+def test_gemv_w4_swiglu_llama_gate_up(torch_cuda, m):
+    """Llama-3.1-8B gate_up at decode: n = 28672 interleaved rows, k = 4096, g = 128."""
+    torch = torch_cuda
+    say(f"gemv_w4_swiglu llama m={m}")
+    rng = np.random.default_rng(7 + m)
+    n, k, g = 2 * 14336, 4096, 128
+    packed, s, o, _ = int4_linear(rng, n, k, g, dense=False)
+    x = randn_f16(rng, (m, k))
+    got = run_swiglu(torch, x, packed, s, o, g)
+    want = oracle.gemv_w4a16_swiglu(x, packed, s, o, g)
+    assert_close_f16(got, want, what="llama swiglu")
+
+
+@pytest.mark.parametrize("cfg", range(8))
+def test_gemv_w4_launch_policies_agree(torch_cuda, cfg):
+    """Every selectable launch policy gives the same result as the default
+    (bit-identical is not required: split-K order differs)."""
+    torch = torch_cuda
+    say(f"gemv_w4 cfg={cfg}")
+    rng = np.random.default_rng(cfg)
+    n, k, g, m = 200, 1024, 128, 9
+    packed, s, o, _ = int4_linear(rng, n, k, g)
+    x = randn_f16(rng, (m, k))
+    want = oracle.gemv_w4a16(x, packed, s, o, g)
+    os.environ["RLK_TUNE_W4_CFG"] = str(cfg)
+    try:
+        got = run_gemv(torch, x, packed, s, o, g, f32=True)
+    finally:
+        del os.environ["RLK_TUNE_W4_CFG"]
+    assert rel_max_err(got, want) <= 1e-4
+
+
+def test_gemv_w4_deterministic_and_errors(torch_cuda):
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    say("gemv_w4 determinism/errors")
+    rng = np.random.default_rng(3)
+    n, k, g, m = 64, 256, 64, 5
+    packed, s, o, _ = int4_linear(rng, n, k, g)
+    x = randn_f16(rng, (m, k))
+    a = run_gemv(torch, x, packed, s, o, g, f32=True)
+    b = run_gemv(torch, x, packed, s, o, g, f32=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    dx, dw, ds, do = (dev(torch, v) for v in (x, packed, s, o))
+    y = torch.zeros((40, n), dtype=torch.float16, device="cuda")
+    with pytest.raises(ra.Error, match="multiples of 32"):
+        K.gemv_w4a16(dx, m, dw, ds, do, 48, None, n, k, y)
+    with pytest.raises(ra.Error, match="multiples of 32"):
+        K.gemv_w4a16(dx, m, dw, ds, do, 64, None, n, 250, y)
+    with pytest.raises(ra.Error, match="unsupported m"):
+        K.gemv_w4a16(torch.zeros((33, k), dtype=torch.float16, device="cuda"), 33, dw, ds, do, g,
+                     None, n, k, y)
+    with pytest.raises(ra.Error, match="even"):
+        K.gemv_w4a16_swiglu(dx, m, dw, ds, do, g, n - 1, k, y)
+    with pytest.raises(ra.Error, match="16-byte aligned"):
+        K.gemv_w4a16(dx.view(-1)[4:], 1, dw, ds, do, g, None, n, k, y)
+    K.gemv_w4a16(dx, 0, dw, ds, do, g, None, n, k, y)  # m = 0: no-op
+    torch.cuda.synchronize()
+    assert not y.any()

@@ -458,3 +458,71 @@ def test_attention_int8_equals_dequantised_fp64():
     want = _attn_numpy(q, kc, vc, ks, vs, tables, pos, hq, hkv, D, 0.125)
     m = safe(want)
     assert m.mean() > 0.98 and np.array_equal(got[m], to16(want)[m])
+
+
+# ------------------------------------------------------------- INT4 GEMV
+
+def test_gemv_w4_nibble_order_kat():
+    """Byte c/2 holds code c, low nibble for even c (tests/cuda/test_gemm.cu:40-45)."""
+    k, g = 64, 32
+    w = np.zeros((2, k // 2), np.uint8)
+    w[0, 0] = 0x21          # codes 1 (c = 0) and 2 (c = 1)
+    w[1, 5] = 0xF0          # code 15 at c = 11, code 0 at c = 10
+    s = np.ones((2, 2), np.float16)
+    o = np.zeros((2, 2), np.float16)
+    o[1, 0] = -0.5
+    x = np.zeros((3, k), np.float16)
+    x[0, 0], x[1, 1], x[2, 11] = 1, 1, 1
+    y = oracle.gemv_w4a16(x, w, s, o, g)
+    assert y[0, 0] == 1 and y[1, 0] == 2 and y[2, 0] == 0
+    assert y[2, 1] == 14.5 and y[0, 1] == -0.5 and y[1, 1] == -0.5
+
+
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_gemv_w4_against_float64_matmul(g):
+    from tests._util import int4_linear
+    rng = np.random.default_rng(g)
+    n, k, m = 37, 256, 5
+    packed, s, o, w = int4_linear(rng, n, k, g)
+    x = randn_f16(rng, (m, k))
+    bias = randn_f16(rng, (n,), 0.1)
+    want = x.astype(np.float64) @ w.T + bias.astype(np.float64)
+    got = oracle.gemv_w4a16(x, packed, s, o, g, bias)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_gemv_w4_closed_forms():
+    """q = 0 -> offset * sum(x); one-hot x picks the dequantised column."""
+    rng = np.random.default_rng(1)
+    n, k, g = 8, 128, 32
+    s = rng.uniform(0.01, 0.1, (n, k // g)).astype(np.float16)
+    o = rng.uniform(-1, 1, (n, k // g)).astype(np.float16)
+    x = randn_f16(rng, (2, k))
+    y = oracle.gemv_w4a16(x, np.zeros((n, k // 2), np.uint8), s, o, g)
+    xs = x.astype(np.float64).reshape(2, k // g, g).sum(-1)
+    np.testing.assert_allclose(y, xs @ o.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    for c in (0, 1, 63, 64, 127):
+        e = np.zeros((1, k), np.float16)
+        e[0, c] = 1
+        q = (packed[:, c // 2] >> (4 * (c & 1))) & 15
+        col = q * s[:, c // g].astype(np.float64) + o[:, c // g].astype(np.float64)
+        np.testing.assert_array_equal(oracle.gemv_w4a16(e, packed, s, o, g)[0], col)
+
+
+def test_gemv_w4_swiglu_is_interleaved_silu_of_fp16_outputs():
+    """The fused epilogue equals the unfused path: fp16 GEMV output, then
+    silu_and_mul_interleaved (pinned above), except where float64 -> fp16
+    sits on a rounding tie."""
+    from tests._util import int4_linear, interleave_rows
+    rng = np.random.default_rng(2)
+    inter, k, g = 96, 256, 64
+    packed, s, o, _ = int4_linear(rng, 2 * inter, k, g)
+    packed, s, o = interleave_rows(packed), interleave_rows(s), interleave_rows(o)
+    x = randn_f16(rng, (4, k))
+    y = oracle.gemv_w4a16(x, packed, s, o, g)
+    unfused = oracle.silu_and_mul(to16(y), inter, interleaved=True)
+    fused = oracle.gemv_w4a16_swiglu(x, packed, s, o, g)
+    ok = safe(y[:, 0::2]) & safe(y[:, 1::2])
+    assert ok.mean() > 0.99
+    np.testing.assert_array_equal(fused.view(np.uint16)[ok], unfused.view(np.uint16)[ok])
