@@ -25,6 +25,7 @@
 //     and across the 8 waves through LDS.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cstdint>
 
@@ -95,12 +96,25 @@ __device__ __forceinline__ float group_sum_dpp(float v) {
   return v;
 }
 
-// One workgroup = one (item, kv head, 256-key partition), 8 waves.  Each
-// wave owns kPasses passes of kKPP keys; all of its K and V rows are
-// requested before the first is used, so a workgroup keeps its whole
-// partition (256 keys x 2 rows) in flight at once.
+// LDS of one work unit.
+template <int D, int G>
+struct UnitLds {
+  float scores[G][kPart];
+  float red[kWaves][G][D];
+  float stat[kWaves][G];
+  int cell[kPart];  // cache cell of each key of the partition
+};
+
+// One work unit = one (item, kv head, 256-key partition), processed by the 8
+// waves of the workgroup.  `blk` is this thread's block-table entry for key
+// `tid` of the partition (threads tid < 256; -1 past the table).  Each wave
+// owns kPasses passes of kKPP keys; all of its K and V rows are requested
+// before the first is used, so a workgroup keeps its whole partition (256
+// keys x 2 rows) in flight at once.  Starts and ends with every thread of the
+// workgroup.
 template <int D, int G, bool kInt8>
-__global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_kernel(AttnArgs args) {
+__device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>& lds, int item,
+                                            int token, int ctx, int part, int kvh, int blk) {
   constexpr int kLPK = D / 8;             // lanes per key row (16 or 8)
   constexpr int kKPP = kWave / kLPK;      // keys per wave pass
   constexpr int kKPB = kKPP * kWaves;     // keys per workgroup pass
@@ -108,36 +122,24 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   using R = Row<kInt8>;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
-
-  __shared__ float scores[G][kPart];
-  __shared__ float red[kWaves][G][D];
-  __shared__ float stat[kWaves][G];
-  __shared__ int cell_s[kPart];  // cache cell of each key of the partition
-
-  const int part = blockIdx.x, kvh = blockIdx.y, item = blockIdx.z;
+  float (&scores)[G][kPart] = lds.scores;
+  float (&red)[kWaves][G][D] = lds.red;
+  float (&stat)[kWaves][G] = lds.stat;
+  int (&cell_s)[kPart] = lds.cell;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int token = w.item_token[item];
-  const int seq = w.item_seq[item];
-  const int ctx = p.positions[token] + 1;
   const int num_parts = (ctx + kPart - 1) / kPart;
-  if (part >= num_parts) return;  // uniform over the workgroup
   const int start = part * kPart;
   const int n = min(kPart, ctx - start);
   const int slot = lane / kLPK;         // key slot of this lane within a wave pass
   const int e0 = (lane % kLPK) * 8;     // first element of the row owned by this lane
 
-  // Resolve every key of the partition to its cache cell once (one block-
-  // table lookup and division per key instead of one per key and pass); the
-  // K/V addresses below are then one LDS read each.  Table rows are padded
-  // with block 0, so every entry read inside the row is valid.
-  {
+  // Every key of the partition resolved once to its cache cell (the block-
+  // table entry `blk` comes from the caller); the K/V addresses below are
+  // then one LDS read each.
+  if (tid < kPart && blk >= 0) {
     const int bs = p.kv.block_size;
     const int pos = start + tid;
-    const int bi = pos / bs;
-    if (tid < kPart && bi < p.max_blocks_per_seq) {
-      const int blk = p.block_tables[static_cast<int64_t>(seq) * p.max_blocks_per_seq + bi];
-      cell_s[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - bi * bs);
-    }
+    cell_s[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
   }
   // q of the G heads, this lane's 8 elements, kept in fp16 pairs for
   // v_dot2_f32_f16 (the softmax scale is applied to the fp32 dot).
@@ -283,6 +285,110 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
       }
     }
   }
+  __syncthreads();  // the unit's LDS may be reused
+}
+
+// Block-table entry of key `tid` of a partition (threads tid < 256), or -1
+// past the table.  Table rows are padded with block 0, so every entry inside
+// the row is a valid block.
+__device__ __forceinline__ int table_entry(const rlk_attention_params& p, int seq, int part) {
+  const int tid = threadIdx.x;
+  const int bi = (part * kPart + tid) / p.kv.block_size;
+  if (tid >= kPart || bi >= p.max_blocks_per_seq) return -1;
+  return p.block_tables[static_cast<int64_t>(seq) * p.max_blocks_per_seq + bi];
+}
+
+// Persistent form.  Every workgroup first reads each decode item's token,
+// sequence and context into LDS and prefix-sums the partitions per item; the
+// work units (item, partition, kv head) -- only those inside a context -- are
+// then split into contiguous ranges, one per workgroup.  Kv head runs fastest,
+// so one partition's block-table entries serve all kv heads, and the chain of
+// dependent loads per unit is the K/V rows alone.  (Pipelining the next
+// unit's rows into the current unit's registers was measured slower: it needs
+// more than the 128 VGPRs that keep two workgroups per CU.)
+constexpr int kMaxItemsLds = 2048;
+
+template <int D, int G, bool kInt8>
+__global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_persistent(AttnArgs args) {
+  const rlk_attention_params& p = args.p;
+  const rlk_decode_attention_work& w = args.w;
+  __shared__ UnitLds<D, G> s;
+  __shared__ int it_tok[kMaxItemsLds], it_seq[kMaxItemsLds], it_ctx[kMaxItemsLds];
+  __shared__ int it_pfx[kMaxItemsLds + 1];  // partitions before item i
+  __shared__ int wave_tot[kWaves];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int items = w.num_items, hkv = p.kv.num_kv_heads;
+
+  // Items are split into kThreads contiguous runs; each thread sums its run,
+  // the runs are scanned across the workgroup, then each thread writes its
+  // run's exclusive prefixes.
+  const int per = (items + kThreads - 1) / kThreads;
+  const int i0 = min(tid * per, items), i1 = min(i0 + per, items);
+  int run = 0;
+  for (int i = i0; i < i1; ++i) {
+    const int tok = w.item_token[i];
+    const int ctx = p.positions[tok] + 1;
+    it_tok[i] = tok;
+    it_seq[i] = w.item_seq[i];
+    it_ctx[i] = ctx;
+    run += (ctx + kPart - 1) / kPart;
+  }
+  int incl = run;  // inclusive scan of runs inside the wave
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int v = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += v;
+  }
+  if (lane == kWave - 1) wave_tot[wave] = incl;
+  __syncthreads();
+  int before = incl - run;
+  for (int ww = 0; ww < wave; ++ww) before += wave_tot[ww];
+  for (int i = i0; i < i1; ++i) {
+    it_pfx[i] = before;
+    before += (it_ctx[i] + kPart - 1) / kPart;
+  }
+  if (tid == kThreads - 1) it_pfx[items] = before;
+  __syncthreads();
+
+  const int total = it_pfx[items] * hkv;
+  const int chunk = (total + gridDim.x - 1) / gridDim.x;
+  const int u0 = blockIdx.x * chunk, u1 = min(u0 + chunk, total);
+  if (u0 >= u1) return;
+  // first unit: binary search of its partition among the items
+  int pu = u0 / hkv, kvh = u0 - pu * hkv;
+  int lo = 0, hi = items - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (it_pfx[mid] <= pu) lo = mid; else hi = mid - 1;
+  }
+  int item = lo, part = pu - it_pfx[item];
+  int blk = table_entry(p, it_seq[item], part);
+  for (int u = u0; u < u1; ++u) {
+    attend_unit<D, G, kInt8>(args, s, item, it_tok[item], it_ctx[item], part, kvh, blk);
+    if (++kvh == hkv) {
+      kvh = 0;
+      if (++part == it_pfx[item + 1] - it_pfx[item]) {
+        part = 0;
+        ++item;
+      }
+      if (u + 1 < u1) blk = table_entry(p, it_seq[item], part);
+    }
+  }
+}
+
+// Grid form: one workgroup per (partition, kv head, item), exiting at once
+// when the partition lies past the item's context.
+template <int D, int G, bool kInt8>
+__global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_kernel(AttnArgs args) {
+  const rlk_attention_params& p = args.p;
+  const rlk_decode_attention_work& w = args.w;
+  __shared__ UnitLds<D, G> s;
+  const int part = blockIdx.x, kvh = blockIdx.y, item = blockIdx.z;
+  const int token = w.item_token[item];
+  const int blk = table_entry(p, w.item_seq[item], part);  // issued before the context is known
+  const int ctx = p.positions[token] + 1;
+  if (part >= (ctx + kPart - 1) / kPart) return;  // uniform over the workgroup
+  attend_unit<D, G, kInt8>(args, s, item, token, ctx, part, kvh, blk);
 }
 
 // Merges the split-K partials of one (item, head): one lane per output dim
@@ -310,8 +416,36 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
       static_cast<_Float16>(o / total);
 }
 
+int compute_units() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// The persistent form serves FP16 caches (measured faster at C2); INT8 keeps
+// the grid form, where the persistent loop's extra state spills registers.
+// RLK_TUNE_ATTN_PERSIST overrides: workgroups per CU for the persistent form
+// (both dtypes), or 0 for the grid form.
 template <int D, int G>
 void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
+  const int mode = tune_knob("RLK_TUNE_ATTN_PERSIST", int8 ? 0 : 2);
+  if (mode > 0 && a.w.num_items <= kMaxItemsLds) {
+    const int64_t units = static_cast<int64_t>(a.w.num_items) * a.w.max_partitions * a.p.kv.num_kv_heads;
+    const int blocks = static_cast<int>(std::min<int64_t>(units, static_cast<int64_t>(compute_units()) * mode));
+    if (int8) {
+      decode_attention_persistent<D, G, true><<<blocks, kThreads, 0, stream>>>(a);
+    } else {
+      decode_attention_persistent<D, G, false><<<blocks, kThreads, 0, stream>>>(a);
+    }
+    return;
+  }
   const dim3 grid(a.w.max_partitions, a.p.kv.num_kv_heads, a.w.num_items);
   if (int8) {
     decode_attention_kernel<D, G, true><<<grid, kThreads, 0, stream>>>(a);

@@ -42,6 +42,19 @@ def run_attention(torch, K, d_q, q_stride, hq, scale, cache, d_tables, max_block
     return out.cpu().numpy()
 
 
+@pytest.fixture(params=["default", "grid", "persistent"])
+def attention_form(request):
+    """The launcher's two kernel forms: one workgroup per (partition, kv head,
+    item), or persistent workgroups over the in-context units only
+    (RLK_TUNE_ATTN_PERSIST = 0 or workgroups per CU)."""
+    import os
+    env = {"grid": "0", "persistent": "2"}.get(request.param)
+    if env is not None:
+        os.environ["RLK_TUNE_ATTN_PERSIST"] = env
+    yield request.param
+    os.environ.pop("RLK_TUNE_ATTN_PERSIST", None)
+
+
 REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
              (6, 2, 128, False, [700]), (8, 1, 64, False, [48, 17]),
              (8, 2, 128, True, [33, 280]), (4, 2, 64, True, [520])]
@@ -49,12 +62,14 @@ REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
 
 @pytest.mark.parametrize("hq,hkv,D,int8,lens", REF_CASES)
 @pytest.mark.parametrize("static_parts", [False, True])
-def test_decode_attention_reference_geometries(torch_cuda, hq, hkv, D, int8, lens, static_parts):
+def test_decode_attention_reference_geometries(torch_cuda, hq, hkv, D, int8, lens, static_parts,
+                                               attention_form):
     """Every token of every sequence is a decode item attending to its causal
     prefix, over a cache written by rope_and_write_kv (shuffled blocks)."""
     torch = torch_cuda
     from redline_amd import kernels as K
-    say(f"attention hq={hq} hkv={hkv} D={D} int8={int8} lens={lens} static={static_parts}")
+    say(f"attention hq={hq} hkv={hkv} D={D} int8={int8} lens={lens} static={static_parts} "
+        f"form={attention_form}")
     bs = 16
     rng = np.random.default_rng(hq * 7 + D + sum(lens))
     S, T, max_len = len(lens), sum(lens), max(lens)
@@ -112,14 +127,14 @@ def test_decode_attention_reference_geometries(torch_cuda, hq, hkv, D, int8, len
 
 
 @pytest.mark.parametrize("int8", [False, True])
-def test_decode_attention_llama_b32(torch_cuda, int8):
+def test_decode_attention_llama_b32(torch_cuda, int8, attention_form):
     """C2: Llama-3.1-8B decode at batch 32, contexts up to 8192 over a
     16384-block pool (random cache contents); only the decode items' rows of
     `out` are written."""
     torch = torch_cuda
     from redline_amd import kernels as K
     from redline_amd.configs import build_batch, make_workload
-    say(f"attention C2 int8={int8}")
+    say(f"attention C2 int8={int8} form={attention_form}")
     w = make_workload("C2")
     m = w.model
     meta, shape, lay, tables_list = build_batch(w)
