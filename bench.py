@@ -410,6 +410,13 @@ def main():
     from redline_amd.configs import make_workload
     torch.cuda.set_device(0)
 
+    if args.only == "paged_attention_decode" and not args.profile_calls and not args.sweep:
+        w = make_workload(args.workload)
+        for int8 in (False, True):
+            r = attention_bench(torch, K, w, int8, args.reps)
+            print(json.dumps({"workload": w.key, "int8_kv": int8, **r}), flush=True)
+        return
+
     if args.only == "gemv_w4a16_swiglu" and not args.profile_calls:
         res = []
         for m in (1, 8, 16, 32):

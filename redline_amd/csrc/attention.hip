@@ -127,7 +127,10 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
   float (&stat)[kWaves][G] = lds.stat;
   int (&cell_s)[kPart] = lds.cell;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int num_parts = (ctx + kPart - 1) / kPart;
+  // partitions of this context the caller's workspace holds (a smaller
+  // max_partitions than the context needs truncates, and never writes past
+  // the workspace rows)
+  const int num_parts = min((ctx + kPart - 1) / kPart, w.max_partitions);
   const int start = part * kPart;
   const int n = min(kPart, ctx - start);
   const int slot = lane / kLPK;         // key slot of this lane within a wave pass
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     it_tok[i] = tok;
     it_seq[i] = w.item_seq[i];
     it_ctx[i] = ctx;
-    run += (ctx + kPart - 1) / kPart;
+    run += min((ctx + kPart - 1) / kPart, w.max_partitions);
   }
   int incl = run;  // inclusive scan of runs inside the wave
 #pragma unroll
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   for (int ww = 0; ww < wave; ++ww) before += wave_tot[ww];
   for (int i = i0; i < i1; ++i) {
     it_pfx[i] = before;
-    before += (it_ctx[i] + kPart - 1) / kPart;
+    before += min((it_ctx[i] + kPart - 1) / kPart, w.max_partitions);
   }
   if (tid == kThreads - 1) it_pfx[items] = before;
   __syncthreads();
@@ -387,31 +390,64 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   const int token = w.item_token[item];
   const int blk = table_entry(p, w.item_seq[item], part);  // issued before the context is known
   const int ctx = p.positions[token] + 1;
-  if (part >= (ctx + kPart - 1) / kPart) return;  // uniform over the workgroup
+  if (part >= (ctx + kPart - 1) / kPart) return;  // uniform over the workgroup (part < max_partitions)
   attend_unit<D, G, kInt8>(args, s, item, token, ctx, part, kvh, blk);
 }
 
-// Merges the split-K partials of one (item, head): one lane per output dim
+// Merges the split-K partials of one (item, head), one lane per output dim
 // (the merge rule of attention.cu:193-210).  Weight of partition i:
-// exp(m_i - max_j m_j) * l_i.
+// exp(m_i - max_j m_j) * l_i.  The partition statistics are read by all lanes
+// together and the weights kept in LDS; each lane then sums its dim over the
+// partitions with kUnroll partial-row loads in flight.
+constexpr int kReduceMaxParts = 4096;  // weights kept in LDS (contexts up to 1M keys)
+
 template <int D>
 __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
+  constexpr int kUnroll = 8;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
-  const int item = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  __shared__ float wgt[kReduceMaxParts];
+  __shared__ float part_red[D / kWave];
+  const int item = blockIdx.x, h = blockIdx.y, d = threadIdx.x, lane = d % kWave, wv = d / kWave;
   const int token = w.item_token[item];
   const int ctx = p.positions[token] + 1;
-  const int num_parts = (ctx + kPart - 1) / kPart;
-  if (num_parts <= 1) return;
+  const int num_parts = min((ctx + kPart - 1) / kPart, w.max_partitions);
+  if (num_parts <= 1) return;  // uniform: written directly by the attention kernel
   const int64_t base = (static_cast<int64_t>(item) * p.num_heads + h) * w.max_partitions;
+
   float mx = -FLT_MAX;
-  for (int i = 0; i < num_parts; ++i) mx = fmaxf(mx, w.ws_max[base + i]);
-  float total = 0.f, o = 0.f;
-  for (int i = 0; i < num_parts; ++i) {
-    const float wgt = __expf(w.ws_max[base + i] - mx) * w.ws_sum[base + i];
-    total += wgt;
-    o += wgt * w.ws_out[(base + i) * D + d];
+  for (int i = d; i < num_parts; i += D) mx = fmaxf(mx, w.ws_max[base + i]);
+  for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if (lane == 0) part_red[wv] = mx;
+  __syncthreads();
+  mx = part_red[0];
+#pragma unroll
+  for (int i = 1; i < D / kWave; ++i) mx = fmaxf(mx, part_red[i]);
+  __syncthreads();  // part_red is reused below
+  float total = 0.f;
+  for (int i = d; i < num_parts; i += D) {
+    const float g = __expf(w.ws_max[base + i] - mx) * w.ws_sum[base + i];
+    wgt[i] = g;
+    total += g;
   }
+  for (int o = kWave / 2; o > 0; o >>= 1) total += __shfl_xor(total, o, kWave);
+  if (lane == 0) part_red[wv] = total;
+  __syncthreads();
+  total = part_red[0];
+#pragma unroll
+  for (int i = 1; i < D / kWave; ++i) total += part_red[i];
+
+  const float* src = w.ws_out + base * D + d;
+  float o = 0.f;
+  int i = 0;
+  for (; i + kUnroll <= num_parts; i += kUnroll) {
+    float v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = src[static_cast<int64_t>(i + u) * D];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) o += wgt[i + u] * v[u];
+  }
+  for (; i < num_parts; ++i) o += wgt[i] * src[static_cast<int64_t>(i) * D];
   reinterpret_cast<_Float16*>(p.out)[static_cast<int64_t>(token) * p.num_heads * D + h * D + d] =
       static_cast<_Float16>(o / total);
 }
@@ -497,6 +533,9 @@ extern "C" int rlk_paged_attention_decode(const rlk_attention_params* p,
   if (w->max_partitions < 1 || p->kv.block_size <= 0)
     return fail(RLK_EINVAL, "paged_attention_decode: bad max_partitions %d or block size %d",
                 w->max_partitions, p->kv.block_size);
+  if (w->max_partitions > kReduceMaxParts)
+    return fail(RLK_EUNSUPPORTED, "paged_attention_decode: max_partitions %d exceeds %d",
+                w->max_partitions, kReduceMaxParts);
   if (w->max_partitions > 1 && (w->ws_out == nullptr || w->ws_max == nullptr || w->ws_sum == nullptr))
     return fail(RLK_EINVAL, "paged_attention_decode: split-K workspace is required when "
                             "max_partitions > 1");

@@ -203,3 +203,32 @@ def test_decode_attention_items_subset_and_errors(torch_cuda):
         K.paged_attention_decode(p, K.decode_work(dev(torch, items), dev(torch, seqs), 2, 2))
     K.paged_attention_decode(p, K.decode_work(dev(torch, items), dev(torch, seqs), 0, 1))  # no-op
     assert _lib.RLK_DECODE_PARTITION_SIZE == K.kDecodePartitionSize == 256
+
+
+@pytest.mark.parametrize("max_parts", [1, 2])
+def test_decode_attention_short_workspace_truncates(torch_cuda, max_parts, attention_form):
+    """A max_partitions smaller than a context needs (a caller error the
+    reference leaves undefined) attends the first max_partitions * 256 keys
+    and never writes past the workspace -- with max_partitions == 1 no
+    workspace is passed at all."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    say(f"attention short workspace max_parts={max_parts} form={attention_form}")
+    rng = np.random.default_rng(11)
+    hq, hkv, D, bs = 4, 2, 64, 16
+    nb = 50
+    cache = K.KVCache(1, nb, hkv, D, bs)
+    k, v, _, _ = cache.tensors(0)
+    k.copy_(torch.randn(k.shape, device="cuda").half())
+    v.copy_(torch.randn(v.shape, device="cuda").half())
+    T = 2
+    q = randn_f16(rng, (T, hq * D))
+    pos = np.array([699, 100], np.int32)
+    tables = rng.integers(1, nb, (2, 44), dtype=np.int32)  # read only: blocks may repeat
+    items, seqs = np.array([0, 1], np.int32), np.array([0, 1], np.int32)
+    got = run_attention(torch, K, dev(torch, q), hq * D, hq, 0.125, cache, dev(torch, tables), 44,
+                        dev(torch, pos), dev(torch, items), dev(torch, seqs), 2, T, max_parts)
+    cut = np.minimum(pos, max_parts * K.kDecodePartitionSize - 1)
+    want = oracle.paged_attention_decode(q, hq * D, hq, 0.125, k.cpu().numpy(), v.cpu().numpy(),
+                                         None, None, tables, cut, items, seqs, T)
+    assert_close_f16(got, want, what="truncated")
