@@ -55,7 +55,12 @@ class LayerData:
         cos, sin = ra.rope_cos_sin_tables(m.theta, m.head_dim, w.max_pos)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         dtype = K.KVDType.kINT8 if w.kv_int8 else K.KVDType.kFP16
-        self.cache = K.KVCache(1, w.num_blocks, m.hkv, m.head_dim, w.block_size, dtype)
+        self.scale_dtype = K.SCALE_F16 if w.kv_scale_f16 else K.SCALE_F32
+        self.cache = K.KVCache(1, w.num_blocks, m.hkv, m.head_dim, w.block_size, dtype,
+                               scale_dtype=self.scale_dtype)
+        # Qwen2's QKV bias ~N(0, 0.02), added before RoPE by the extension entry point
+        self.bias = ((torch.randn(m.qkv_cols, generator=g, device=dev) * 0.02).half()
+                     if w.qkv_bias else None)
         # enough sets that every kernel's own footprint over the rotation
         # exceeds twice the Infinity Cache
         smallest = min(self.bytes().values())
@@ -93,8 +98,12 @@ class LayerData:
 
     def rope(self, r):
         s, m = self.sets[r], self.w.model
-        self.K.rope_and_write_kv(s["qkv"], s["pos"], s["slot"], self.T, m.hq, self.cos, self.sin,
-                                 self.cache.layer(0))
+        if self.bias is None and self.scale_dtype == self.K.SCALE_F32:
+            self.K.rope_and_write_kv(s["qkv"], s["pos"], s["slot"], self.T, m.hq, self.cos,
+                                     self.sin, self.cache.layer(0))
+        else:  # C4 (fp16 INT8 scales), C5 (QKV bias)
+            self.K.rope_and_write_kv_ex(s["qkv"], s["pos"], s["slot"], self.T, m.hq, self.cos,
+                                        self.sin, self.cache.layer(0), self.bias, self.scale_dtype)
 
     def swiglu(self, r):
         s, m = self.sets[r], self.w.model
@@ -113,7 +122,8 @@ class LayerData:
         return {
             "embedding_lookup": C.bytes_embedding(T, m.hidden),
             "fused_add_rmsnorm": C.bytes_add_rmsnorm(T, m.hidden),
-            "rope_and_write_kv": C.bytes_rope_kv(T, m.hq, m.hkv, m.head_dim, self.w.kv_int8),
+            "rope_and_write_kv": C.bytes_rope_kv(T, m.hq, m.hkv, m.head_dim, self.w.kv_int8,
+                                                 self.w.kv_scale_f16, self.w.qkv_bias),
             "silu_and_mul": C.bytes_swiglu(T, m.inter),
         }
 

@@ -68,6 +68,7 @@ class Workload:
     kv_outlier_dims: int = 0     # per-head channels with N(0, 8) (C4)
     zipf: float = 0.0            # Zipf exponent of token ids (C5), 0 = uniform
     qkv_bias: bool = False       # Qwen2 QKV bias (applied before RoPE)
+    kv_scale_f16: bool = False   # INT8 KV scales stored as fp16 (C4)
     block_size: int = 16
     seed: int = 0
 
@@ -91,7 +92,8 @@ def make_workload(key: str, seed: int = 0) -> Workload:
         return Workload("C3", LLAMA31_8B, segs, outlier_frac=0.01, seed=seed)
     if key == "C4":
         segs = [Segment(0, 4096) for _ in range(4)]
-        return Workload("C4", LLAMA31_8B, segs, kv_int8=True, kv_outlier_dims=2, seed=seed)
+        return Workload("C4", LLAMA31_8B, segs, kv_int8=True, kv_outlier_dims=2, kv_scale_f16=True,
+                        seed=seed)
     if key == "C5":
         segs = [Segment(4096 * i, 4096) for i in range(4)]
         return Workload("C5", QWEN2_7B, segs, num_blocks=16384, max_pos=16384, zipf=1.1,
@@ -156,11 +158,13 @@ def bytes_swiglu(T, I):
     return T * 6 * I
 
 
-def bytes_rope_kv(T, hq, hkv, D, int8=False):
+def bytes_rope_kv(T, hq, hkv, D, int8=False, scale16=False, bias=False):
+    """qkv read, q written back, K/V cells (and INT8 scales) written, cos/sin
+    rows and position/slot read per token; the QKV bias vector once."""
     qkv_read = 2 * (hq + 2 * hkv) * D
     q_write = 2 * hq * D
-    kv_write = (2 * hkv * D + 8 * hkv) if int8 else 4 * hkv * D
-    return T * (qkv_read + q_write + kv_write + 4 * D + 8)
+    kv_write = (2 * hkv * D + (4 if scale16 else 8) * hkv) if int8 else 4 * hkv * D
+    return T * (qkv_read + q_write + kv_write + 4 * D + 8) + (qkv_read if bias else 0)
 
 
 def bytes_decode_attention(contexts, hq, hkv, D, int8=False):

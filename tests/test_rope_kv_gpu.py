@@ -32,14 +32,16 @@ def dev(torch, a):
 
 
 def run_case(torch, qkv, positions, slots, hq, hkv, D, num_blocks, int8, theta=1e4, bs=16,
-             max_pos=None, meta=None, layout=None):
-    """Runs GPU and oracle on the same inputs; returns the GPU cache tensors."""
+             max_pos=None, meta=None, layout=None, bias=None, scale16=False):
+    """Runs GPU and oracle on the same inputs; returns the GPU cache tensors.
+    With a QKV bias or fp16 INT8 scales the extension entry point runs."""
     from redline_amd import kernels as K
     T = positions.size
     max_pos = max_pos or int(positions.max()) + 1
     cos, sin = ra.rope_cos_sin_tables(theta, D, max_pos)
     dtype = K.KVDType.kINT8 if int8 else K.KVDType.kFP16
-    cache = K.KVCache(1, num_blocks, hkv, D, bs, dtype)
+    sdt = K.SCALE_F16 if scale16 else K.SCALE_F32
+    cache = K.KVCache(1, num_blocks, hkv, D, bs, dtype, scale_dtype=sdt)
     d_qkv = dev(torch, qkv)
     if meta is not None:  # the engine's single metadata buffer
         d_meta = dev(torch, meta)
@@ -47,19 +49,24 @@ def run_case(torch, qkv, positions, slots, hq, hkv, D, num_blocks, int8, theta=1
         d_slot = d_meta[layout["slot_mapping"]:layout["slot_mapping"] + T]
     else:
         d_pos, d_slot = dev(torch, positions), dev(torch, slots)
-    K.rope_and_write_kv(d_qkv, d_pos, d_slot, T, hq, dev(torch, cos), dev(torch, sin),
-                        cache.layer(0))
+    if bias is None and not scale16:
+        K.rope_and_write_kv(d_qkv, d_pos, d_slot, T, hq, dev(torch, cos), dev(torch, sin),
+                            cache.layer(0))
+    else:
+        K.rope_and_write_kv_ex(d_qkv, d_pos, d_slot, T, hq, dev(torch, cos), dev(torch, sin),
+                               cache.layer(0), None if bias is None else dev(torch, bias), sdt)
     torch.cuda.synchronize()
 
     # oracle on a cache of the same geometry (zero pages are not materialised)
     shape = (num_blocks, hkv, bs, D)
     kc = np.zeros(shape, np.int8 if int8 else np.float16)
     vc = np.zeros_like(kc)
-    ks = np.zeros(shape[:3], np.float32) if int8 else None
-    vs = np.zeros(shape[:3], np.float32) if int8 else None
+    sc_np = np.uint16 if scale16 else np.float32
+    ks = np.zeros(shape[:3], sc_np) if int8 else None
+    vs = np.zeros(shape[:3], sc_np) if int8 else None
     want_qkv = np.array(qkv, copy=True)
     oracle.rope_and_write_kv(want_qkv, positions, slots, hq, hkv, D, cos, sin, kc, vc, ks, vs,
-                             bs, int8)
+                             bs, int8, bias=bias, scale16=scale16)
     assert_bits_equal(d_qkv.cpu().numpy(), want_qkv, "qkv (q roped in place, k/v untouched)")
 
     # the written cells, bit for bit
@@ -79,6 +86,8 @@ def run_case(torch, qkv, positions, slots, hq, hkv, D, num_blocks, int8, theta=1
     if int8:
         for name, gpu, cpu in (("k_scale", k_s, ks), ("v_scale", v_s, vs)):
             got = gpu.reshape(-1).index_select(0, d_cells).cpu().numpy()
+            if scale16:
+                got = got.view(np.uint16)
             assert_bits_equal(got, cpu.reshape(-1)[cells], name)
             assert int((gpu != 0).sum().item()) == int((got != 0).sum())
     return cache, want_qkv, cells
@@ -190,14 +199,35 @@ def test_rope_kv_workloads_fp16(torch_cuda, key):
              max_pos=w.max_pos, meta=meta, layout=lay)
 
 
-def test_rope_kv_int8_16k_outliers(torch_cuda):
+def test_rope_kv_workload_c5_bias_in_kernel(torch_cuda):
+    """C5 (Qwen2-7B, 16384 tokens): the QKV bias ~N(0, 0.02) added before RoPE
+    by the extension entry point, bit-exact against the oracle's extension."""
+    torch = torch_cuda
+    w = make_workload("C5")
+    m = w.model
+    say("rope workload C5 bias in kernel")
+    meta, shape, lay, _ = build_batch(w)
+    T = w.num_tokens
+    pos = meta[lay["positions"]:lay["positions"] + T].copy()
+    slots = meta[lay["slot_mapping"]:lay["slot_mapping"] + T].copy()
+    rng = np.random.default_rng(13)
+    qkv = randn_f16(rng, (T, m.qkv_cols))
+    bias = randn_f16(rng, (m.qkv_cols,), 0.02)
+    run_case(torch, qkv, pos, slots, m.hq, m.hkv, m.head_dim, w.num_blocks, False, theta=m.theta,
+             max_pos=w.max_pos, meta=meta, layout=lay, bias=bias)
+
+
+@pytest.mark.parametrize("scale16", [False, True])
+def test_rope_kv_int8_16k_outliers(torch_cuda, scale16):
     """C4: 16384 tokens, INT8 KV, K/V ~ N(0,1) with 2 of 128 channels per head
     ~ N(0, 8): codes and scales bit-exact; dequantised cache within 0.51 scale
-    of the fp16 cache written by the FP16 path on the same inputs."""
+    of the fp16 cache written by the FP16 path on the same inputs.  The config
+    stores the scales as fp16 (extension entry point); fp32 is the reference's
+    own format."""
     torch = torch_cuda
     w = make_workload("C4")
     m = w.model
-    say("rope workload C4 int8")
+    say(f"rope workload C4 int8 scale16={scale16}")
     meta, shape, lay, _ = build_batch(w)
     T = w.num_tokens
     pos = meta[lay["positions"]:lay["positions"] + T].copy()
@@ -208,7 +238,8 @@ def test_rope_kv_int8_16k_outliers(torch_cuda):
     qkv[:, m.hq:, dims] = randn_f16(rng, (T, 2 * m.hkv, 2), 8.0)
     qkv = qkv.reshape(T, -1)
     c8, _, cells = run_case(torch, qkv, pos, slots, m.hq, m.hkv, m.head_dim, w.num_blocks, True,
-                            theta=m.theta, max_pos=w.max_pos, meta=meta, layout=lay)
+                            theta=m.theta, max_pos=w.max_pos, meta=meta, layout=lay,
+                            scale16=scale16)
     c16, _, _ = run_case(torch, qkv, pos, slots, m.hq, m.hkv, m.head_dim, w.num_blocks, False,
                          theta=m.theta, max_pos=w.max_pos, meta=meta, layout=lay)
     d_cells = dev(torch, cells.astype(np.int64))
@@ -219,9 +250,13 @@ def test_rope_kv_int8_16k_outliers(torch_cuda):
         codes = q8.reshape(-1, D).index_select(0, d_cells).float()
         scale = sc.reshape(-1).index_select(0, d_cells).float()[:, None]
         ref = f16.reshape(-1, D).index_select(0, d_cells).float()
-        assert bool(((codes * scale - ref).abs() <= 0.51 * scale).all())
         assert bool((codes.abs() <= 127).all())
-        assert bool((codes.abs().amax(1) == 127).all())  # the absmax element maps to +/-127
+        if scale16:  # the scale is fp16(amax/127): amax/scale may round just past 127 (clamped)
+            assert bool(((codes * scale - ref).abs() <= 0.51 * scale + 2e-3 * ref.abs()).all())
+            assert bool((codes.abs().amax(1) >= 126).all())
+        else:
+            assert bool(((codes * scale - ref).abs() <= 0.51 * scale).all())
+            assert bool((codes.abs().amax(1) == 127).all())  # the absmax element maps to +/-127
 
 
 def test_rope_int8_zero_head_scale_one(torch_cuda):
