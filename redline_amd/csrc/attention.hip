@@ -126,7 +126,12 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
   float (&red)[kWaves][G][D] = lds.red;
   float (&stat)[kWaves][G] = lds.stat;
   int (&cell_s)[kPart] = lds.cell;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  // The thread index passes through an empty asm (no instruction) so that the
+  // lane-dependent address arithmetic below is recomputed per unit instead of
+  // being hoisted out of the persistent loop and kept live across it.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
   // partitions of this context the caller's workspace holds (a smaller
   // max_partitions than the context needs truncates, and never writes past
   // the workspace rows)
@@ -139,10 +144,19 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
   // Every key of the partition resolved once to its cache cell (the block-
   // table entry `blk` comes from the caller); the K/V addresses below are
   // then one LDS read each.
+  // For INT8 the thread that owns key `tid` in the softmax below also loads
+  // that key's scales here; they are in flight with the rows and applied once
+  // per key (k scale on the score, v scale folded into the probability).
+  float key_ks = 1.f, key_vs = 1.f;
   if (tid < kPart && blk >= 0) {
     const int bs = p.kv.block_size;
     const int pos = start + tid;
-    cell_s[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
+    const int cell = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
+    cell_s[tid] = cell;
+    if constexpr (kInt8) {
+      key_ks = p.kv.k_scale[cell];
+      key_vs = p.kv.v_scale[cell];
+    }
   }
   // q of the G heads, this lane's 8 elements, kept in fp16 pairs for
   // v_dot2_f32_f16 (the softmax scale is applied to the fp32 dot).
@@ -163,20 +177,18 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
 
   // ---- all K and V rows of this wave in flight at once
   typename R::Raw kr[kPasses], vr[kPasses];
-  float ksc[kPasses], vsc[kPasses];
 #pragma unroll
   for (int u = 0; u < kPasses; ++u) {
     const int64_t cell = cell_of(key_of(u));
     kr[u] = R::load(p.kv.k, cell, D, e0);
     vr[u] = R::load(p.kv.v, cell, D, e0);
-    ksc[u] = kInt8 ? p.kv.k_scale[cell] : 1.f;
-    vsc[u] = kInt8 ? p.kv.v_scale[cell] : 1.f;
   }
   // Keep the scheduler from consuming a row right after its own load (which
   // would wait for each load in turn) and from converting V rows early.
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- phase 1: scores[g][j] = scale * (q_g . k_j) * k_scale_j
+  // ---- phase 1: scores[g][j] = scale * (q_g . k_j)  (the INT8 k scale is
+  // applied in the softmax, by the thread owning key j)
 #pragma unroll
   for (int u = 0; u < kPasses; ++u) {
     const f16x8v k = R::halves(kr[u]);
@@ -194,9 +206,8 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
       dot[g] = group_sum_dpp<kLPK>(d2);
     }
     if (j < n && lane % kLPK == 0) {
-      const float sc = p.scale * ksc[u];
 #pragma unroll
-      for (int g = 0; g < G; ++g) scores[g][j] = dot[g] * sc;
+      for (int g = 0; g < G; ++g) scores[g][j] = dot[g] * p.scale;
     }
   }
   __syncthreads();
@@ -207,7 +218,7 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
     float sv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      sv[g] = tid < n ? scores[g][tid] : -FLT_MAX;
+      sv[g] = tid < n ? (kInt8 ? scores[g][tid] * key_ks : scores[g][tid]) : -FLT_MAX;
       float v = sv[g];
 #pragma unroll
       for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
@@ -225,7 +236,7 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float e = tid < n ? __expf(sv[g] - m[g]) : 0.f;
-      if (tid < n) scores[g][tid] = e;
+      if (tid < n) scores[g][tid] = kInt8 ? e * key_vs : e;  // P . V weight of key tid
       float v = e;
 #pragma unroll
       for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -241,14 +252,14 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
     }
   }
 
-  // ---- phase 2: o[g][e0..e0+7] += p_gj * v_scale_j * v_j
+  // ---- phase 2: o[g][e0..e0+7] += (p_gj * v_scale_j) * v_j
   f32x8 acc[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) acc[g] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < kPasses; ++u) {
     const int j = key_of(u);
-    const float live = j < n ? vsc[u] : 0.f;
+    const float live = j < n ? 1.f : 0.f;
     const f32x8 v = R::floats(vr[u]);
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] += (scores[g][min(j, n - 1)] * live) * v;
@@ -308,7 +319,9 @@ __device__ __forceinline__ int table_entry(const rlk_attention_params& p, int se
 // so one partition's block-table entries serve all kv heads, and the chain of
 // dependent loads per unit is the K/V rows alone.  (Pipelining the next
 // unit's rows into the current unit's registers was measured slower: it needs
-// more than the 128 VGPRs that keep two workgroups per CU.)
+// more than the 128 VGPRs that keep two workgroups per CU.)  The unit body
+// re-derives its lane-dependent addresses per unit (see attend_unit), which
+// keeps the loop within those 128 VGPRs.
 constexpr int kMaxItemsLds = 2048;
 
 template <int D, int G, bool kInt8>
@@ -465,13 +478,12 @@ int compute_units() {
   return cus[dev];
 }
 
-// The persistent form serves FP16 caches (measured faster at C2); INT8 keeps
-// the grid form, where the persistent loop's extra state spills registers.
-// RLK_TUNE_ATTN_PERSIST overrides: workgroups per CU for the persistent form
-// (both dtypes), or 0 for the grid form.
+// The persistent form (two workgroups per CU) serves batches of up to
+// kMaxItemsLds decode items, the grid form larger ones.  RLK_TUNE_ATTN_PERSIST
+// overrides: workgroups per CU for the persistent form, or 0 for the grid form.
 template <int D, int G>
 void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
-  const int mode = tune_knob("RLK_TUNE_ATTN_PERSIST", int8 ? 0 : 2);
+  const int mode = tune_knob("RLK_TUNE_ATTN_PERSIST", 2);
   if (mode > 0 && a.w.num_items <= kMaxItemsLds) {
     const int64_t units = static_cast<int64_t>(a.w.num_items) * a.w.max_partitions * a.p.kv.num_kv_heads;
     const int blocks = static_cast<int>(std::min<int64_t>(units, static_cast<int64_t>(compute_units()) * mode));
