@@ -465,19 +465,6 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
       static_cast<_Float16>(o / total);
 }
 
-int compute_units() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cus[dev] = v;
-  }
-  return cus[dev];
-}
-
 // The persistent form (two workgroups per CU) serves batches of up to
 // kMaxItemsLds decode items, the grid form larger ones.  RLK_TUNE_ATTN_PERSIST
 // overrides: workgroups per CU for the persistent form, or 0 for the grid form.

@@ -59,10 +59,13 @@ struct W4Args {
   int cpp;            // K chunks per x pass (a multiple of K-split ways x ring depth)
   int npass;
   int xstride;        // halves per staged x row
+  int slab_off;       // bytes from the end of x to the first chunk-pair slab
   int y_ld;
 };
 
 constexpr int kModeF16 = 0, kModeF32 = 1, kModeSwiglu = 2;
+constexpr int kSlabRow = 144;                // bytes per slab row: 128 code bytes + 16 pad
+constexpr int kSlabBytes = 16 * kSlabRow;    // one wave's chunk-pair slab
 
 // Codes of one lane for one chunk: 32 K (16 bytes) for 128-K chunks, 8 K
 // (4 bytes) for 32-K chunks.  Weights are read exactly once: non-temporal.
@@ -163,8 +166,20 @@ __device__ __forceinline__ void store_tile(const W4Args& a, f32x4 v, int m0, int
 // times S K-split ways: wave w takes row slot w % wr and K part w / wr.
 // P: chunks in flight per wave; KC: K per chunk (128 or 32); MT: 16-row
 // activation tiles (m <= 16 MT).
-template <int S, int P, int KC, int MT, int MODE>
-__global__ __launch_bounds__(1024) void gemv_w4_kernel(W4Args a) {
+//
+// PR = 2 (128-K chunks, no K split, an even chunk count): codes are fetched
+// as chunk pairs with 8 rows x 128 bytes per load instruction (full cache
+// lines; the MFMA layout itself allows only 16 rows x 64 bytes) and moved to
+// the MFMA layout through a private LDS slab of the wave.
+//
+// At most 8 waves per workgroup (about one workgroup per CU, so two waves per
+// SIMD): a wave may use up to 256 VGPRs, which pays for a deep ring of loads
+// in flight.
+constexpr int kMaxWaves = 8;
+
+template <int S, int P, int KC, int MT, int MODE, int PR = 1>
+__global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
+  static_assert(PR == 1 || (PR == 2 && KC == 128 && S == 1), "chunk pairs: 128-K chunks, no split");
   constexpr int kSteps = KC / 32, kLaneK = KC / 4;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int threads = blockDim.x, wr = threads / (64 * S);
@@ -182,11 +197,26 @@ __global__ __launch_bounds__(1024) void gemv_w4_kernel(W4Args a) {
   // The weight codes of this lane's row travel in a ring of P chunks; part
   // `part` takes chunks part, part + S, part + 2S, ...  The ring is started
   // before scales, offsets and x are staged, so that all are in flight together.
-  const uint8_t* wp = a.w + static_cast<size_t>(rowc) * (a.k / 2) + qd * (kLaneK / 2);
-  u32x4 wbuf[P];
-  auto fetch = [&](int p, int c) { wbuf[p] = load_codes<KC>(wp + static_cast<size_t>(c) * (KC / 2)); };
+  // A ring slot holds PR chunks; slot p of a round starts at chunk
+  // cb + (part + S p) PR.
+  u32x4 wbuf[P][PR];
+  const uint8_t* wp[PR];
+  if constexpr (PR == 1) {
+    wp[0] = a.w + static_cast<size_t>(rowc) * (a.k / 2) + qd * (kLaneK / 2);
+  } else {  // load instruction h covers rows 8h .. 8h+7 of the tile, 8 lanes x 16 bytes each
 #pragma unroll
-  for (int p = 0; p < P; ++p) fetch(p, min(part + S * p, last));
+    for (int h = 0; h < 2; ++h)
+      wp[h] = a.w + static_cast<size_t>(min(row - r16 + 8 * h + lane / 8, a.n - 1)) * (a.k / 2) +
+              (lane % 8) * 16;
+  }
+  const int last_slot = PR == 1 ? last : a.nchunks - PR;  // first chunk of the last slot
+  auto fetch = [&](int p, int c) {
+#pragma unroll
+    for (int h = 0; h < PR; ++h)
+      wbuf[p][h] = load_codes<KC>(wp[h] + static_cast<size_t>(c) * (KC / 2));
+  };
+#pragma unroll
+  for (int p = 0; p < P; ++p) fetch(p, min((part + S * p) * PR, last_slot));
 
   // Both staging loops keep kBatch loads in flight before their LDS writes
   // (indices clamped so the loads are unconditional).  Scales and offsets go
@@ -250,12 +280,20 @@ __global__ __launch_bounds__(1024) void gemv_w4_kernel(W4Args a) {
   constexpr f16x8 kOnes = {1, 1, 1, 1, 1, 1, 1, 1};
   const uint32_t magic = opaque(0x54005400u);  // 64.0 in both halves
 
-  // Rounds of P chunks per part.  A pass holds cpp chunks, a multiple of S*P,
-  // so pass boundaries fall on round boundaries for every part alike.
-  const int rounds = (a.nchunks + S * P - 1) / (S * P);
+  // The wave's private slab for chunk-pair transposes (after x and the
+  // split-K reduction space): 16 rows of 128 code bytes, rows padded to 144
+  // bytes so that both the row-major writes and the MFMA-layout reads are
+  // free of bank conflicts.
+  uint8_t* slab = reinterpret_cast<uint8_t*>(x_lds + static_cast<size_t>(a.m) * a.xstride) +
+                  a.slab_off + wave * kSlabBytes;
+
+  // Rounds of P slots per part.  A pass holds cpp chunks, a multiple of
+  // S*P*PR, so pass boundaries fall on round boundaries for every part alike.
+  constexpr int kRound = S * P * PR;
+  const int rounds = (a.nchunks + kRound - 1) / kRound;
   int c0 = 0;  // first chunk of the staged pass
   for (int rd = 0; rd < rounds; ++rd) {
-    const int cb = rd * S * P;
+    const int cb = rd * kRound;
     if (cb % a.cpp == 0) {  // workgroup-uniform
       if (cb > 0) {
         __syncthreads();  // every wave is done with the previous pass's x
@@ -266,38 +304,54 @@ __global__ __launch_bounds__(1024) void gemv_w4_kernel(W4Args a) {
     }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int c = cb + part + S * p;
-      if (c < a.nchunks) {  // wave-uniform: only the last round has idle slots
-        f16x8 xa[MT][kSteps];
-        f32x4 xs[MT];
+      const int cs = cb + (part + S * p) * PR;
+      if (cs < a.nchunks) {  // wave-uniform: only the last round has idle slots
+        u32x4 words[PR];
+        if constexpr (PR == 1) {
+          words[0] = wbuf[p][0];
+        } else {  // row-major pair -> MFMA layout (lane (qd, r16): row r16, 16 bytes at qd)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<u32x4*>(slab + (8 * h + lane / 8) * kSlabRow + (lane % 8) * 16) =
+                wbuf[p][h];
 #pragma unroll
-          for (int j = 0; j < kSteps; ++j) {
-            xa[mt][j] = *reinterpret_cast<const f16x8*>(xl[mt] + (c - c0) * KC + 8 * j);
-            xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], kOnes, xs[mt], 0, 0, 0);
+          for (int h = 0; h < 2; ++h)
+            words[h] = *reinterpret_cast<const u32x4*>(slab + r16 * kSlabRow + h * 64 + qd * 16);
+        }
+#pragma unroll
+        for (int h = 0; h < PR; ++h) {
+          const int c = cs + h;
+          f16x8 xa[MT][kSteps];
+          f32x4 xs[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kSteps; ++j) {
+              xa[mt][j] = *reinterpret_cast<const f16x8*>(xl[mt] + (c - c0) * KC + 8 * j);
+              xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], kOnes, xs[mt], 0, 0, 0);
+            }
+          }
+          const uint32_t so = so_lds[(c * KC / a.group_size) * rows_wg + slot * 16 + r16];
+          const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
+          const float of = fmaf(-kCodeBias, sc,
+                                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16))));
+          f16x8 q[kSteps];
+#pragma unroll
+          for (int j = 0; j < kSteps; ++j) q[j] = codes_f16(words[h][j], magic);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kSteps; ++j)
+              d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], q[j], d, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(of, xs[mt][e], fmaf(sc, d[e], acc[mt][e]));
           }
         }
-        const uint32_t so = so_lds[(c * KC / a.group_size) * rows_wg + slot * 16 + r16];
-        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
-        const float of = fmaf(-kCodeBias, sc,
-                              static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16))));
-        f16x8 q[kSteps];
-#pragma unroll
-        for (int j = 0; j < kSteps; ++j) q[j] = codes_f16(wbuf[p][j], magic);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int j = 0; j < kSteps; ++j)
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], q[j], d, 0, 0, 0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(of, xs[mt][e], fmaf(sc, d[e], acc[mt][e]));
-        }
       }
-      // refill the slot with this part's chunk one round ahead
-      fetch(p, min(c + S * P, last));
+      // refill the slot with this part's chunks one round ahead
+      fetch(p, min(cs + kRound, last_slot));
     }
   }
 
@@ -325,33 +379,22 @@ __global__ __launch_bounds__(1024) void gemv_w4_kernel(W4Args a) {
 constexpr size_t kLdsBudget = 160 * 1024;
 constexpr int kNoFit = 1;  // launch(): the policy's smallest x pass exceeds the LDS budget
 
-int compute_units() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cus[dev] = v;
-  }
-  return cus[dev];
-}
-
-template <int S, int P, int KC, int MT, int MODE>
+template <int S, int P, int KC, int MT, int MODE, int PR = 1>
 int launch(W4Args a, int wr_max, hipStream_t stream) {
+  if (PR == 2 && a.nchunks % 2 != 0) return kNoFit;
   // Row waves per workgroup: enough that the grid is about one workgroup per
   // compute unit, so x is staged about once per CU.
   const int tiles = (a.n + 15) / 16;
   const int cus = compute_units();
-  const int wr = std::max(1, std::min(std::min(wr_max, 16 / S), (tiles + cus - 1) / cus));
+  const int wr = std::max(1, std::min(std::min(wr_max, kMaxWaves / S), (tiles + cus - 1) / cus));
   const size_t red_bytes = static_cast<size_t>(S - 1) * wr * MT * kWave * sizeof(f32x4);
   const size_t so_bytes = static_cast<size_t>(a.groups) * 16 * wr * 4;
-  const size_t fixed = red_bytes + so_bytes;
-  const size_t min_x = static_cast<size_t>(a.m) * (S * P * KC + 8) * 2;
+  const size_t slab_bytes = PR == 2 ? static_cast<size_t>(wr) * S * kSlabBytes : 0;
+  const size_t fixed = red_bytes + so_bytes + slab_bytes;
+  const size_t unit = static_cast<size_t>(S) * P * PR;  // chunks per round
+  const size_t min_x = static_cast<size_t>(a.m) * (unit * KC + 8) * 2;
   if (fixed + min_x > kLdsBudget) return kNoFit;
-  // chunks per x pass: as many as fit, balanced over the passes, a multiple of S*P
-  const size_t unit = static_cast<size_t>(S) * P;
+  // chunks per x pass: as many as fit, balanced over the passes, a multiple of a round
   const size_t fit =
       ((kLdsBudget - fixed) / (2 * static_cast<size_t>(a.m)) - 8) / KC / unit * unit;
   const int npass = static_cast<int>((a.nchunks + fit - 1) / fit);
@@ -359,44 +402,53 @@ int launch(W4Args a, int wr_max, hipStream_t stream) {
   a.cpp = static_cast<int>((per + unit - 1) / unit * unit);
   a.npass = (a.nchunks + a.cpp - 1) / a.cpp;
   a.xstride = a.cpp * KC + 8;
+  a.slab_off = static_cast<int>(red_bytes);
   const size_t lds = fixed + static_cast<size_t>(a.m) * a.xstride * 2;
-  auto kernel = gemv_w4_kernel<S, P, KC, MT, MODE>;
+  auto kernel = gemv_w4_kernel<S, P, KC, MT, MODE, PR>;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(lds));
-    if (e != hipSuccess)
-      return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
-                  hipGetErrorString(e));
+    // dynamic LDS above 64 KiB must be granted per kernel and device; the
+    // grant is remembered so that steady-state launches make no extra call
+    static size_t granted[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || granted[dev] < lds) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(kLdsBudget));
+      if (e != hipSuccess)
+        return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
+                    hipGetErrorString(e));
+      if (dev >= 0 && dev < 64) granted[dev] = kLdsBudget;
+    }
   }
   const int blocks = (tiles + wr - 1) / wr;
   kernel<<<blocks, 64 * wr * S, lds, stream>>>(a);
   return RLK_OK;
 }
 
-// Launch policies (K-split ways, chunks in flight per wave, most row waves per
-// workgroup); entry 0 -- no split, 8 chunks in flight -- is the default, the others are selectable for tuning
-// sweeps through RLK_TUNE_W4_CFG.  32-K chunks always use the default.
+// Launch policies (K-split ways, slots in flight per wave, most row waves per
+// workgroup, chunks per slot); entry 0 -- no split, 4 chunk pairs (8 chunks)
+// in flight -- is the default, the others are selectable for tuning sweeps
+// through RLK_TUNE_W4_CFG.  32-K chunks always use the single-chunk default.
 template <int KC, int MT, int MODE>
 int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
   int st = kNoFit;
   if constexpr (KC == 128) {
     switch (cfg) {
-      case 1: st = launch<2, 8, KC, MT, MODE>(a, 8, s); break;
-      case 2: st = launch<2, 4, KC, MT, MODE>(a, 8, s); break;
-      case 3: st = launch<4, 4, KC, MT, MODE>(a, 4, s); break;
-      case 4: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
-      case 5: st = launch<1, 8, KC, MT, MODE>(a, 4, s); break;
-      case 6: st = launch<4, 2, KC, MT, MODE>(a, 4, s); break;
-      case 7: st = launch<2, 8, KC, MT, MODE>(a, 2, s); break;
-      default: break;
+      case 1: st = launch<1, 8, KC, MT, MODE>(a, 8, s); break;
+      case 2: st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s); break;
+      case 3: st = launch<1, 6, KC, MT, MODE, 2>(a, 8, s); break;
+      case 4: st = launch<1, 16, KC, MT, MODE>(a, 8, s); break;
+      case 5: st = launch<1, 12, KC, MT, MODE>(a, 8, s); break;
+      case 6: st = launch<1, 8, KC, MT, MODE, 2>(a, 4, s); break;
+      case 7: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
+      default: st = launch<1, 4, KC, MT, MODE, 2>(a, 8, s); break;
     }
   }
   (void)cfg;
-  // the default, then shallower rings when x passes do not fit
-  if (st == kNoFit) st = launch<1, 8, KC, MT, MODE>(a, 16, s);
-  if (st == kNoFit) st = launch<1, 4, KC, MT, MODE>(a, 16, s);
-  if (st == kNoFit) st = launch<1, 2, KC, MT, MODE>(a, 16, s);
+  // single-chunk slots, then shallower rings when x passes do not fit
+  if (st == kNoFit) st = launch<1, 8, KC, MT, MODE>(a, 8, s);
+  if (st == kNoFit) st = launch<1, 4, KC, MT, MODE>(a, 8, s);
+  if (st == kNoFit) st = launch<1, 2, KC, MT, MODE>(a, 8, s);
   if (st == kNoFit)
     return fail(RLK_EUNSUPPORTED, "gemv_w4a16: k=%d does not fit the LDS budget", a.k);
   return st;

@@ -27,6 +27,19 @@ int launch_status(const char* what) {
   return fail(static_cast<int>(e), "%s: kernel launch failed: %s", what, hipGetErrorString(e));
 }
 
+int compute_units() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;  // the same value from any thread
+  }
+  return cus[dev];
+}
+
 int tune_knob(const char* name, int fallback) {
   const char* v = std::getenv(name);
   if (v == nullptr || *v == '\0') return fallback;

@@ -16,6 +16,10 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // naming `what`.
 int launch_status(const char* what);
 
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int compute_units();
+
 // Environment override of a launch-policy knob (tuning experiments only);
 // returns `fallback` when the variable is unset.
 int tune_knob(const char* name, int fallback);

@@ -77,7 +77,7 @@ def test_gemv_w4_reference_geometry(torch_cuda, g, m):
     assert_close_f16(got16, want.astype(np.float16), what="gemv fp16")
 
 
-@pytest.mark.parametrize("g,k", [(64, 256), (128, 512), (32, 96)])
+@pytest.mark.parametrize("g,k", [(64, 256), (128, 512), (32, 96), (128, 640)])
 @pytest.mark.parametrize("m", [1, 3, 8, 16, 20, 32])
 def test_gemv_w4_swiglu_interleaved_rows(torch_cuda, g, k, m):
     """gemv_w4a16_swiglu_interleaved_rows: [gate; up] quantised, rows interleaved
