@@ -99,11 +99,64 @@ __device__ __forceinline__ float group_sum_dpp(float v) {
 // LDS of one work unit.
 template <int D, int G>
 struct UnitLds {
-  float scores[G][kPart];
-  float red[kWaves][G][D];
-  float stat[kWaves][G];
-  int cell[kPart];  // cache cell of each key of the partition
+  float red[kWaves][G][D];   // each wave's P . V partial
+  float stat[kWaves][G][2];  // each wave's (max, sum) per head
+  int cell[kPart];           // cache cell of each key of the partition
 };
+
+// The 64 / N key slots of a wave (lanes l, l + N, l + 2N, ...) combined,
+// every lane receiving the result.  Slots 16 and 32 lanes apart are paired by
+// the gfx950 permlane swaps (VALU, no LDS): a swap of v with a copy of itself
+// leaves v and its partner in the two registers.  The instruction writes both
+// operands; the compiler's builtin exposes only one of them, so it is issued
+// as asm on two in/out operands, after the two wait states a VALU write needs
+// before a permlane read.  Slots 8 apart (N = 8) are paired by a DPP rotation
+// by 8 within each row of 16.
+template <bool k32>
+__device__ __forceinline__ void swap_rows(float v, float& a, float& b) {
+  unsigned x = __builtin_bit_cast(unsigned, v), y = x;
+  if constexpr (k32) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  } else {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  }
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+__device__ __forceinline__ float swap16_sum(float v) {
+  float a, b;
+  swap_rows<false>(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+  float a, b;
+  swap_rows<true>(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float swap16_max(float v) {
+  float a, b;
+  swap_rows<false>(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float swap32_max(float v) {
+  float a, b;
+  swap_rows<true>(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float ror8(float v) {  // row_ror:8
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128,
+                                                               0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ float slots_sum(float v) {
+  if constexpr (N == 8) v += ror8(v);
+  return swap32_sum(swap16_sum(v));
+}
+template <int N>
+__device__ __forceinline__ float slots_max(float v) {
+  if constexpr (N == 8) v = fmaxf(v, ror8(v));
+  return swap32_max(swap16_max(v));
+}
 
 // One work unit = one (item, kv head, 256-key partition), processed by the 8
 // waves of the workgroup.  `blk` is this thread's block-table entry for key
@@ -122,9 +175,8 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
   using R = Row<kInt8>;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
-  float (&scores)[G][kPart] = lds.scores;
   float (&red)[kWaves][G][D] = lds.red;
-  float (&stat)[kWaves][G] = lds.stat;
+  float (&stat)[kWaves][G][2] = lds.stat;
   int (&cell_s)[kPart] = lds.cell;
   // The thread index passes through an empty asm (no instruction) so that the
   // lane-dependent address arithmetic below is recomputed per unit instead of
@@ -144,19 +196,10 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
   // Every key of the partition resolved once to its cache cell (the block-
   // table entry `blk` comes from the caller); the K/V addresses below are
   // then one LDS read each.
-  // For INT8 the thread that owns key `tid` in the softmax below also loads
-  // that key's scales here; they are in flight with the rows and applied once
-  // per key (k scale on the score, v scale folded into the probability).
-  float key_ks = 1.f, key_vs = 1.f;
   if (tid < kPart && blk >= 0) {
     const int bs = p.kv.block_size;
     const int pos = start + tid;
-    const int cell = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
-    cell_s[tid] = cell;
-    if constexpr (kInt8) {
-      key_ks = p.kv.k_scale[cell];
-      key_vs = p.kv.v_scale[cell];
-    }
+    cell_s[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
   }
   // q of the G heads, this lane's 8 elements, kept in fp16 pairs for
   // v_dot2_f32_f16 (the softmax scale is applied to the fp32 dot).
@@ -175,25 +218,28 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
   auto key_of = [&](int pass) { return (pass * kWaves + wave) * kKPP + slot; };
   auto cell_of = [&](int j) -> int64_t { return cell_s[min(j, n - 1)]; };
 
-  // ---- all K and V rows of this wave in flight at once
+  // ---- all K and V rows of this wave (and INT8 scales) in flight at once
   typename R::Raw kr[kPasses], vr[kPasses];
+  float ksc[kPasses], vsc[kPasses];
 #pragma unroll
   for (int u = 0; u < kPasses; ++u) {
     const int64_t cell = cell_of(key_of(u));
     kr[u] = R::load(p.kv.k, cell, D, e0);
     vr[u] = R::load(p.kv.v, cell, D, e0);
+    ksc[u] = kInt8 ? p.kv.k_scale[cell] : 1.f;
+    vsc[u] = kInt8 ? p.kv.v_scale[cell] : 1.f;
   }
   // Keep the scheduler from consuming a row right after its own load (which
   // would wait for each load in turn) and from converting V rows early.
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- phase 1: scores[g][j] = scale * (q_g . k_j)  (the INT8 k scale is
-  // applied in the softmax, by the thread owning key j)
+  // ---- scores of this wave's keys, in registers: s = scale * (q_g . k_j) * k_scale_j
+  // (every lane of a key holds its score after the DPP reduction)
+  float sc[kPasses][G];
 #pragma unroll
   for (int u = 0; u < kPasses; ++u) {
     const f16x8v k = R::halves(kr[u]);
-    const int j = key_of(u);
-    float dot[G];
+    const bool valid = key_of(u) < n;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float d2 = 0.f;
@@ -203,89 +249,77 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
         const f16x2 b = {k[x], k[x + 1]};
         d2 = __builtin_amdgcn_fdot2(a, b, d2, false);
       }
-      dot[g] = group_sum_dpp<kLPK>(d2);
-    }
-    if (j < n && lane % kLPK == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) scores[g][j] = dot[g] * p.scale;
-    }
-  }
-  __syncthreads();
-
-  // ---- softmax statistics per head: thread t < 256 owns key t
-  float m[G], l[G];
-  {
-    float sv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      sv[g] = tid < n ? (kInt8 ? scores[g][tid] * key_ks : scores[g][tid]) : -FLT_MAX;
-      float v = sv[g];
-#pragma unroll
-      for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-      if (lane == 0) stat[wave][g] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float v = stat[0][g];
-#pragma unroll
-      for (int ww = 1; ww < kWaves; ++ww) v = fmaxf(v, stat[ww][g]);
-      m[g] = v;
-    }
-    __syncthreads();  // stat is reused below
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float e = tid < n ? __expf(sv[g] - m[g]) : 0.f;
-      if (tid < n) scores[g][tid] = kInt8 ? e * key_vs : e;  // P . V weight of key tid
-      float v = e;
-#pragma unroll
-      for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-      if (lane == 0) stat[wave][g] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float v = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) v += stat[ww][g];
-      l[g] = v;
+      const float dot = group_sum_dpp<kLPK>(d2);
+      sc[u][g] = valid ? dot * (p.scale * ksc[u]) : -FLT_MAX;
     }
   }
 
-  // ---- phase 2: o[g][e0..e0+7] += (p_gj * v_scale_j) * v_j
+  // ---- softmax over this wave's keys (flash-decoding inside the workgroup):
+  // the wave's own max and sum, combined across waves at the output
+  float mw[G], lw[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float v = sc[0][g];
+#pragma unroll
+    for (int u = 1; u < kPasses; ++u) v = fmaxf(v, sc[u][g]);
+    mw[g] = slots_max<kLPK>(v);
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float v = 0.f;
+#pragma unroll
+    for (int u = 0; u < kPasses; ++u) {
+      const float e = key_of(u) < n ? __expf(sc[u][g] - mw[g]) : 0.f;
+      sc[u][g] = e;  // the probability (unnormalised) replaces the score
+      v += e;
+    }
+    lw[g] = slots_sum<kLPK>(v);
+  }
+
+  // ---- P . V: o[g][e0..e0+7] += (p_gj * v_scale_j) * v_j, then the key slots folded
   f32x8 acc[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) acc[g] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < kPasses; ++u) {
-    const int j = key_of(u);
-    const float live = j < n ? 1.f : 0.f;
     const f32x8 v = R::floats(vr[u]);
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] += (scores[g][min(j, n - 1)] * live) * v;
+    for (int g = 0; g < G; ++g) acc[g] += (sc[u][g] * vsc[u]) * v;
   }
-  // fold the key slots of the wave (lanes e0-equal, slot-different)
 #pragma unroll
-  for (int o = kLPK; o < kWave; o <<= 1) {
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int x = 0; x < 8; ++x) acc[g][x] += __shfl_xor(acc[g][x], o, kWave);
-  }
+    for (int x = 0; x < 8; ++x) acc[g][x] = slots_sum<kLPK>(acc[g][x]);
   if (slot == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int x = 0; x < 8; ++x) red[wave][g][e0 + x] = acc[g][x];
   }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      stat[wave][g][0] = mw[g];
+      stat[wave][g][1] = lw[g];
+    }
+  }
   __syncthreads();
 
+  // ---- combine the waves: M = max m_w, L = sum e^(m_w - M) l_w,
+  // o = sum e^(m_w - M) o_w / L
   for (int i = tid; i < G * D; i += kThreads) {
     const int g = i / D, d = i % D;
-    float o = 0.f;
+    float M = stat[0][g][0];
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) o += red[ww][g][d];
-    o /= l[g];
+    for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, stat[ww][g][0]);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float f = __expf(stat[ww][g][0] - M);
+      L += f * stat[ww][g][1];
+      o += f * red[ww][g][d];
+    }
+    o /= L;
     const int h = kvh * G + g;
     if (num_parts == 1) {
       reinterpret_cast<_Float16*>(p.out)[static_cast<int64_t>(token) * p.num_heads * D + h * D + d] =
@@ -294,8 +328,8 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
       const int64_t row = (static_cast<int64_t>(item) * p.num_heads + h) * w.max_partitions + part;
       w.ws_out[row * D + d] = o;
       if (d == 0) {
-        w.ws_max[row] = m[g];
-        w.ws_sum[row] = l[g];
+        w.ws_max[row] = M;
+        w.ws_sum[row] = L;
       }
     }
   }
