@@ -78,24 +78,6 @@ struct Row<true> {  // 8 int8 codes, 8 bytes
   }
 };
 
-// v + the value of the lane picked by DPP control CTRL (within 16-lane rows).
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                           0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over aligned groups of N (8 or 16) lanes, every lane receiving it: four
-// (three) DPP-modified adds, no LDS traffic.
-template <int N>
-__device__ __forceinline__ float group_sum_dpp(float v) {
-  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]: pairs
-  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]: quads
-  v = dpp_add<0x141>(v);  // row_half_mirror: groups of 8
-  if constexpr (N == 16) v = dpp_add<0x140>(v);  // row_mirror: groups of 16
-  return v;
-}
-
 // LDS of one work unit.
 template <int D, int G>
 struct UnitLds {
@@ -105,57 +87,19 @@ struct UnitLds {
 };
 
 // The 64 / N key slots of a wave (lanes l, l + N, l + 2N, ...) combined,
-// every lane receiving the result.  Slots 16 and 32 lanes apart are paired by
-// the gfx950 permlane swaps (VALU, no LDS): a swap of v with a copy of itself
-// leaves v and its partner in the two registers.  The instruction writes both
-// operands; the compiler's builtin exposes only one of them, so it is issued
-// as asm on two in/out operands, after the two wait states a VALU write needs
-// before a permlane read.  Slots 8 apart (N = 8) are paired by a DPP rotation
-// by 8 within each row of 16.
-template <bool k32>
-__device__ __forceinline__ void swap_rows(float v, float& a, float& b) {
-  unsigned x = __builtin_bit_cast(unsigned, v), y = x;
-  if constexpr (k32) {
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-  } else {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-  }
-  a = __builtin_bit_cast(float, x);
-  b = __builtin_bit_cast(float, y);
-}
-__device__ __forceinline__ float swap16_sum(float v) {
-  float a, b;
-  swap_rows<false>(v, a, b);
-  return a + b;
-}
-__device__ __forceinline__ float swap32_sum(float v) {
-  float a, b;
-  swap_rows<true>(v, a, b);
-  return a + b;
-}
-__device__ __forceinline__ float swap16_max(float v) {
-  float a, b;
-  swap_rows<false>(v, a, b);
-  return fmaxf(a, b);
-}
-__device__ __forceinline__ float swap32_max(float v) {
-  float a, b;
-  swap_rows<true>(v, a, b);
-  return fmaxf(a, b);
-}
-__device__ __forceinline__ float ror8(float v) {  // row_ror:8
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128,
-                                                               0xF, 0xF, false));
-}
+// every lane receiving the result: slots 16 and 32 lanes apart through the
+// permlane row swaps, slots 8 apart (N = 8) through a DPP rotation by 8
+// within each row of 16.
+__device__ __forceinline__ float ror8(float v) { return dpp<0x128>(v); }  // row_ror:8
 template <int N>
 __device__ __forceinline__ float slots_sum(float v) {
   if constexpr (N == 8) v += ror8(v);
-  return swap32_sum(swap16_sum(v));
+  return rows_sum<true>(rows_sum<false>(v));
 }
 template <int N>
 __device__ __forceinline__ float slots_max(float v) {
   if constexpr (N == 8) v = fmaxf(v, ror8(v));
-  return swap32_max(swap16_max(v));
+  return rows_max<true>(rows_max<false>(v));
 }
 
 // One work unit = one (item, kv head, 256-key partition), processed by the 8
@@ -249,7 +193,7 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
         const f16x2 b = {k[x], k[x + 1]};
         d2 = __builtin_amdgcn_fdot2(a, b, d2, false);
       }
-      const float dot = group_sum_dpp<kLPK>(d2);
+      const float dot = group_sum<kLPK>(d2);
       sc[u][g] = valid ? dot * (p.scale * ksc[u]) : -FLT_MAX;
     }
   }
@@ -464,7 +408,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
 
   float mx = -FLT_MAX;
   for (int i = d; i < num_parts; i += D) mx = fmaxf(mx, w.ws_max[base + i]);
-  for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  mx = rows_max<true>(rows_max<false>(group_max<16>(mx)));
   if (lane == 0) part_red[wv] = mx;
   __syncthreads();
   mx = part_red[0];
@@ -477,7 +421,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
     wgt[i] = g;
     total += g;
   }
-  for (int o = kWave / 2; o > 0; o >>= 1) total += __shfl_xor(total, o, kWave);
+  total = wave_sum(total);
   if (lane == 0) part_red[wv] = total;
   __syncthreads();
   total = part_red[0];

@@ -46,19 +46,69 @@ __device__ __forceinline__ float silu_f16(float g) {
   return round_f16(__fdividef(g, 1.0f + __expf(-g)));
 }
 
-// Butterfly reductions over all 64 lanes of a wavefront; every lane gets the result.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// ---- cross-lane reductions without LDS.  Inside rows of 16 lanes they use
+// DPP (quad_perm, row_half_mirror, row_mirror); across rows the gfx950
+// v_permlane16/32_swap VALU instructions.  __shfl_xor by 16 or 32 would
+// compile to ds_bpermute, an LDS round trip per step.
+
+// v as read from the lane that DPP control CTRL selects (within rows of 16).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                0xF, 0xF, false));
+}
+
+// Sum / max over aligned groups of N lanes (N = 2, 4, 8 or 16), every lane
+// receiving the result.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]: pairs
+  if constexpr (N >= 4) v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]: quads
+  if constexpr (N >= 8) v += dpp<0x141>(v);   // row_half_mirror: groups of 8
+  if constexpr (N >= 16) v += dpp<0x140>(v);  // row_mirror: groups of 16
+  return v;
+}
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, dpp<0xB1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<0x4E>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<0x141>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<0x140>(v));
   return v;
 }
 
-// Max over aligned groups of G consecutive lanes (G a power of two <= 64).
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+// A swap of the rows of v (16 or 32 lanes apart) with a copy of itself: the
+// two registers then hold v and its partner, in some order.  The instruction
+// writes both operands; the compiler's builtin exposes only one of them, so
+// it is issued as asm on two in/out operands, after the two wait states a
+// VALU write needs before a permlane read.
+template <bool k32>
+__device__ __forceinline__ void swap_rows(float v, float& a, float& b) {
+  unsigned x = __builtin_bit_cast(unsigned, v), y = x;
+  if constexpr (k32) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  } else {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  }
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+template <bool k32>
+__device__ __forceinline__ float rows_sum(float v) {
+  float a, b;
+  swap_rows<k32>(v, a, b);
+  return a + b;
+}
+template <bool k32>
+__device__ __forceinline__ float rows_max(float v) {
+  float a, b;
+  swap_rows<k32>(v, a, b);
+  return fmaxf(a, b);
+}
+
+// Sum over all 64 lanes of a wavefront; every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) {
+  return rows_sum<true>(rows_sum<false>(group_sum<16>(v)));
 }
 
 __device__ __forceinline__ u32x4 load16(const void* p) {
