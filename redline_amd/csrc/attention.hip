@@ -46,8 +46,22 @@ struct AttnArgs {
 
 };
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+// 8 int8 codes to fp16, exactly: each code + 128 (the sign bit flipped)
+// becomes the low byte of an fp16 whose high byte is 0x64, i.e. the value
+// 1024 + code + 128 (fp16 spacing is 1 on [1024, 2048)); one packed fp16
+// subtract of 1152 leaves the code.  4 byte permutes + 4 packed subtracts
+// for 8 codes.
+__device__ __forceinline__ f16x8 codes_f16(u32x2 r) {
+  const uint32_t lo = r.x ^ 0x80808080u, hi = r.y ^ 0x80808080u;
+  // v_perm_b32 selectors: bytes 0-3 of the second source, 4 = byte 0 of the
+  // first (0x64)
+  const u32x4 w = {__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
+                   __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
+  return __builtin_bit_cast(f16x8, w) - static_cast<_Float16>(1152);
+}
 
 template <bool kInt8>
 struct Row;
@@ -58,7 +72,7 @@ struct Row<false> {  // 8 fp16 elements, 16 bytes
   __device__ static Raw load(const void* base, int64_t cell, int D, int e0) {
     return ld16<true>(reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + cell * D + e0));
   }
-  __device__ static f16x8v halves(Raw r) { return __builtin_bit_cast(f16x8v, r); }
+  __device__ static f16x8 halves(Raw r) { return __builtin_bit_cast(f16x8, r); }
   __device__ static f32x8 floats(Raw r) { return unpack8(r); }
 };
 
@@ -69,21 +83,10 @@ struct Row<true> {  // 8 int8 codes, 8 bytes
     return __builtin_nontemporal_load(
         reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(base) + cell * D + e0));
   }
-  // |code| <= 127 is exact in fp16
-  __device__ static f16x8v halves(Raw r) {
-    return __builtin_convertvector(__builtin_bit_cast(i8x8, r), f16x8v);
-  }
+  __device__ static f16x8 halves(Raw r) { return codes_f16(r); }
   __device__ static f32x8 floats(Raw r) {
     return __builtin_convertvector(__builtin_bit_cast(i8x8, r), f32x8);
   }
-};
-
-// LDS of one work unit.
-template <int D, int G>
-struct UnitLds {
-  float red[kWaves][G][D];   // each wave's P . V partial
-  float stat[kWaves][G][2];  // each wave's (max, sum) per head
-  int cell[kPart];           // cache cell of each key of the partition
 };
 
 // The 64 / N key slots of a wave (lanes l, l + N, l + 2N, ...) combined,
@@ -102,155 +105,291 @@ __device__ __forceinline__ float slots_max(float v) {
   return rows_max<true>(rows_max<false>(v));
 }
 
-// One work unit = one (item, kv head, 256-key partition), processed by the 8
-// waves of the workgroup.  `blk` is this thread's block-table entry for key
-// `tid` of the partition (threads tid < 256; -1 past the table).  Each wave
-// owns kPasses passes of kKPP keys; all of its K and V rows are requested
-// before the first is used, so a workgroup keeps its whole partition (256
-// keys x 2 rows) in flight at once.  Starts and ends with every thread of the
-// workgroup.
-template <int D, int G, bool kInt8>
-__device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>& lds, int item,
-                                            int token, int ctx, int part, int kvh, int blk) {
-  constexpr int kLPK = D / 8;             // lanes per key row (16 or 8)
-  constexpr int kKPP = kWave / kLPK;      // keys per wave pass
-  constexpr int kKPB = kKPP * kWaves;     // keys per workgroup pass
-  constexpr int kPasses = kPart / kKPB;   // passes over a full partition (8 or 4)
-  using R = Row<kInt8>;
-  const rlk_attention_params& p = args.p;
-  const rlk_decode_attention_work& w = args.w;
-  float (&red)[kWaves][G][D] = lds.red;
-  float (&stat)[kWaves][G][2] = lds.stat;
-  int (&cell_s)[kPart] = lds.cell;
-  // The thread index passes through an empty asm (no instruction) so that the
-  // lane-dependent address arithmetic below is recomputed per unit instead of
-  // being hoisted out of the persistent loop and kept live across it.
+// ---- one work unit = one (item, kv head, 256-key partition), processed by
+// the 8 waves of a workgroup in stages.  A wave owns kPasses passes of kKPP
+// keys (key j of pass u is (u * kWaves + wave) * kKPP + slot); the K rows of
+// a unit and its V rows are two separate batches of loads, so the persistent
+// form can keep one batch in flight while it computes with the other.
+
+template <int D>
+struct Geo {
+  static constexpr int kLPK = D / 8;             // lanes per key row (16 or 8)
+  static constexpr int kKPP = kWave / kLPK;      // keys per wave pass
+  static constexpr int kPasses = kPart / (kKPP * kWaves);  // 8 or 4
+};
+
+// This thread's coordinates inside a unit.  The thread index passes through
+// an empty asm (no instruction) so that the lane-dependent address arithmetic
+// is re-derived per unit rather than hoisted out of the persistent loop and
+// kept live across it.
+struct LaneCoord {
+  int tid, wave, slot, e0;
+};
+template <int D>
+__device__ __forceinline__ LaneCoord lane_coord() {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
-  // partitions of this context the caller's workspace holds (a smaller
-  // max_partitions than the context needs truncates, and never writes past
-  // the workspace rows)
-  const int num_parts = min((ctx + kPart - 1) / kPart, w.max_partitions);
-  const int start = part * kPart;
-  const int n = min(kPart, ctx - start);
-  const int slot = lane / kLPK;         // key slot of this lane within a wave pass
-  const int e0 = (lane % kLPK) * 8;     // first element of the row owned by this lane
+  const int lane = tid % kWave;
+  return {tid, __builtin_amdgcn_readfirstlane(tid / kWave), lane / Geo<D>::kLPK,
+          (lane % Geo<D>::kLPK) * 8};
+}
+template <int D>
+__device__ __forceinline__ int key_of(const LaneCoord& c, int pass) {
+  return (pass * kWaves + c.wave) * Geo<D>::kKPP + c.slot;
+}
 
-  // Every key of the partition resolved once to its cache cell (the block-
-  // table entry `blk` comes from the caller); the K/V addresses below are
-  // then one LDS read each.
-  if (tid < kPart && blk >= 0) {
-    const int bs = p.kv.block_size;
-    const int pos = start + tid;
-    cell_s[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
-  }
-  // q of the G heads, this lane's 8 elements, kept in fp16 pairs for
-  // v_dot2_f32_f16 (the softmax scale is applied to the fp32 dot).
-  f16x8v q[G];
-  {
-    const _Float16* qrow = reinterpret_cast<const _Float16*>(p.q) +
-                           static_cast<int64_t>(token) * p.q_stride + (kvh * G) * D + e0;
+// The K (or V) rows of this thread's keys and their INT8 scales, in flight.
+template <int D, bool kInt8>
+struct RowBatch {
+  typename Row<kInt8>::Raw r[Geo<D>::kPasses];
+  float s[Geo<D>::kPasses];
+};
+
+// Requests every row of this thread's keys of a unit whose first `n` keys
+// are in context (cells: the unit's cache cells, in LDS).  Slots past the
+// context re-read the last valid row (a cache hit) and are masked out later,
+// which keeps every load unconditional.
+template <int D, bool kInt8>
+__device__ __forceinline__ void issue_rows(RowBatch<D, kInt8>& rb, const void* base,
+                                           const float* scales, const int* cells, int n,
+                                           const LaneCoord& c) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) q[g] = __builtin_bit_cast(f16x8v, load16(qrow + g * D));
+  for (int u = 0; u < Geo<D>::kPasses; ++u) {
+    const int64_t cell = cells[min(key_of<D>(c, u), n - 1)];
+    rb.r[u] = Row<kInt8>::load(base, cell, D, c.e0);
+    rb.s[u] = kInt8 ? scales[cell] : 1.f;
   }
-  __syncthreads();
-
-  // Key j of pass u for this lane; slots past the context re-read the last
-  // valid row (a cache hit) and are masked out of the results, which keeps
-  // every load unconditional.
-  auto key_of = [&](int pass) { return (pass * kWaves + wave) * kKPP + slot; };
-  auto cell_of = [&](int j) -> int64_t { return cell_s[min(j, n - 1)]; };
-
-  // ---- all K and V rows of this wave (and INT8 scales) in flight at once
-  typename R::Raw kr[kPasses], vr[kPasses];
-  float ksc[kPasses], vsc[kPasses];
-#pragma unroll
-  for (int u = 0; u < kPasses; ++u) {
-    const int64_t cell = cell_of(key_of(u));
-    kr[u] = R::load(p.kv.k, cell, D, e0);
-    vr[u] = R::load(p.kv.v, cell, D, e0);
-    ksc[u] = kInt8 ? p.kv.k_scale[cell] : 1.f;
-    vsc[u] = kInt8 ? p.kv.v_scale[cell] : 1.f;
-  }
-  // Keep the scheduler from consuming a row right after its own load (which
-  // would wait for each load in turn) and from converting V rows early.
+  // keeps the scheduler from moving the batch next to its first use
   __builtin_amdgcn_sched_barrier(0);
+}
 
-  // ---- scores of this wave's keys, in registers: s = scale * (q_g . k_j) * k_scale_j
-  // (every lane of a key holds its score after the DPP reduction)
-  float sc[kPasses][G];
+// ---- q . k on the matrix cores.  For each of the wave's two tiles of 16 keys
+// one v_mfma_f32_16x16x32_f16 per 32 dims multiplies K (A: 16 keys x 32
+// dims) by q (B: 32 dims x 16 columns, column g = head g of the group, the
+// columns past G zero).  Lane l supplies A row l % 16 and B column l % 16 at
+// k-slot l / 16, and receives D rows 4 (l / 16) + i, column l % 16.
+//
+// The keys are numbered so that D lands where P . V needs it: tile t, row
+// 4 rho + i is key (slot rho, pass 4t + i) for 16 lanes per key (D = 128) and
+// (slot 2 rho + t, pass i) for 8 (D = 64).  Lane (rho, g) then holds head g's
+// scores of keys its own row of 16 lanes consumes in P . V, and a DPP row
+// broadcast of lane g hands head g's probability to the whole row.
+template <int D>
+__device__ __forceinline__ int mma_slot(int t, int r) {
+  return Geo<D>::kLPK == 16 ? r / 4 : 2 * (r / 4) + t;
+}
+template <int D>
+__device__ __forceinline__ int mma_pass(int t, int r) {
+  return Geo<D>::kLPK == 16 ? 4 * t + r % 4 : r % 4;
+}
+template <int D>
+__device__ __forceinline__ int mma_key(const LaneCoord& c, int t, int r) {
+  return (mma_pass<D>(t, r) * kWaves + c.wave) * Geo<D>::kKPP + mma_slot<D>(t, r);
+}
+
+// K rows of a unit in the matrix-core layout: per tile, lane (j, r) holds the
+// 16-byte pieces [64 x + 16 j, +16) of key row r's bytes (x < kLoads), which
+// are k-slot j of one (fp16) or two (int8, 8 codes each) MFMA steps; plus
+// the INT8 k scales of the 8 keys whose scores the lane receives.
+template <int D, bool kInt8>
+struct KBatch {
+  static constexpr int kLoads = D * (kInt8 ? 1 : 2) / 64;
+  u32x4 r[2][kLoads];
+  float s[8];
+};
+
+// dims of MFMA step `step` held at k-slot j
+template <int D, bool kInt8>
+__device__ __forceinline__ int step_dim(int step, int j) {
+  return kInt8 ? 64 * (step / 2) + 16 * j + 8 * (step % 2) : 32 * step + 8 * j;
+}
+
+template <int D, bool kInt8>
+__device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* base,
+                                           const float* scales, const int* cells, int n,
+                                           const LaneCoord& c) {
+  const int lane = c.tid % kWave, r = lane % 16, j = lane / 16;
+  constexpr int kRowBytes = D * (kInt8 ? 1 : 2);
 #pragma unroll
-  for (int u = 0; u < kPasses; ++u) {
-    const f16x8v k = R::halves(kr[u]);
-    const bool valid = key_of(u) < n;
+  for (int t = 0; t < 2; ++t) {
+    const int64_t cell = cells[min(mma_key<D>(c, t, r), n - 1)];
+    const char* row = static_cast<const char*>(base) + cell * kRowBytes + 16 * j;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float d2 = 0.f;
+    for (int x = 0; x < KBatch<D, kInt8>::kLoads; ++x)
+      kb.r[t][x] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 64 * x));
+  }
 #pragma unroll
-      for (int x = 0; x < 8; x += 2) {
-        const f16x2 a = {q[g][x], q[g][x + 1]};
-        const f16x2 b = {k[x], k[x + 1]};
-        d2 = __builtin_amdgcn_fdot2(a, b, d2, false);
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      kb.s[4 * t + i] = kInt8 ? scales[cells[min(mma_key<D>(c, t, 4 * j + i), n - 1)]] : 1.f;
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// v of lane `g` of each row of 16, to the whole row (DPP row_newbcast)
+__device__ __forceinline__ float row_bcast(float v, int g) {
+  switch (g) {
+    case 0: return dpp<0x150>(v);
+    case 1: return dpp<0x151>(v);
+    case 2: return dpp<0x152>(v);
+    case 3: return dpp<0x153>(v);
+    case 4: return dpp<0x154>(v);
+    case 5: return dpp<0x155>(v);
+    case 6: return dpp<0x156>(v);
+    default: return dpp<0x157>(v);
+  }
+}
+
+// Scores s = scale * (q_g . k) * k_scale on the matrix cores, then the
+// softmax over the wave's keys per head: p = exp(s - m_g) (0 past the
+// context), with the wave's max m and sum l per head stored to stat[wave]
+// (flash-decoding inside the workgroup; the waves are combined at the
+// output).  The probabilities leave in the P . V layout, passes 2h and 2h + 1
+// of this lane's key slot as fp16 pairs per head: the operands of
+// v_dot2_f32_f16.
+template <int D, int G, bool kInt8>
+__device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _Float16* qs,
+                                            float scale, int n, const LaneCoord& c,
+                                            f16x2 (&pp)[Geo<D>::kPasses / 2][G],
+                                            float (&stat)[kWaves][G][2]) {
+  constexpr int kSteps = D / 32, kP = Geo<D>::kPasses;
+  const int lane = c.tid % kWave, g = lane % 16, rho = lane / 16;
+  f16x8 qb[kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    qb[st] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (g < G) qb[st] = *reinterpret_cast<const f16x8*>(qs + g * D + step_dim<D, kInt8>(st, rho));
+  }
+  float e[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      f16x8 a;
+      if constexpr (kInt8) {
+        const u32x4 w = kb.r[t][st / 2];
+        a = codes_f16(st % 2 ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
+      } else {
+        a = __builtin_bit_cast(f16x8, kb.r[t][st]);
       }
-      const float dot = group_sum<kLPK>(d2);
-      sc[u][g] = valid ? dot * (p.scale * ksc[u]) : -FLT_MAX;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      e[t][i] = mma_key<D>(c, t, 4 * rho + i) < n ? acc[i] * (scale * kb.s[4 * t + i]) : -FLT_MAX;
+  }
+  float m = e[0][0];
+#pragma unroll
+  for (int x = 1; x < 8; ++x) m = fmaxf(m, e[x / 4][x % 4]);
+  m = rows_max<true>(rows_max<false>(m));
+  float l = 0.f;
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    const float v = mma_key<D>(c, x / 4, 4 * rho + x % 4) < n ? __expf(e[x / 4][x % 4] - m) : 0.f;
+    e[x / 4][x % 4] = v;
+    l += v;
+  }
+  l = rows_sum<true>(rows_sum<false>(l));
+  if (rho == 0 && g < G) {
+    stat[c.wave][g][0] = m;
+    stat[c.wave][g][1] = l;
+  }
+  // to the P . V layout: pass u of this lane's key slot is (t, i) = (u / 4,
+  // u % 4) of its row (D = 128), or (t, i) = (half of the row, u) (D = 64)
+#pragma unroll
+  for (int h = 0; h < kP / 2; ++h)
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+      float pr[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int u = 2 * h + k;
+        if constexpr (Geo<D>::kLPK == 16) {
+          pr[k] = row_bcast(e[u / 4][u % 4], gg);
+        } else {
+          const float x0 = row_bcast(e[0][u], gg), x1 = row_bcast(e[1][u], gg);
+          pr[k] = (lane % 16) < 8 ? x0 : x1;
+        }
+      }
+      pp[h][gg] = f16x2{static_cast<_Float16>(pr[0]), static_cast<_Float16>(pr[1])};
+    }
+}
+
+// P . V for this thread's 8 output dims and G heads, fp32 accumulation of
+// v_dot2_f32_f16 over pairs of keys; then the wave's key slots are summed and
+// the wave's partial output written to red[wave].
+//
+// The slot sum is a transpose-reduction: one permlane16 swap of two values
+// followed by one add leaves the sum over a pair of rows of the first value
+// in even rows and of the second in odd rows, so each level halves the
+// values a lane carries.  After the row-pair (16 lanes) and row-half (32
+// lanes) levels, row r holds the wave-wide sum of flat value 4i + r
+// (flat = g * 8 + x) as z[i].  With 8 lanes per key (D = 64) the two slots
+// of a row are first summed by a DPP rotation.
+template <int D, int G, bool kInt8>
+__device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb,
+                                        const f16x2 (&pp)[Geo<D>::kPasses / 2][G], const LaneCoord& c,
+                                        float (&red)[kWaves][G][D]) {
+  constexpr int kP = Geo<D>::kPasses, kN = G * 8;
+  float v[kN];
+#pragma unroll
+  for (int i = 0; i < kN; ++i) v[i] = 0.f;
+#pragma unroll
+  for (int h = 0; h < kP / 2; ++h) {
+    const f16x8 va = Row<kInt8>::halves(vb.r[2 * h]), vb2 = Row<kInt8>::halves(vb.r[2 * h + 1]);
+    f16x2 ph[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) ph[g] = pp[h][g];
+    if constexpr (kInt8) {  // p * v_scale, per key
+      const f16x2 vs = {static_cast<_Float16>(vb.s[2 * h]), static_cast<_Float16>(vb.s[2 * h + 1])};
+#pragma unroll
+      for (int g = 0; g < G; ++g) ph[g] *= vs;
+    }
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      const f16x2 vv = {va[x], vb2[x]};
+#pragma unroll
+      for (int g = 0; g < G; ++g) v[g * 8 + x] = __builtin_amdgcn_fdot2(ph[g], vv, v[g * 8 + x], false);
     }
   }
-
-  // ---- softmax over this wave's keys (flash-decoding inside the workgroup):
-  // the wave's own max and sum, combined across waves at the output
-  float mw[G], lw[G];
+  if constexpr (Geo<D>::kLPK == 8) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float v = sc[0][g];
-#pragma unroll
-    for (int u = 1; u < kPasses; ++u) v = fmaxf(v, sc[u][g]);
-    mw[g] = slots_max<kLPK>(v);
+    for (int i = 0; i < kN; ++i) v[i] += ror8(v[i]);
   }
+  float w[kN / 2];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float v = 0.f;
-#pragma unroll
-    for (int u = 0; u < kPasses; ++u) {
-      const float e = key_of(u) < n ? __expf(sc[u][g] - mw[g]) : 0.f;
-      sc[u][g] = e;  // the probability (unnormalised) replaces the score
-      v += e;
-    }
-    lw[g] = slots_sum<kLPK>(v);
+  for (int i = 0; i < kN / 2; ++i) {
+    float a = v[2 * i], b = v[2 * i + 1];
+    swap_rows_pair<false>(a, b);
+    w[i] = a + b;
   }
-
-  // ---- P . V: o[g][e0..e0+7] += (p_gj * v_scale_j) * v_j, then the key slots folded
-  f32x8 acc[G];
+  float z[kN / 4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-  for (int u = 0; u < kPasses; ++u) {
-    const f32x8 v = R::floats(vr[u]);
-#pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] += (sc[u][g] * vsc[u]) * v;
+  for (int i = 0; i < kN / 4; ++i) {
+    float a = w[2 * i], b = w[2 * i + 1];
+    swap_rows_pair<true>(a, b);
+    z[i] = a + b;
   }
+  const int lane = c.tid % kWave, r = lane / 16;
+  if (Geo<D>::kLPK == 16 || lane % 16 < 8) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int x = 0; x < 8; ++x) acc[g][x] = slots_sum<kLPK>(acc[g][x]);
-  if (slot == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int x = 0; x < 8; ++x) red[wave][g][e0 + x] = acc[g][x];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      stat[wave][g][0] = mw[g];
-      stat[wave][g][1] = lw[g];
+    for (int i = 0; i < kN / 4; ++i) {
+      const int f = 4 * i + r;
+      red[c.wave][f / 8][c.e0 + f % 8] = z[i];
     }
   }
-  __syncthreads();
+}
 
-  // ---- combine the waves: M = max m_w, L = sum e^(m_w - M) l_w,
-  // o = sum e^(m_w - M) o_w / L
+// Combines the waves of a unit: M = max m_w, L = sum e^(m_w - M) l_w,
+// o = sum e^(m_w - M) o_w / L; written as the output row (one partition) or
+// as the unit's split-K partial row.
+template <int D, int G>
+__device__ __forceinline__ void combine_waves(const AttnArgs& args, const float (&red)[kWaves][G][D],
+                                              const float (&stat)[kWaves][G][2], int tid, int item,
+                                              int token, int num_parts, int part, int kvh) {
+  const rlk_attention_params& p = args.p;
+  const rlk_decode_attention_work& w = args.w;
   for (int i = tid; i < G * D; i += kThreads) {
     const int g = i / D, d = i % D;
     float M = stat[0][g][0];
@@ -277,14 +416,46 @@ __device__ __forceinline__ void attend_unit(const AttnArgs& args, UnitLds<D, G>&
       }
     }
   }
-  __syncthreads();  // the unit's LDS may be reused
+}
+
+// LDS of the unit stages.  cells and q are double-buffered in the persistent
+// form (the next unit's are written while the current one computes).
+template <int D, int G>
+struct UnitLds {
+  float red[kWaves][G][D];   // each wave's P . V partial
+  float stat[kWaves][G][2];  // each wave's (max, sum) per head
+  int cell[2][kPart];        // cache cell of each key of the partition
+  alignas(16) _Float16 q[2][G * D];
+};
+
+// Cache cells of a partition's keys, from this thread's block-table entry
+// `blk` for key `tid` (threads tid < 256; blk < 0 past the table).
+__device__ __forceinline__ void write_cells(int* cells, const rlk_attention_params& p, int tid,
+                                            int blk, int part, int kvh) {
+  if (tid < kPart && blk >= 0) {
+    const int bs = p.kv.block_size;
+    const int pos = part * kPart + tid;
+    cells[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
+  }
+}
+
+// q of the G heads of a kv head: G * D fp16 contiguous in the token's row,
+// one 16-byte piece per thread kPart <= tid < kPart + G * D / 8.
+template <int D, int G>
+__device__ __forceinline__ bool q_piece(int tid) {
+  return tid >= kPart && tid < kPart + G * D / 8;
+}
+template <int D, int G>
+__device__ __forceinline__ u32x4 load_q_piece(const rlk_attention_params& p, int tid, int token, int kvh) {
+  const _Float16* q = reinterpret_cast<const _Float16*>(p.q) + static_cast<int64_t>(token) * p.q_stride +
+                      kvh * G * D + (tid - kPart) * 8;
+  return load16(q);
 }
 
 // Block-table entry of key `tid` of a partition (threads tid < 256), or -1
 // past the table.  Table rows are padded with block 0, so every entry inside
 // the row is a valid block.
-__device__ __forceinline__ int table_entry(const rlk_attention_params& p, int seq, int part) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ int table_entry(const rlk_attention_params& p, int tid, int seq, int part) {
   const int bi = (part * kPart + tid) / p.kv.block_size;
   if (tid >= kPart || bi >= p.max_blocks_per_seq) return -1;
   return p.block_tables[static_cast<int64_t>(seq) * p.max_blocks_per_seq + bi];
@@ -293,17 +464,23 @@ __device__ __forceinline__ int table_entry(const rlk_attention_params& p, int se
 // Persistent form.  Every workgroup first reads each decode item's token,
 // sequence and context into LDS and prefix-sums the partitions per item; the
 // work units (item, partition, kv head) -- only those inside a context -- are
-// then split into contiguous ranges, one per workgroup.  Kv head runs fastest,
-// so one partition's block-table entries serve all kv heads, and the chain of
-// dependent loads per unit is the K/V rows alone.  (Pipelining the next
-// unit's rows into the current unit's registers was measured slower: it needs
-// more than the 128 VGPRs that keep two workgroups per CU.)  The unit body
-// re-derives its lane-dependent addresses per unit (see attend_unit), which
-// keeps the loop within those 128 VGPRs.
+// then split into contiguous ranges, one per workgroup.  Kv head runs fastest.
+//
+// The units of a range are software-pipelined across their two row batches:
+//   wait K(n) -> scores and softmax -> request K(n+1) -> wait V(n) -> P . V
+//   -> barrier -> combine; write cells(n+2) and q(n+1) -> barrier -> request V(n+1)
+// so one batch is always in flight while the other is consumed, in the same
+// registers a non-pipelined unit needs (cells and q of later units are
+// staged in LDS, their block-table entries and q requested one unit ahead).
 constexpr int kMaxItemsLds = 2048;
+
+struct UnitPos {
+  int item, part, kvh;
+};
 
 template <int D, int G, bool kInt8>
 __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_persistent(AttnArgs args) {
+  constexpr int kP = Geo<D>::kPasses;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ UnitLds<D, G> s;
@@ -349,40 +526,102 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   const int u0 = blockIdx.x * chunk, u1 = min(u0 + chunk, total);
   if (u0 >= u1) return;
   // first unit: binary search of its partition among the items
-  int pu = u0 / hkv, kvh = u0 - pu * hkv;
+  const int pu = u0 / hkv;
   int lo = 0, hi = items - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) / 2;
     if (it_pfx[mid] <= pu) lo = mid; else hi = mid - 1;
   }
-  int item = lo, part = pu - it_pfx[item];
-  int blk = table_entry(p, it_seq[item], part);
-  for (int u = u0; u < u1; ++u) {
-    attend_unit<D, G, kInt8>(args, s, item, it_tok[item], it_ctx[item], part, kvh, blk);
-    if (++kvh == hkv) {
-      kvh = 0;
-      if (++part == it_pfx[item + 1] - it_pfx[item]) {
-        part = 0;
-        ++item;
+  auto advance = [&](UnitPos q) {
+    if (++q.kvh == hkv) {
+      q.kvh = 0;
+      if (++q.part == it_pfx[q.item + 1] - it_pfx[q.item]) {
+        q.part = 0;
+        ++q.item;
       }
-      if (u + 1 < u1) blk = table_entry(p, it_seq[item], part);
     }
+    return q;
+  };
+  auto keys_in = [&](const UnitPos& q) { return min(kPart, it_ctx[q.item] - q.part * kPart); };
+  auto num_parts = [&](const UnitPos& q) {
+    return min((it_ctx[q.item] + kPart - 1) / kPart, w.max_partitions);
+  };
+
+  UnitPos cur = {lo, pu - it_pfx[lo], u0 - pu * hkv};
+  UnitPos nxt = u0 + 1 < u1 ? advance(cur) : cur;
+  write_cells(s.cell[0], p, tid, table_entry(p, tid, it_seq[cur.item], cur.part), cur.part, cur.kvh);
+  if (u0 + 1 < u1)
+    write_cells(s.cell[1], p, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part), nxt.part, nxt.kvh);
+  if (q_piece<D, G>(tid))
+    store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, it_tok[cur.item], cur.kvh));
+  __syncthreads();
+
+  KBatch<D, kInt8> kb;
+  RowBatch<D, kInt8> vb;
+  {
+    const LaneCoord c = lane_coord<D>();
+    issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[0], keys_in(cur), c);
+    issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[0], keys_in(cur), c);
+  }
+  for (int u = u0; u < u1; ++u) {
+    const int b = (u - u0) & 1;
+    const bool has1 = u + 1 < u1, has2 = u + 2 < u1;
+    const UnitPos nn = has2 ? advance(nxt) : nxt;
+    const LaneCoord c = lane_coord<D>();
+    // block-table entries of unit n+2 and the q piece of unit n+1, consumed
+    // after the first barrier
+    const int blk2 = has2 ? table_entry(p, c.tid, it_seq[nn.item], nn.part) : -1;
+    u32x4 qn = {0, 0, 0, 0};
+    if (has1 && q_piece<D, G>(c.tid)) qn = load_q_piece<D, G>(p, c.tid, it_tok[nxt.item], nxt.kvh);
+
+    f16x2 pp[kP / 2][G];
+    wave_softmax<D, G, kInt8>(kb, s.q[b], p.scale, keys_in(cur), c, pp, s.stat);
+    // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
+    if (has1 && q_piece<D, G>(c.tid)) store16(s.q[b ^ 1] + (c.tid - kPart) * 8, qn);
+    if (has1) issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[b ^ 1], keys_in(nxt), c);
+    wave_pv<D, G, kInt8>(vb, pp, c, s.red);
+    __syncthreads();
+
+    // cells(n+2) go to the buffer cells(n) used: free once every wave has
+    // requested V(n), i.e. after this barrier
+    if (has2) write_cells(s.cell[b], p, c.tid, blk2, nn.part, nn.kvh);
+    combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
+                        cur.part, cur.kvh);
+    __syncthreads();
+    if (has1) issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[b ^ 1], keys_in(nxt), c);
+    cur = nxt;
+    nxt = nn;
   }
 }
 
 // Grid form: one workgroup per (partition, kv head, item), exiting at once
-// when the partition lies past the item's context.
+// when the partition lies past the item's context; the same stages, in order.
 template <int D, int G, bool kInt8>
 __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_kernel(AttnArgs args) {
+  constexpr int kP = Geo<D>::kPasses;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ UnitLds<D, G> s;
-  const int part = blockIdx.x, kvh = blockIdx.y, item = blockIdx.z;
+  const int part = blockIdx.x, kvh = blockIdx.y, item = blockIdx.z, tid = threadIdx.x;
   const int token = w.item_token[item];
-  const int blk = table_entry(p, w.item_seq[item], part);  // issued before the context is known
+  const int blk = table_entry(p, tid, w.item_seq[item], part);  // issued before the context is known
   const int ctx = p.positions[token] + 1;
   if (part >= (ctx + kPart - 1) / kPart) return;  // uniform over the workgroup (part < max_partitions)
-  attend_unit<D, G, kInt8>(args, s, item, token, ctx, part, kvh, blk);
+  const int n = min(kPart, ctx - part * kPart);
+  write_cells(s.cell[0], p, tid, blk, part, kvh);
+  if (q_piece<D, G>(tid)) store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, token, kvh));
+  __syncthreads();
+  const LaneCoord c = lane_coord<D>();
+  KBatch<D, kInt8> kb;
+  RowBatch<D, kInt8> vb;
+  issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[0], n, c);
+  issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[0], n, c);
+  f16x2 pp[kP / 2][G];
+  wave_softmax<D, G, kInt8>(kb, s.q[0], p.scale, n, c, pp, s.stat);
+  wave_pv<D, G, kInt8>(vb, pp, c, s.red);
+  __syncthreads();
+  combine_waves<D, G>(args, s.red, s.stat, tid, item, token,
+                      min((ctx + kPart - 1) / kPart, w.max_partitions), part, kvh);
 }
 
 // Merges the split-K partials of one (item, head), one lane per output dim

@@ -77,14 +77,15 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
-// A swap of the rows of v (16 or 32 lanes apart) with a copy of itself: the
-// two registers then hold v and its partner, in some order.  The instruction
-// writes both operands; the compiler's builtin exposes only one of them, so
-// it is issued as asm on two in/out operands, after the two wait states a
-// VALU write needs before a permlane read.
+// One v_permlane16_swap_b32 (k32 false) or v_permlane32_swap_b32 (k32 true)
+// on a and b: the odd rows (16 lanes) or the upper half (32 lanes) of a trade
+// places with the even rows or lower half of b.  The instruction writes both
+// operands; the compiler's builtin exposes only one of them, so it is issued
+// as asm on two in/out operands, after the two wait states a VALU write needs
+// before a permlane read.
 template <bool k32>
-__device__ __forceinline__ void swap_rows(float v, float& a, float& b) {
-  unsigned x = __builtin_bit_cast(unsigned, v), y = x;
+__device__ __forceinline__ void swap_rows_pair(float& a, float& b) {
+  unsigned x = __builtin_bit_cast(unsigned, a), y = __builtin_bit_cast(unsigned, b);
   if constexpr (k32) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
   } else {
@@ -92,6 +93,14 @@ __device__ __forceinline__ void swap_rows(float v, float& a, float& b) {
   }
   a = __builtin_bit_cast(float, x);
   b = __builtin_bit_cast(float, y);
+}
+// A swap of the rows of v with a copy of itself: the two registers then hold
+// v and its partner (16 or 32 lanes apart), in some order.
+template <bool k32>
+__device__ __forceinline__ void swap_rows(float v, float& a, float& b) {
+  a = v;
+  b = v;
+  swap_rows_pair<k32>(a, b);
 }
 template <bool k32>
 __device__ __forceinline__ float rows_sum(float v) {
