@@ -246,12 +246,13 @@ __device__ __forceinline__ float row_bcast(float v, int g) {
 // (flash-decoding inside the workgroup; the waves are combined at the
 // output).  The probabilities leave in the P . V layout, passes 2h and 2h + 1
 // of this lane's key slot as fp16 pairs per head: the operands of
-// v_dot2_f32_f16.
-template <int D, int G, bool kInt8>
+// v_dot2_f32_f16.  `then` runs once the K rows are consumed (the persistent
+// form requests the next unit's K rows into the same registers there).
+template <int D, int G, bool kInt8, class Then>
 __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _Float16* qs,
                                             float scale, int n, const LaneCoord& c,
                                             f16x2 (&pp)[Geo<D>::kPasses / 2][G],
-                                            float (&stat)[kWaves][G][2]) {
+                                            float (&stat)[kWaves][G][2], Then then) {
   constexpr int kSteps = D / 32, kP = Geo<D>::kPasses;
   const int lane = c.tid % kWave, g = lane % 16, rho = lane / 16;
   f16x8 qb[kSteps];
@@ -260,10 +261,11 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
     qb[st] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     if (g < G) qb[st] = *reinterpret_cast<const f16x8*>(qs + g * D + step_dim<D, kInt8>(st, rho));
   }
-  float e[2][4];
+  f32x4 acc[2];
+  float ks[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       f16x8 a;
@@ -273,12 +275,18 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
       } else {
         a = __builtin_bit_cast(f16x8, kb.r[t][st]);
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], acc, 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], acc[t], 0, 0, 0);
     }
+  }
+#pragma unroll
+  for (int x = 0; x < 8; ++x) ks[x] = kb.s[x];
+  then();
+  float e[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      e[t][i] = mma_key<D>(c, t, 4 * rho + i) < n ? acc[i] * (scale * kb.s[4 * t + i]) : -FLT_MAX;
-  }
+      e[t][i] = mma_key<D>(c, t, 4 * rho + i) < n ? acc[t][i] * (scale * ks[4 * t + i]) : -FLT_MAX;
   float m = e[0][0];
 #pragma unroll
   for (int x = 1; x < 8; ++x) m = fmaxf(m, e[x / 4][x % 4]);
@@ -327,10 +335,13 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
 // lanes) levels, row r holds the wave-wide sum of flat value 4i + r
 // (flat = g * 8 + x) as z[i].  With 8 lanes per key (D = 64) the two slots
 // of a row are first summed by a DPP rotation.
-template <int D, int G, bool kInt8>
+// `then` runs once the V rows are consumed and the first level of the slot
+// sum has halved the accumulators (the persistent form requests the next
+// unit's V rows into the same registers there).
+template <int D, int G, bool kInt8, class Then>
 __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb,
                                         const f16x2 (&pp)[Geo<D>::kPasses / 2][G], const LaneCoord& c,
-                                        float (&red)[kWaves][G][D]) {
+                                        float (&red)[kWaves][G][D], Then then) {
   constexpr int kP = Geo<D>::kPasses, kN = G * 8;
   float v[kN];
 #pragma unroll
@@ -364,6 +375,7 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb,
     swap_rows_pair<false>(a, b);
     w[i] = a + b;
   }
+  then();  // after the first level, with half the accumulators live
   float z[kN / 4];
 #pragma unroll
   for (int i = 0; i < kN / 4; ++i) {
@@ -467,11 +479,13 @@ __device__ __forceinline__ int table_entry(const rlk_attention_params& p, int ti
 // then split into contiguous ranges, one per workgroup.  Kv head runs fastest.
 //
 // The units of a range are software-pipelined across their two row batches:
-//   wait K(n) -> scores and softmax -> request K(n+1) -> wait V(n) -> P . V
-//   -> barrier -> combine; write cells(n+2) and q(n+1) -> barrier -> request V(n+1)
-// so one batch is always in flight while the other is consumed, in the same
-// registers a non-pipelined unit needs (cells and q of later units are
-// staged in LDS, their block-table entries and q requested one unit ahead).
+//   wait K(n) -> q . k -> request K(n+1) -> softmax -> wait V(n) -> P . V
+//   -> request V(n+1) -> slot sums -> barrier -> combine, write cells(n+2)
+//   -> barrier
+// so each batch is requested as soon as its registers are free and one is
+// always in flight while the other is consumed, in the registers a
+// non-pipelined unit needs.  Cells and q of later units are staged in LDS
+// (double-buffered), their block-table entries and q requested a unit ahead.
 constexpr int kMaxItemsLds = 2048;
 
 struct UnitPos {
@@ -575,11 +589,14 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     if (has1 && q_piece<D, G>(c.tid)) qn = load_q_piece<D, G>(p, c.tid, it_tok[nxt.item], nxt.kvh);
 
     f16x2 pp[kP / 2][G];
-    wave_softmax<D, G, kInt8>(kb, s.q[b], p.scale, keys_in(cur), c, pp, s.stat);
+    wave_softmax<D, G, kInt8>(kb, s.q[b], p.scale, keys_in(cur), c, pp, s.stat, [&] {
+      if (has1) issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[b ^ 1], keys_in(nxt), c);
+    });
     // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
     if (has1 && q_piece<D, G>(c.tid)) store16(s.q[b ^ 1] + (c.tid - kPart) * 8, qn);
-    if (has1) issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[b ^ 1], keys_in(nxt), c);
-    wave_pv<D, G, kInt8>(vb, pp, c, s.red);
+    wave_pv<D, G, kInt8>(vb, pp, c, s.red, [&] {
+      if (has1) issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[b ^ 1], keys_in(nxt), c);
+    });
     __syncthreads();
 
     // cells(n+2) go to the buffer cells(n) used: free once every wave has
@@ -588,7 +605,6 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
                         cur.part, cur.kvh);
     __syncthreads();
-    if (has1) issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[b ^ 1], keys_in(nxt), c);
     cur = nxt;
     nxt = nn;
   }
@@ -617,8 +633,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[0], n, c);
   issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[0], n, c);
   f16x2 pp[kP / 2][G];
-  wave_softmax<D, G, kInt8>(kb, s.q[0], p.scale, n, c, pp, s.stat);
-  wave_pv<D, G, kInt8>(vb, pp, c, s.red);
+  wave_softmax<D, G, kInt8>(kb, s.q[0], p.scale, n, c, pp, s.stat, [] {});
+  wave_pv<D, G, kInt8>(vb, pp, c, s.red, [] {});
   __syncthreads();
   combine_waves<D, G>(args, s.red, s.stat, tid, item, token,
                       min((ctx + kPart - 1) / kPart, w.max_partitions), part, kvh);
