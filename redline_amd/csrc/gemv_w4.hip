@@ -39,6 +39,7 @@
 // (group_size % 128 == 0, the common case) are one scale window each; other
 // group sizes (32, 64, 96, ...) use 32-K chunks.
 #include <algorithm>
+#include <type_traits>
 
 #include "device.hpp"
 #include "redline_amd/rlk.h"
@@ -237,11 +238,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int i = i0 + u * threads;
-      if (i < staged) {
-        const int r = quot(i, inv_groups), g = i - r * a.groups;
-        so_lds[g * rows_wg + r] = v[u];
-      }
+      // unconditional: indices past the end rewrite the last entry with its
+      // own value, so no load is left unconsumed on any path (a pending load
+      // would make the compiler drain the weight ring where its register is
+      // reused)
+      const int i = min(i0 + u * threads, staged - 1);
+      const int r = quot(i, inv_groups), g = i - r * a.groups;
+      so_lds[g * rows_wg + r] = v[u];
     }
   }
   auto stage_x = [&](int c0, int c1) {
@@ -257,12 +260,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
         val[u] = load16(a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(c0) * KC + e * 8);
       }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int v = v0 + u * threads;
-        if (v < total) {
-          const int r = quot(v, inv_vpr), e = v - r * vpr;
-          *reinterpret_cast<f16x8*>(x_lds + r * a.xstride + e * 8) = x_perm(val[u]);
-        }
+      for (int u = 0; u < kBatch; ++u) {  // unconditional, as above
+        const int v = min(v0 + u * threads, total - 1);
+        const int r = quot(v, inv_vpr), e = v - r * vpr;
+        *reinterpret_cast<f16x8*>(x_lds + r * a.xstride + e * 8) = x_perm(val[u]);
       }
     }
   };
@@ -289,23 +290,17 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
 
   // Rounds of P slots per part.  A pass holds cpp chunks, a multiple of
   // S*P*PR, so pass boundaries fall on round boundaries for every part alike.
+  // Full rounds are straight-line code (every slot valid); only the last,
+  // partial round of the last pass tests its slots.  Branches inside a round
+  // would make the compiler's wait-count tracking merge conservatively and
+  // wait for the whole ring instead of one slot.
   constexpr int kRound = S * P * PR;
-  const int rounds = (a.nchunks + kRound - 1) / kRound;
-  int c0 = 0;  // first chunk of the staged pass
-  for (int rd = 0; rd < rounds; ++rd) {
-    const int cb = rd * kRound;
-    if (cb % a.cpp == 0) {  // workgroup-uniform
-      if (cb > 0) {
-        __syncthreads();  // every wave is done with the previous pass's x
-        stage_x(cb, min(cb + a.cpp, a.nchunks));
-        c0 = cb;
-      }
-      __syncthreads();
-    }
+  auto round = [&](int cb, int c0, auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int cs = cb + (part + S * p) * PR;
-      if (cs < a.nchunks) {  // wave-uniform: only the last round has idle slots
+      if (kFull || cs < a.nchunks) {  // wave-uniform
         u32x4 words[PR];
         if constexpr (PR == 1) {
           words[0] = wbuf[p][0];
@@ -353,6 +348,17 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
       // refill the slot with this part's chunks one round ahead
       fetch(p, min(cs + kRound, last_slot));
     }
+  };
+  for (int c0 = 0; c0 < a.nchunks; c0 += a.cpp) {  // x passes (workgroup-uniform)
+    const int c1 = min(c0 + a.cpp, a.nchunks);
+    if (c0 > 0) {
+      __syncthreads();  // every wave is done with the previous pass's x
+      stage_x(c0, c1);
+    }
+    __syncthreads();
+    const int full_end = c0 + (c1 - c0) / kRound * kRound;
+    for (int cb = c0; cb < full_end; cb += kRound) round(cb, c0, std::true_type{});
+    if (full_end < c1) round(full_end, c0, std::false_type{});
   }
 
   if constexpr (S > 1) {
@@ -435,13 +441,13 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
   if constexpr (KC == 128) {
     switch (cfg) {
       case 1: st = launch<1, 8, KC, MT, MODE>(a, 8, s); break;
-      case 2: st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s); break;
+      case 2: st = launch<1, 4, KC, MT, MODE, 2>(a, 8, s); break;
       case 3: st = launch<1, 6, KC, MT, MODE, 2>(a, 8, s); break;
       case 4: st = launch<1, 16, KC, MT, MODE>(a, 8, s); break;
       case 5: st = launch<1, 12, KC, MT, MODE>(a, 8, s); break;
       case 6: st = launch<1, 8, KC, MT, MODE, 2>(a, 4, s); break;
       case 7: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
-      default: st = launch<1, 4, KC, MT, MODE, 2>(a, 8, s); break;
+      default: st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s); break;
     }
   }
   (void)cfg;
