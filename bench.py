@@ -512,8 +512,8 @@ def main():
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": dk["gb_per_s"],
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_of_hbm_peak"],
                 "traffic": measured_traffic(w.key, KERNEL_SYMBOL[dominant]),
-                "traffic_source": "profiles/hbm_traffic_C2_C5.md (rocprofv3 FETCH_SIZE x2.0 + "
-                                  "WRITE_SIZE x1.0, calibrated on a 256 MiB copy)",
+                "traffic_source": "profiles/hbm_traffic_C2_C5.md (rocprofv3 FETCH_SIZE and "
+                                  "WRITE_SIZE, each scaled by its reading for a 256 MiB copy)",
                 "bytes_per_launch": nb[dominant]}
 
     extra = {}
