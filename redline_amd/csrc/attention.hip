@@ -7,22 +7,19 @@
 // group; partitions are merged by a small reduction kernel when a context
 // spans more than one.
 //
-// The in-workgroup mapping is wave64-first (8 waves per workgroup):
+// The in-workgroup mapping is wave64-first (8 waves per workgroup, 32 keys
+// each):
 //   * every key of the partition is resolved once to its cache cell (block
 //     table lookup) into LDS, so K/V addresses are one LDS read each;
-//   * a K or V row of D elements is D/8 lanes x 8 elements: one 16-byte load
-//     per lane for fp16 rows, one 8-byte load for int8 rows; a wave covers
-//     64/(D/8) keys per pass and each wave requests all of its K and V rows
-//     for the partition before consuming the first (loads past the context
-//     re-read the last valid row and are masked, so none is conditional);
-//   * q . k runs on fp16 pairs with v_dot2_f32_f16 (fp32 accumulate) and the
-//     D/8 lanes of a key finish the dot with DPP row operations (quad_perm,
-//     row_half_mirror, row_mirror): no LDS traffic; scores go to LDS;
-//   * the softmax statistics of all G heads are reduced together (wave
-//     butterflies, one LDS exchange);
-//   * P . V keeps the row mapping, each lane accumulating its 8 output dims
-//     for the G heads; key slots are folded with xor shuffles inside the wave
-//     and across the 8 waves through LDS.
+//   * q . k runs on the matrix cores (v_mfma_f32_16x16x32_f16, K as the A
+//     operand, the G heads of the group as B columns); the keys are numbered
+//     so that each lane receives scores of keys its own row of 16 lanes uses
+//     in P . V, and the softmax runs once per (key, head) on that output;
+//   * P . V reads V rows 8 elements per lane and accumulates fp16 pairs of
+//     probabilities with v_dot2_f32_f16 (fp32); the key slots of a wave are
+//     summed with permlane swaps and the 8 waves combined through LDS;
+//   * INT8 codes become exact fp16 values through byte permutes under an
+//     fp16 exponent, without conversion instructions.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
