@@ -135,11 +135,10 @@ __device__ __forceinline__ int key_of(const LaneCoord& c, int pass) {
   return (pass * kWaves + c.wave) * Geo<D>::kKPP + c.slot;
 }
 
-// The K (or V) rows of this thread's keys and their INT8 scales, in flight.
+// The V rows of this thread's keys, in flight.
 template <int D, bool kInt8>
 struct RowBatch {
   typename Row<kInt8>::Raw r[Geo<D>::kPasses];
-  float s[Geo<D>::kPasses];
 };
 
 // Requests every row of this thread's keys of a unit whose first `n` keys
@@ -148,14 +147,10 @@ struct RowBatch {
 // which keeps every load unconditional.
 template <int D, bool kInt8>
 __device__ __forceinline__ void issue_rows(RowBatch<D, kInt8>& rb, const void* base,
-                                           const float* scales, const int* cells, int n,
-                                           const LaneCoord& c) {
+                                           const int* cells, int n, const LaneCoord& c) {
 #pragma unroll
-  for (int u = 0; u < Geo<D>::kPasses; ++u) {
-    const int64_t cell = cells[min(key_of<D>(c, u), n - 1)];
-    rb.r[u] = Row<kInt8>::load(base, cell, D, c.e0);
-    rb.s[u] = kInt8 ? scales[cell] : 1.f;
-  }
+  for (int u = 0; u < Geo<D>::kPasses; ++u)
+    rb.r[u] = Row<kInt8>::load(base, cells[min(key_of<D>(c, u), n - 1)], D, c.e0);
   // keeps the scheduler from moving the batch next to its first use
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -186,13 +181,11 @@ __device__ __forceinline__ int mma_key(const LaneCoord& c, int t, int r) {
 
 // K rows of a unit in the matrix-core layout: per tile, lane (j, r) holds the
 // 16-byte pieces [64 x + 16 j, +16) of key row r's bytes (x < kLoads), which
-// are k-slot j of one (fp16) or two (int8, 8 codes each) MFMA steps; plus
-// the INT8 k scales of the 8 keys whose scores the lane receives.
+// are k-slot j of one (fp16) or two (int8, 8 codes each) MFMA steps.
 template <int D, bool kInt8>
 struct KBatch {
   static constexpr int kLoads = D * (kInt8 ? 1 : 2) / 64;
   u32x4 r[2][kLoads];
-  float s[8];
 };
 
 // dims of MFMA step `step` held at k-slot j
@@ -203,8 +196,7 @@ __device__ __forceinline__ int step_dim(int step, int j) {
 
 template <int D, bool kInt8>
 __device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* base,
-                                           const float* scales, const int* cells, int n,
-                                           const LaneCoord& c) {
+                                           const int* cells, int n, const LaneCoord& c) {
   const int lane = c.tid % kWave, r = lane % 16, j = lane / 16;
   constexpr int kRowBytes = D * (kInt8 ? 1 : 2);
 #pragma unroll
@@ -215,11 +207,6 @@ __device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* bas
     for (int x = 0; x < KBatch<D, kInt8>::kLoads; ++x)
       kb.r[t][x] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 64 * x));
   }
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      kb.s[4 * t + i] = kInt8 ? scales[cells[min(mma_key<D>(c, t, 4 * j + i), n - 1)]] : 1.f;
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -247,7 +234,7 @@ __device__ __forceinline__ float row_bcast(float v, int g) {
 // form requests the next unit's K rows into the same registers there).
 template <int D, int G, bool kInt8, class Then>
 __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _Float16* qs,
-                                            float scale, int n, const LaneCoord& c,
+                                            const float* ksc, float scale, int n, const LaneCoord& c,
                                             f16x2 (&pp)[Geo<D>::kPasses / 2][G],
                                             float (&stat)[kWaves][G][2], Then then) {
   constexpr int kSteps = D / 32, kP = Geo<D>::kPasses;
@@ -276,7 +263,8 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
     }
   }
 #pragma unroll
-  for (int x = 0; x < 8; ++x) ks[x] = kb.s[x];
+  for (int x = 0; x < 8; ++x)  // INT8 k scales of the lane's keys, from LDS
+    ks[x] = kInt8 ? ksc[mma_key<D>(c, x / 4, 4 * rho + x % 4)] : 1.f;
   then();
   float e[2][4];
 #pragma unroll
@@ -336,7 +324,7 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
 // sum has halved the accumulators (the persistent form requests the next
 // unit's V rows into the same registers there).
 template <int D, int G, bool kInt8, class Then>
-__device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb,
+__device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const float* vsc,
                                         const f16x2 (&pp)[Geo<D>::kPasses / 2][G], const LaneCoord& c,
                                         float (&red)[kWaves][G][D], Then then) {
   constexpr int kP = Geo<D>::kPasses, kN = G * 8;
@@ -350,7 +338,8 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb,
 #pragma unroll
     for (int g = 0; g < G; ++g) ph[g] = pp[h][g];
     if constexpr (kInt8) {  // p * v_scale, per key
-      const f16x2 vs = {static_cast<_Float16>(vb.s[2 * h]), static_cast<_Float16>(vb.s[2 * h + 1])};
+      const f16x2 vs = {static_cast<_Float16>(vsc[key_of<D>(c, 2 * h)]),
+                        static_cast<_Float16>(vsc[key_of<D>(c, 2 * h + 1)])};
 #pragma unroll
       for (int g = 0; g < G; ++g) ph[g] *= vs;
     }
@@ -434,17 +423,29 @@ struct UnitLds {
   float red[kWaves][G][D];   // each wave's P . V partial
   float stat[kWaves][G][2];  // each wave's (max, sum) per head
   int cell[2][kPart];        // cache cell of each key of the partition
+  float ksc[2][kPart];       // its INT8 k and v scales
+  float vsc[2][kPart];
   alignas(16) _Float16 q[2][G * D];
 };
 
 // Cache cells of a partition's keys, from this thread's block-table entry
 // `blk` for key `tid` (threads tid < 256; blk < 0 past the table).
+// (threads tid >= 256 or past the table: nothing); the key's INT8 scales
+// are requested into ks / vs (0 when there is no cell).
+template <bool kInt8>
 __device__ __forceinline__ void write_cells(int* cells, const rlk_attention_params& p, int tid,
-                                            int blk, int part, int kvh) {
+                                            int blk, int part, int kvh, float& ks, float& vs) {
+  ks = 0.f;
+  vs = 0.f;
   if (tid < kPart && blk >= 0) {
     const int bs = p.kv.block_size;
     const int pos = part * kPart + tid;
-    cells[tid] = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
+    const int cell = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
+    cells[tid] = cell;
+    if constexpr (kInt8) {
+      ks = p.kv.k_scale[cell];
+      vs = p.kv.v_scale[cell];
+    }
   }
 }
 
@@ -474,6 +475,8 @@ __device__ __forceinline__ int table_entry(const rlk_attention_params& p, int ti
 // sequence and context into LDS and prefix-sums the partitions per item; the
 // work units (item, partition, kv head) -- only those inside a context -- are
 // then split into contiguous ranges, one per workgroup.  Kv head runs fastest.
+// The INT8 scales of a partition's keys are fetched once, by the threads that
+// resolve its cells, into LDS next to the cells.
 //
 // The units of a range are software-pipelined across their two row batches:
 //   wait K(n) -> q . k -> request K(n+1) -> softmax -> wait V(n) -> P . V
@@ -560,9 +563,21 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
 
   UnitPos cur = {lo, pu - it_pfx[lo], u0 - pu * hkv};
   UnitPos nxt = u0 + 1 < u1 ? advance(cur) : cur;
-  write_cells(s.cell[0], p, tid, table_entry(p, tid, it_seq[cur.item], cur.part), cur.part, cur.kvh);
+  // INT8 scales of key tid of unit n+1, requested in unit n-1 and written to
+  // LDS in unit n (the cells of unit n+2 are written there too)
+  float sk_next = 0.f, sv_next = 0.f;
+  {
+    float ks0, vs0;
+    write_cells<kInt8>(s.cell[0], p, tid, table_entry(p, tid, it_seq[cur.item], cur.part), cur.part,
+                       cur.kvh, ks0, vs0);
+    if (kInt8 && tid < kPart) {
+      s.ksc[0][tid] = ks0;
+      s.vsc[0][tid] = vs0;
+    }
+  }
   if (u0 + 1 < u1)
-    write_cells(s.cell[1], p, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part), nxt.part, nxt.kvh);
+    write_cells<kInt8>(s.cell[1], p, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part), nxt.part,
+                       nxt.kvh, sk_next, sv_next);
   if (q_piece<D, G>(tid))
     store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, it_tok[cur.item], cur.kvh));
   __syncthreads();
@@ -571,8 +586,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   RowBatch<D, kInt8> vb;
   {
     const LaneCoord c = lane_coord<D>();
-    issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[0], keys_in(cur), c);
-    issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[0], keys_in(cur), c);
+    issue_keys<D, kInt8>(kb, p.kv.k, s.cell[0], keys_in(cur), c);
+    issue_rows<D, kInt8>(vb, p.kv.v, s.cell[0], keys_in(cur), c);
   }
   for (int u = u0; u < u1; ++u) {
     const int b = (u - u0) & 1;
@@ -586,19 +601,24 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     if (has1 && q_piece<D, G>(c.tid)) qn = load_q_piece<D, G>(p, c.tid, it_tok[nxt.item], nxt.kvh);
 
     f16x2 pp[kP / 2][G];
-    wave_softmax<D, G, kInt8>(kb, s.q[b], p.scale, keys_in(cur), c, pp, s.stat, [&] {
-      if (has1) issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[b ^ 1], keys_in(nxt), c);
+    wave_softmax<D, G, kInt8>(kb, s.q[b], s.ksc[b], p.scale, keys_in(cur), c, pp, s.stat, [&] {
+      if (has1) issue_keys<D, kInt8>(kb, p.kv.k, s.cell[b ^ 1], keys_in(nxt), c);
     });
     // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
     if (has1 && q_piece<D, G>(c.tid)) store16(s.q[b ^ 1] + (c.tid - kPart) * 8, qn);
-    wave_pv<D, G, kInt8>(vb, pp, c, s.red, [&] {
-      if (has1) issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[b ^ 1], keys_in(nxt), c);
+    wave_pv<D, G, kInt8>(vb, s.vsc[b], pp, c, s.red, [&] {
+      if (has1) issue_rows<D, kInt8>(vb, p.kv.v, s.cell[b ^ 1], keys_in(nxt), c);
     });
     __syncthreads();
 
-    // cells(n+2) go to the buffer cells(n) used: free once every wave has
+    // scales(n+1) go to the buffers unit n-1 read (free since its barriers);
+    // cells(n+2) to the buffer cells(n) used, free once every wave has
     // requested V(n), i.e. after this barrier
-    if (has2) write_cells(s.cell[b], p, c.tid, blk2, nn.part, nn.kvh);
+    if (kInt8 && has1 && c.tid < kPart) {
+      s.ksc[b ^ 1][c.tid] = sk_next;
+      s.vsc[b ^ 1][c.tid] = sv_next;
+    }
+    if (has2) write_cells<kInt8>(s.cell[b], p, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next);
     combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
                         cur.part, cur.kvh);
     __syncthreads();
@@ -621,17 +641,24 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   const int ctx = p.positions[token] + 1;
   if (part >= (ctx + kPart - 1) / kPart) return;  // uniform over the workgroup (part < max_partitions)
   const int n = min(kPart, ctx - part * kPart);
-  write_cells(s.cell[0], p, tid, blk, part, kvh);
+  {
+    float ks0, vs0;
+    write_cells<kInt8>(s.cell[0], p, tid, blk, part, kvh, ks0, vs0);
+    if (kInt8 && tid < kPart) {
+      s.ksc[0][tid] = ks0;
+      s.vsc[0][tid] = vs0;
+    }
+  }
   if (q_piece<D, G>(tid)) store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, token, kvh));
   __syncthreads();
   const LaneCoord c = lane_coord<D>();
   KBatch<D, kInt8> kb;
   RowBatch<D, kInt8> vb;
-  issue_keys<D, kInt8>(kb, p.kv.k, p.kv.k_scale, s.cell[0], n, c);
-  issue_rows<D, kInt8>(vb, p.kv.v, p.kv.v_scale, s.cell[0], n, c);
+  issue_keys<D, kInt8>(kb, p.kv.k, s.cell[0], n, c);
+  issue_rows<D, kInt8>(vb, p.kv.v, s.cell[0], n, c);
   f16x2 pp[kP / 2][G];
-  wave_softmax<D, G, kInt8>(kb, s.q[0], p.scale, n, c, pp, s.stat, [] {});
-  wave_pv<D, G, kInt8>(vb, pp, c, s.red, [] {});
+  wave_softmax<D, G, kInt8>(kb, s.q[0], s.ksc[0], p.scale, n, c, pp, s.stat, [] {});
+  wave_pv<D, G, kInt8>(vb, s.vsc[0], pp, c, s.red, [] {});
   __syncthreads();
   combine_waves<D, G>(args, s.red, s.stat, tid, item, token,
                       min((ctx + kPart - 1) / kPart, w.max_partitions), part, kvh);
