@@ -210,6 +210,19 @@ typedef struct rlk_decode_attention_work {
 int rlk_paged_attention_decode(const rlk_attention_params* params,
                                const rlk_decode_attention_work* work, hipStream_t stream);
 
+/* Extension, no counterpart in the reference (whose scales are fp32 only):
+ * decode attention over an INT8 cache whose scales were stored as fp16 by
+ * rlk_rope_and_write_kv_ex with RLK_SCALE_F16 (k_scale / v_scale then address
+ * uint16_t cells).  options->scale_dtype: RLK_SCALE_F32 or RLK_SCALE_F16;
+ * NULL options = rlk_paged_attention_decode. */
+typedef struct rlk_attention_options {
+  int scale_dtype;
+} rlk_attention_options;
+
+int rlk_paged_attention_decode_ex(const rlk_attention_params* params,
+                                  const rlk_decode_attention_work* work,
+                                  const rlk_attention_options* options, hipStream_t stream);
+
 /* ------------------------------------------------------ host-side helpers */
 
 /* IEEE fp16 <-> fp32 with round-to-nearest-even.

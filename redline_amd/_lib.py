@@ -51,6 +51,12 @@ class RopeKVOptions(C.Structure):
     _fields_ = [("qkv_bias", C.c_void_p), ("scale_dtype", C.c_int)]
 
 
+class AttentionOptions(C.Structure):
+    """Mirror of rlk_attention_options (extension of paged_attention_decode)."""
+
+    _fields_ = [("scale_dtype", C.c_int)]
+
+
 RLK_DECODE_PARTITION_SIZE = 256
 RLK_GEMV_W4_MAX_M = 32
 
@@ -104,6 +110,9 @@ _SIGNATURES = {
                                       C.POINTER(RopeKVOptions), _P]),
     "rlk_paged_attention_decode": (_I, [C.POINTER(AttentionParams),
                                         C.POINTER(DecodeAttentionWork), _P]),
+    "rlk_paged_attention_decode_ex": (_I, [C.POINTER(AttentionParams),
+                                           C.POINTER(DecodeAttentionWork),
+                                           C.POINTER(AttentionOptions), _P]),
     "rlk_gemv_w4a16": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _I, _P]),
     "rlk_gemv_w4a16_swiglu": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]),
     "rlk_float_to_half_bits": (C.c_uint16, [C.c_float]),

@@ -40,7 +40,7 @@ constexpr int kPart = RLK_DECODE_PARTITION_SIZE;  // keys per partition
 struct AttnArgs {
   rlk_attention_params p;
   rlk_decode_attention_work w;
-
+  int scale16;  // INT8 scales stored as fp16 (extension)
 };
 
 
@@ -433,8 +433,9 @@ struct UnitLds {
 // (threads tid >= 256 or past the table: nothing); the key's INT8 scales
 // are requested into ks / vs (0 when there is no cell).
 template <bool kInt8>
-__device__ __forceinline__ void write_cells(int* cells, const rlk_attention_params& p, int tid,
-                                            int blk, int part, int kvh, float& ks, float& vs) {
+__device__ __forceinline__ void write_cells(int* cells, const AttnArgs& args, int tid, int blk,
+                                            int part, int kvh, float& ks, float& vs) {
+  const rlk_attention_params& p = args.p;
   ks = 0.f;
   vs = 0.f;
   if (tid < kPart && blk >= 0) {
@@ -443,8 +444,13 @@ __device__ __forceinline__ void write_cells(int* cells, const rlk_attention_para
     const int cell = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
     cells[tid] = cell;
     if constexpr (kInt8) {
-      ks = p.kv.k_scale[cell];
-      vs = p.kv.v_scale[cell];
+      if (args.scale16) {  // uniform
+        ks = static_cast<float>(reinterpret_cast<const _Float16*>(p.kv.k_scale)[cell]);
+        vs = static_cast<float>(reinterpret_cast<const _Float16*>(p.kv.v_scale)[cell]);
+      } else {
+        ks = p.kv.k_scale[cell];
+        vs = p.kv.v_scale[cell];
+      }
     }
   }
 }
@@ -568,7 +574,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   float sk_next = 0.f, sv_next = 0.f;
   {
     float ks0, vs0;
-    write_cells<kInt8>(s.cell[0], p, tid, table_entry(p, tid, it_seq[cur.item], cur.part), cur.part,
+    write_cells<kInt8>(s.cell[0], args, tid, table_entry(p, tid, it_seq[cur.item], cur.part), cur.part,
                        cur.kvh, ks0, vs0);
     if (kInt8 && tid < kPart) {
       s.ksc[0][tid] = ks0;
@@ -576,7 +582,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     }
   }
   if (u0 + 1 < u1)
-    write_cells<kInt8>(s.cell[1], p, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part), nxt.part,
+    write_cells<kInt8>(s.cell[1], args, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part), nxt.part,
                        nxt.kvh, sk_next, sv_next);
   if (q_piece<D, G>(tid))
     store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, it_tok[cur.item], cur.kvh));
@@ -618,7 +624,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
       s.ksc[b ^ 1][c.tid] = sk_next;
       s.vsc[b ^ 1][c.tid] = sv_next;
     }
-    if (has2) write_cells<kInt8>(s.cell[b], p, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next);
+    if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next);
     combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
                         cur.part, cur.kvh);
     __syncthreads();
@@ -643,7 +649,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   const int n = min(kPart, ctx - part * kPart);
   {
     float ks0, vs0;
-    write_cells<kInt8>(s.cell[0], p, tid, blk, part, kvh, ks0, vs0);
+    write_cells<kInt8>(s.cell[0], args, tid, blk, part, kvh, ks0, vs0);
     if (kInt8 && tid < kPart) {
       s.ksc[0][tid] = ks0;
       s.vsc[0][tid] = vs0;
@@ -769,9 +775,10 @@ bool launch_d(const AttnArgs& a, int G, bool int8, hipStream_t stream) {
 
 using namespace rlk;
 
-extern "C" int rlk_paged_attention_decode(const rlk_attention_params* p,
-                                          const rlk_decode_attention_work* w,
-                                          hipStream_t stream) {
+namespace {
+
+int attention_launch(const rlk_attention_params* p, const rlk_decode_attention_work* w,
+                     int scale16, hipStream_t stream) {
   if (p == nullptr || w == nullptr)
     return fail(RLK_EINVAL, "paged_attention_decode: null params or work");
   if (w->num_items <= 0) return RLK_OK;
@@ -798,10 +805,28 @@ extern "C" int rlk_paged_attention_decode(const rlk_attention_params* p,
   AttnArgs a;
   a.p = *p;
   a.w = *w;
+  a.scale16 = scale16;
   const int G = p->num_heads / hkv;
   const bool int8 = p->kv.dtype == RLK_KV_INT8;
   const bool ok = p->kv.head_dim == 128 ? launch_d<128>(a, G, int8, stream)
                                         : launch_d<64>(a, G, int8, stream);
   if (!ok) return fail(RLK_EUNSUPPORTED, "unsupported GQA group size %d", G);
   return launch_status("paged_attention_decode");
+}
+
+}  // namespace
+
+extern "C" int rlk_paged_attention_decode(const rlk_attention_params* p,
+                                          const rlk_decode_attention_work* w,
+                                          hipStream_t stream) {
+  return attention_launch(p, w, 0, stream);
+}
+
+extern "C" int rlk_paged_attention_decode_ex(const rlk_attention_params* p,
+                                             const rlk_decode_attention_work* w,
+                                             const rlk_attention_options* o, hipStream_t stream) {
+  const int scale_dtype = o != nullptr ? o->scale_dtype : RLK_SCALE_F32;
+  if (scale_dtype != RLK_SCALE_F32 && scale_dtype != RLK_SCALE_F16)
+    return fail(RLK_EINVAL, "paged_attention_decode_ex: unknown scale dtype %d", scale_dtype);
+  return attention_launch(p, w, scale_dtype == RLK_SCALE_F16, stream);
 }

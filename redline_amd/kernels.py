@@ -19,7 +19,8 @@ from ._lib import KVLayerView, check, lib
 __all__ = [
     "embedding_lookup", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
     "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
-    "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "attention_params",
+    "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "paged_attention_decode_ex",
+    "attention_params",
     "decode_work", "DecodeWorkspace", "kDecodePartitionSize", "gemv_w4a16", "gemv_w4a16_swiglu",
     "kGemvW4MaxM",
 ]
@@ -214,6 +215,15 @@ def paged_attention_decode(params: _lib.AttentionParams, work: _lib.DecodeAttent
                            stream=None):
     """Flash-decoding paged attention (kernels::paged_attention_decode)."""
     check(lib().rlk_paged_attention_decode(C.byref(params), C.byref(work), _stream(stream)))
+
+
+def paged_attention_decode_ex(params: _lib.AttentionParams, work: _lib.DecodeAttentionWork,
+                              scale_dtype=SCALE_F32, stream=None):
+    """Extension: decode attention over an INT8 cache with fp16 scales
+    (written by rope_and_write_kv_ex with SCALE_F16)."""
+    opt = _lib.AttentionOptions(scale_dtype)
+    check(lib().rlk_paged_attention_decode_ex(C.byref(params), C.byref(work), C.byref(opt),
+                                              _stream(stream)))
 
 
 class KVCache:

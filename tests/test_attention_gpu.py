@@ -170,6 +170,69 @@ def test_decode_attention_llama_b32(torch_cuda, int8, attention_form):
     assert_close_f16(got, want, what="attention C2")
 
 
+@pytest.mark.parametrize("hq,hkv,D,lens", [(8, 2, 128, [33, 280]), (4, 2, 64, [520]),
+                                           (32, 8, 128, [300, 17])])
+def test_decode_attention_int8_fp16_scales(torch_cuda, hq, hkv, D, lens, attention_form):
+    """Extension: an INT8 cache whose scales rope_and_write_kv_ex stored as
+    fp16 (C4's scale format), attended by paged_attention_decode_ex; the
+    oracle dequantises with the same fp16 scales.  Bad scale dtypes are
+    rejected."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    say(f"attention fp16 scales hq={hq} hkv={hkv} D={D} lens={lens} form={attention_form}")
+    bs = 16
+    rng = np.random.default_rng(11 * hq + D + sum(lens))
+    S, T, max_len = len(lens), sum(lens), max(lens)
+    nblocks = 1 + sum((L + bs - 1) // bs for L in lens)
+    ids = rng.permutation(np.arange(1, nblocks, dtype=np.int32))
+    max_blocks = (max_len + bs - 1) // bs
+    b = ra.BatchBuilder(T, S, S, max_blocks, bs, 1 << 30)
+    nxt = 0
+    for L in lens:
+        nb = (L + bs - 1) // bs
+        b.add(np.zeros(L, np.int32), 0, L, None, ids[nxt:nxt + nb])
+        nxt += nb
+    meta, shape, lay = b.write()
+    stride = (hq + 2 * hkv) * D
+    qkv = randn_f16(rng, (T, stride))
+    cos, sin = ra.rope_cos_sin_tables(1e4, D, max_len)
+    cache = K.KVCache(1, nblocks, hkv, D, bs, K.KVDType.kINT8, scale_dtype=K.SCALE_F16)
+    d_meta, d_qkv = dev(torch, meta), dev(torch, qkv)
+    sl = lambda name, n: d_meta[lay[name]:lay[name] + n]  # noqa: E731
+    K.rope_and_write_kv_ex(d_qkv, sl("positions", T), sl("slot_mapping", T), T, hq,
+                           dev(torch, cos), dev(torch, sin), cache.layer(0),
+                           scale_dtype=K.SCALE_F16)
+    max_parts = (shape.max_context + 255) // 256
+    out = torch.zeros((T, hq * D), dtype=torch.float16, device="cuda")
+    ws = K.DecodeWorkspace(T, hq, max_parts, D) if max_parts > 1 else None
+    prm = K.attention_params(d_qkv, stride, out, hq, 1 / np.sqrt(D), cache.layer(0),
+                             d_meta[lay["block_tables"]:], max_blocks, sl("positions", T))
+    wk = K.decode_work(sl("decode_token", T), sl("decode_seq", T), T, max_parts, ws)
+    K.paged_attention_decode_ex(prm, wk, K.SCALE_F16)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+
+    pos = meta[lay["positions"]:lay["positions"] + T]
+    slots = meta[lay["slot_mapping"]:lay["slot_mapping"] + T]
+    shape4 = (nblocks, hkv, bs, D)
+    kc = np.zeros(shape4, np.int8)
+    vc = np.zeros_like(kc)
+    ks16 = np.zeros(shape4[:3], np.uint16)
+    vs16 = np.zeros_like(ks16)
+    roped = qkv.copy()
+    oracle.rope_and_write_kv(roped, pos, slots, hq, hkv, D, cos, sin, kc, vc, ks16, vs16, bs, True,
+                             scale16=True)
+    tables = meta[lay["block_tables"]:lay["block_tables"] + S * max_blocks].reshape(S, max_blocks)
+    want = oracle.paged_attention_decode(
+        roped, stride, hq, 1 / np.sqrt(D), kc, vc, ks16.view(np.float16).astype(np.float32),
+        vs16.view(np.float16).astype(np.float32), tables, pos,
+        meta[lay["decode_token"]:lay["decode_token"] + T],
+        meta[lay["decode_seq"]:lay["decode_seq"] + T], T, True)
+    assert_close_f16(got, want, what="attention fp16 scales")
+    with pytest.raises(ra.Error, match="scale dtype"):
+        K.paged_attention_decode_ex(prm, wk, 7)
+
+
 def test_decode_attention_items_subset_and_errors(torch_cuda):
     """Only decode items' rows are written (mixed prefill/decode batch), and
     argument errors are reported before launch."""
