@@ -196,10 +196,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
   const int last = a.nchunks - 1;
 
   // The weight codes of this lane's row travel in a ring of P chunks; part
-  // `part` takes chunks part, part + S, part + 2S, ...  The ring is started
-  // before scales, offsets and x are staged, so that all are in flight together.
-  // A ring slot holds PR chunks; slot p of a round starts at chunk
-  // cb + (part + S p) PR.
+  // `part` takes chunks part, part + S, part + 2S, ...  A ring slot holds PR
+  // chunks; slot p of a round starts at chunk cb + (part + S p) PR.
   u32x4 wbuf[P][PR];
   const uint8_t* wp[PR];
   if constexpr (PR == 1) {
@@ -216,19 +214,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
     for (int h = 0; h < PR; ++h)
       wbuf[p][h] = load_codes<KC>(wp[h] + static_cast<size_t>(c) * (KC / 2));
   };
-#pragma unroll
-  for (int p = 0; p < P; ++p) fetch(p, min((part + S * p) * PR, last_slot));
 
-  // Both staging loops keep kBatch loads in flight before their LDS writes
-  // (indices clamped so the loads are unconditional).  Scales and offsets go
-  // to LDS as [group][row]: per-lane loads of them would touch 16 rows' lines
-  // per instruction, as costly as a weight load.
+  // Staging of scales/offsets (to LDS as [group][row]: per-lane loads of them
+  // would touch 16 rows' lines per instruction, as costly as a weight load)
+  // and of x, in batches of kBatch loads per thread (indices clamped so that
+  // every load is consumed on every path).  The first batch of each is
+  // requested BEFORE the ring's first chunks and stored after them: wait
+  // counts retire in issue order, so the stores then wait for the staging
+  // loads only, and the ring keeps flowing through the staging and the
+  // barrier.  (Requested after the ring, the staging data would make every
+  // wave wait for its whole ring before its first chunk.)
   constexpr int kBatch = 8;
   const int staged = rows_wg * a.groups;
   const float inv_groups = 1.0f / static_cast<float>(a.groups);
   const int row_wg0 = blockIdx.x * rows_wg;
-  for (int i0 = tid; i0 < staged; i0 += threads * kBatch) {
-    uint32_t v[kBatch];
+  auto so_load = [&](int i0, uint32_t (&v)[kBatch]) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int i = min(i0 + u * threads, staged - 1);
@@ -236,38 +236,63 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
       const size_t src = static_cast<size_t>(min(row_wg0 + r, a.n - 1)) * a.groups + g;
       v[u] = a.scales[src] | (static_cast<uint32_t>(a.offsets[src]) << 16);
     }
+  };
+  auto so_store = [&](int i0, const uint32_t (&v)[kBatch]) {
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      // unconditional: indices past the end rewrite the last entry with its
-      // own value, so no load is left unconsumed on any path (a pending load
-      // would make the compiler drain the weight ring where its register is
-      // reused)
+    for (int u = 0; u < kBatch; ++u) {  // past the end: the last entry again, same value
       const int i = min(i0 + u * threads, staged - 1);
       const int r = quot(i, inv_groups), g = i - r * a.groups;
       so_lds[g * rows_wg + r] = v[u];
     }
-  }
-  auto stage_x = [&](int c0, int c1) {
+  };
+  struct XPass {
+    int c0, vpr, total;
+    float inv_vpr;
+  };
+  auto x_pass = [&](int c0, int c1) {
     const int vpr = (c1 - c0) * (KC / 8);  // 8-half vectors per row
-    const int total = a.m * vpr;
-    const float inv_vpr = 1.0f / static_cast<float>(vpr);
-    for (int v0 = tid; v0 < total; v0 += threads * kBatch) {
-      u32x4 val[kBatch];
+    return XPass{c0, vpr, a.m * vpr, 1.0f / static_cast<float>(vpr)};
+  };
+  auto x_load = [&](const XPass& xp, int v0, u32x4 (&val)[kBatch]) {
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int v = min(v0 + u * threads, total - 1);
-        const int r = quot(v, inv_vpr), e = v - r * vpr;
-        val[u] = load16(a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(c0) * KC + e * 8);
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {  // unconditional, as above
-        const int v = min(v0 + u * threads, total - 1);
-        const int r = quot(v, inv_vpr), e = v - r * vpr;
-        *reinterpret_cast<f16x8*>(x_lds + r * a.xstride + e * 8) = x_perm(val[u]);
-      }
+    for (int u = 0; u < kBatch; ++u) {
+      const int v = min(v0 + u * threads, xp.total - 1);
+      const int r = quot(v, xp.inv_vpr), e = v - r * xp.vpr;
+      val[u] = load16(a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(xp.c0) * KC + e * 8);
     }
   };
-  stage_x(0, min(a.cpp, a.nchunks));
+  auto x_store = [&](const XPass& xp, int v0, const u32x4 (&val)[kBatch]) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {  // unconditional, as above
+      const int v = min(v0 + u * threads, xp.total - 1);
+      const int r = quot(v, xp.inv_vpr), e = v - r * xp.vpr;
+      *reinterpret_cast<f16x8*>(x_lds + r * a.xstride + e * 8) = x_perm(val[u]);
+    }
+  };
+  // a pass of x, from vector v_first of this thread on
+  auto stage_x = [&](const XPass& xp, int v_first) {
+    for (int v0 = v_first; v0 < xp.total; v0 += threads * kBatch) {
+      u32x4 val[kBatch];
+      x_load(xp, v0, val);
+      x_store(xp, v0, val);
+    }
+  };
+  {
+    const XPass xp = x_pass(0, min(a.cpp, a.nchunks));
+    uint32_t sov[kBatch];
+    u32x4 xv[kBatch];
+    so_load(tid, sov);
+    x_load(xp, tid, xv);
+#pragma unroll
+    for (int p = 0; p < P; ++p) fetch(p, min((part + S * p) * PR, last_slot));
+    so_store(tid, sov);
+    x_store(xp, tid, xv);
+    for (int i0 = tid + threads * kBatch; i0 < staged; i0 += threads * kBatch) {
+      so_load(i0, sov);
+      so_store(i0, sov);
+    }
+    stage_x(xp, tid + threads * kBatch);
+  }
 
   // A-fragment rows of this lane (activation rows past m repeat the last one)
   const uint16_t* xl[MT];
@@ -353,7 +378,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
     const int c1 = min(c0 + a.cpp, a.nchunks);
     if (c0 > 0) {
       __syncthreads();  // every wave is done with the previous pass's x
-      stage_x(c0, c1);
+      stage_x(x_pass(c0, c1), tid);
     }
     __syncthreads();
     const int full_end = c0 + (c1 - c0) / kRound * kRound;
