@@ -330,8 +330,6 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const floa
   constexpr int kP = Geo<D>::kPasses, kN = G * 8;
   float v[kN];
 #pragma unroll
-  for (int i = 0; i < kN; ++i) v[i] = 0.f;
-#pragma unroll
   for (int h = 0; h < kP / 2; ++h) {
     const f16x8 va = Row<kInt8>::halves(vb.r[2 * h]), vb2 = Row<kInt8>::halves(vb.r[2 * h + 1]);
     f16x2 ph[G];
@@ -347,7 +345,8 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const floa
     for (int x = 0; x < 8; ++x) {
       const f16x2 vv = {va[x], vb2[x]};
 #pragma unroll
-      for (int g = 0; g < G; ++g) v[g * 8 + x] = __builtin_amdgcn_fdot2(ph[g], vv, v[g * 8 + x], false);
+      for (int g = 0; g < G; ++g)  // the first pair starts from 0 (no zeroed accumulator)
+        v[g * 8 + x] = __builtin_amdgcn_fdot2(ph[g], vv, h == 0 ? 0.f : v[g * 8 + x], false);
     }
   }
   if constexpr (Geo<D>::kLPK == 8) {

@@ -52,10 +52,13 @@ __device__ __forceinline__ float silu_f16(float g) {
 // compile to ds_bpermute, an LDS round trip per step.
 
 // v as read from the lane that DPP control CTRL selects (within rows of 16).
+// Every control used here selects a valid lane of the same row, so no "old"
+// value is involved (mov_dpp with bound_ctrl: no zeroing of the destination
+// before a plain DPP move).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                                                0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF,
+                                                             0xF, true));
 }
 
 // Sum / max over aligned groups of N lanes (N = 2, 4, 8 or 16), every lane
