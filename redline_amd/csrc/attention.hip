@@ -801,6 +801,14 @@ int attention_launch(const rlk_attention_params* p, const rlk_decode_attention_w
   if (w->max_partitions > 1 && (w->ws_out == nullptr || w->ws_max == nullptr || w->ws_sum == nullptr))
     return fail(RLK_EINVAL, "paged_attention_decode: split-K workspace is required when "
                             "max_partitions > 1");
+  if (p->q == nullptr || p->out == nullptr || p->block_tables == nullptr || p->positions == nullptr ||
+      w->item_token == nullptr || w->item_seq == nullptr || p->kv.k == nullptr ||
+      p->kv.v == nullptr ||
+      (p->kv.dtype == RLK_KV_INT8 && (p->kv.k_scale == nullptr || p->kv.v_scale == nullptr)))
+    return fail(RLK_EINVAL, "paged_attention_decode: null pointer argument");
+  if (p->q_stride % 8 != 0 || (reinterpret_cast<uintptr_t>(p->q) & 15) != 0)
+    return fail(RLK_EINVAL, "paged_attention_decode: q rows must be 16-byte aligned (q_stride %d)",
+                p->q_stride);
   AttnArgs a;
   a.p = *p;
   a.w = *w;

@@ -335,6 +335,8 @@ extern "C" int rlk_embedding_lookup(const int32_t* ids, const uint16_t* table, i
   if (n <= 0) return RLK_OK;
   if (hidden <= 0 || hidden % 8 != 0)
     return fail(RLK_EINVAL, "embedding_lookup: hidden size must be a multiple of 8 (got %d)", hidden);
+  if (ids == nullptr || table == nullptr || out == nullptr)
+    return fail(RLK_EINVAL, "embedding_lookup: null pointer argument");
   return launch_gather(ids, table, n, hidden / 8, out, stream, "embedding_lookup");
 }
 
@@ -343,6 +345,7 @@ extern "C" int rlk_gather_rows(const uint16_t* src, const int32_t* idx, int n, i
   if (n <= 0) return RLK_OK;
   if (cols <= 0 || cols % 8 != 0)
     return fail(RLK_EINVAL, "gather_rows: row width must be a multiple of 8 (got %d)", cols);
+  if (src == nullptr || dst == nullptr) return fail(RLK_EINVAL, "gather_rows: null pointer argument");
   return launch_gather(idx, src, n, cols / 8, dst, stream, "gather_rows");
 }
 
@@ -353,6 +356,8 @@ extern "C" int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta,
   if (hidden <= 0 || hidden % 8 != 0)
     return fail(RLK_EINVAL, "fused_add_rmsnorm: hidden size must be a multiple of 8 (got %d)",
                 hidden);
+  if (residual == nullptr || weight == nullptr || out == nullptr)
+    return fail(RLK_EINVAL, "fused_add_rmsnorm: null pointer argument");
   NormArgs a;
   a.res = reinterpret_cast<u32x4*>(residual);
   a.del = reinterpret_cast<const u32x4*>(delta);
@@ -387,6 +392,7 @@ extern "C" int rlk_silu_and_mul(const uint16_t* gate_up, int rows, int inter, ui
   if (inter <= 0 || inter % 8 != 0)
     return fail(RLK_EINVAL, "silu_and_mul: intermediate size must be a multiple of 8 (got %d)",
                 inter);
+  if (gate_up == nullptr || out == nullptr) return fail(RLK_EINVAL, "silu_and_mul: null pointer argument");
   const uint32_t vecs = inter / 8;
   const uint64_t total = static_cast<uint64_t>(rows) * vecs;
   if (total > 0x7fffffffull)
@@ -400,6 +406,8 @@ extern "C" int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, i
                                             uint16_t* out, hipStream_t stream) {
   if (rows <= 0) return RLK_OK;
   if (inter <= 0) return fail(RLK_EINVAL, "silu_and_mul_interleaved: bad intermediate size %d", inter);
+  if (gate_up == nullptr || out == nullptr)
+    return fail(RLK_EINVAL, "silu_and_mul_interleaved: null pointer argument");
   const uint64_t pairs = static_cast<uint64_t>(rows) * inter;
   if (pairs > 0x7fffffffull)
     return fail(RLK_EINVAL, "silu_and_mul_interleaved: %d rows exceed one launch; split the call",
@@ -419,6 +427,9 @@ extern "C" int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, i
 extern "C" int rlk_resolve_input_ids(int32_t* input_ids, const int32_t* src,
                                      const int32_t* prev_sampled, int n, hipStream_t stream) {
   if (n <= 0) return RLK_OK;
+  // prev_sampled is read only where src >= 0, so a batch without such rows may pass null
+  if (input_ids == nullptr || src == nullptr)
+    return fail(RLK_EINVAL, "resolve_input_ids: null pointer argument");
   resolve_input_ids_kernel<<<(n + 255) / 256, 256, 0, stream>>>(input_ids, src, prev_sampled, n);
   return launch_status("resolve_input_ids");
 }

@@ -185,6 +185,10 @@ int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_map
   if (num_heads < 0 || kv->num_kv_heads < 0 || kv->block_size <= 0)
     return fail(RLK_EINVAL, "%s: bad head counts (%d, %d) or block size %d", what, num_heads,
                 kv->num_kv_heads, kv->block_size);
+  if (qkv == nullptr || positions == nullptr || slot_mapping == nullptr || cos_table == nullptr ||
+      sin_table == nullptr || kv->k == nullptr || kv->v == nullptr ||
+      (kv->dtype == RLK_KV_INT8 && (kv->k_scale == nullptr || kv->v_scale == nullptr)))
+    return fail(RLK_EINVAL, "%s: null pointer argument", what);
   RopeArgs a;
   a.qkv = reinterpret_cast<_Float16*>(qkv);
   a.positions = positions;

@@ -61,6 +61,32 @@ def test_shape_errors_fail_before_launch():
         _lib.RLK_EINVAL
 
 
+def test_null_pointers_fail_before_launch():
+    """Required device pointers are checked before anything is launched
+    (optional ones -- delta, the gather index, prev_sampled, bias -- may be
+    null)."""
+    L = ra.lib()
+    d = C.c_void_p(16)  # a non-null stand-in: nothing is launched
+    assert L.rlk_embedding_lookup(d, None, 4, 16, d, None) == _lib.RLK_EINVAL
+    assert b"null pointer" in L.rlk_last_error()
+    assert L.rlk_gather_rows(None, None, 2, 8, d, None) == _lib.RLK_EINVAL
+    assert L.rlk_fused_add_rmsnorm(d, None, None, 3, 64, 1e-5, d, None) == _lib.RLK_EINVAL
+    assert L.rlk_silu_and_mul(d, 2, 16, None, None) == _lib.RLK_EINVAL
+    assert L.rlk_silu_and_mul_interleaved(None, 2, 3, d, None) == _lib.RLK_EINVAL
+    assert L.rlk_resolve_input_ids(d, None, d, 4, None) == _lib.RLK_EINVAL
+    kv = _lib.KVLayerView(d, d, None, None, 16, 2, 128, 1)  # INT8 without scales
+    assert L.rlk_rope_and_write_kv(d, d, d, 1, 4, d, d, C.byref(kv), None) == _lib.RLK_EINVAL
+    assert b"null pointer" in L.rlk_last_error()
+    kv = _lib.KVLayerView(d, d, None, None, 16, 2, 128, 0)
+    prm = _lib.AttentionParams(d, 384, d, 4, 0.1, kv, None, 4, d)
+    wk = _lib.DecodeAttentionWork(d, d, 2, 1, None, None, None)
+    assert L.rlk_paged_attention_decode(C.byref(prm), C.byref(wk), None) == _lib.RLK_EINVAL
+    assert b"null pointer" in L.rlk_last_error()
+    prm = _lib.AttentionParams(d, 100, d, 4, 0.1, kv, d, 4, d)
+    assert L.rlk_paged_attention_decode(C.byref(prm), C.byref(wk), None) == _lib.RLK_EINVAL
+    assert b"16-byte aligned" in L.rlk_last_error()
+
+
 def test_empty_batches_are_noops():
     L = ra.lib()
     assert L.rlk_embedding_lookup(None, None, 0, 12, None, None) == 0  # checked after n <= 0
