@@ -40,6 +40,7 @@
 // group sizes (32, 64, 96, ...) use 32-K chunks.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "device.hpp"
 #include "redline_amd/rlk.h"
@@ -62,6 +63,8 @@ struct W4Args {
   int xstride;        // halves per staged x row
   int slab_off;       // bytes from the end of x to the first chunk-pair slab
   int y_ld;
+  int gq_shift;       // pair kernel: log2(group_size / 128)
+  int gpp;            // pair kernel: quantisation groups per x pass
 };
 
 constexpr int kModeF16 = 0, kModeF32 = 1, kModeSwiglu = 2;
@@ -406,6 +409,230 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
   for (int mt = 0; mt < MT; ++mt) store_tile<MODE>(a, acc[mt], 16 * mt + 4 * qd, row, r16);
 }
 
+// The pair kernel: the default for 128-K chunks, an even chunk count and a
+// power-of-two group_size / 128.  A wave owns one 16-row tile over the full K
+// and walks it in chunk pairs (256 K = 128 bytes of each row).  Each pair is
+// fetched by two load instructions of 8 rows x 128 bytes (full lines): in
+// instruction 0 the lanes with (lane & 8) == 0 load piece qd of their own
+// row r16 and the others piece 4 + qd of row r16 - 8; instruction 1 covers
+// rows 8..15 the same way.  So every lane loads 16 bytes it keeps (chunk 0 of
+// the pair in the MFMA layout: row r16, K qd*32 .. qd*32 + 31) and 16 bytes
+// that its partner lane r16 ^ 8 keeps (chunk 1), handed over by one DPP
+// row_ror:8 per dword -- no LDS round trip.
+//
+// Measured against the slab kernel above (same MFMA math): a ring of P = 4
+// pairs per wave (8 KB in flight) beats deeper rings; the last round issues
+// no refills (re-fetching the last pair in every slot cost ~2 us at the
+// Llama-3.1-8B gate_up shape); x is staged in one batch of loads; and each
+// wave stages the scales and offsets of its own 16 rows into its own LDS rows
+// with 16-byte loads, so that only x needs the workgroup barrier.
+//
+// Order of the prologue: x and scale loads, then the ring's first P pairs,
+// then the LDS stores of x and scales.  Wait counts retire in issue order, so
+// the stores wait for the staging loads only.
+template <int P, int MT, int MODE, int NB, bool kMulti>
+__global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int threads = blockDim.x, nw = threads / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, qd = lane >> 4;
+  const bool low = (lane & 8) == 0;
+  const int npairs = a.nchunks / 2, lastp = npairs - 1;
+  const int sstride = a.gpp + 1;  // dwords per staged row (odd: conflict-free column reads)
+  uint32_t* so_lds = reinterpret_cast<uint32_t*>(lds) + wave * 16 * sstride;  // this wave's rows
+  uint16_t* x_lds = reinterpret_cast<uint16_t*>(lds + static_cast<size_t>(nw) * 16 * sstride * 4);
+  const int row0 = (blockIdx.x * nw + wave) * 16;  // first row of this wave's tile
+  const int row = row0 + r16;                       // this lane's output row
+  const size_t kb = static_cast<size_t>(a.k) / 2;
+  const uint8_t* wp0 = a.w + static_cast<size_t>(min(row0 + (low ? r16 : r16 - 8), a.n - 1)) * kb +
+                       (low ? qd : 4 + qd) * 16;
+  const uint8_t* wp1 = a.w + static_cast<size_t>(min(row0 + (low ? r16 + 8 : r16), a.n - 1)) * kb +
+                       (low ? 4 + qd : qd) * 16;
+  u32x4 ring[P][2];
+  auto fetch = [&](int s, int q) {
+    ring[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp0 + q * 128));
+    ring[s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp1 + q * 128));
+  };
+
+  // x of pairs [qa, qa + cpp) -> LDS, permuted to the codes' order; vectors
+  // past the end re-load the last one (same value, no branch).
+  const int kpass = a.cpp * 256;
+  auto x_addr = [&](int v, int qa, int xvecs) {
+    v = min(v, xvecs - 1);
+    const int per = min(kpass, a.k - qa * 256) / 8;  // vectors per row in this pass
+    const int r = quot(v, 1.0f / static_cast<float>(per)), e = v - r * per;
+    return std::pair<const uint16_t*, uint16_t*>(
+        a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(qa) * 256 + e * 8,
+        x_lds + r * a.xstride + e * 8);
+  };
+  auto stage_x_rest = [&](int qa, int v_from) {  // in batches of 8 loads per thread
+    const int xvecs = a.m * (min(kpass, a.k - qa * 256) / 8);
+    for (int v0 = v_from; v0 < xvecs; v0 += 8 * threads) {
+      u32x4 val[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) val[u] = load16(x_addr(v0 + u * threads, qa, xvecs).first);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        *reinterpret_cast<f16x8*>(x_addr(v0 + u * threads, qa, xvecs).second) = x_perm(val[u]);
+    }
+  };
+  // scales and offsets of this wave's rows for groups [g0, g0 + gn): lane
+  // (qd, r16) takes row r16, 8 groups per 16-byte vector when aligned
+  const bool svec = (a.groups % 8) == 0 && (a.gpp % 8) == 0;
+  const size_t srow = static_cast<size_t>(min(row, a.n - 1)) * a.groups;
+  auto so_put = [&](int gl, u32x4 s4, u32x4 o4) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      so_lds[r16 * sstride + gl + 2 * t] = (s4[t] & 0xFFFFu) | (o4[t] << 16);
+      so_lds[r16 * sstride + gl + 2 * t + 1] = (s4[t] >> 16) | (o4[t] & 0xFFFF0000u);
+    }
+  };
+  // (vector path: vectors first_vec, first_vec + 4, ...; scalar path: groups qd, qd + 4, ...)
+  auto stage_so = [&](int g0, int gn, int first_vec) {
+    if (svec) {
+      for (int gv = first_vec; gv < gn / 8; gv += 4)
+        so_put(gv * 8, load16(a.scales + srow + g0 + gv * 8), load16(a.offsets + srow + g0 + gv * 8));
+    } else {
+      for (int g = qd; g < gn; g += 4)
+        so_lds[r16 * sstride + g] = a.scales[srow + g0 + g] |
+                                    (static_cast<uint32_t>(a.offsets[srow + g0 + g]) << 16);
+    }
+  };
+
+  {  // prologue of pass 0
+    const int xvecs = a.m * (min(kpass, a.k) / 8);
+    u32x4 xv[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) xv[u] = load16(x_addr(tid + u * threads, 0, xvecs).first);
+    const int gn = min(a.gpp, a.groups);
+    const int gv0 = min(qd, gn / 8 - 1);  // first vector of this lane (clamped; vector path)
+    u32x4 s4 = {0u, 0u, 0u, 0u}, o4 = {0u, 0u, 0u, 0u};
+    if (svec) {
+      s4 = load16(a.scales + srow + gv0 * 8);
+      o4 = load16(a.offsets + srow + gv0 * 8);
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) fetch(p, min(p, lastp));
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const auto pr = x_addr(tid + u * threads, 0, xvecs);
+      *reinterpret_cast<f16x8*>(pr.second) = x_perm(xv[u]);
+    }
+    if (svec) {
+      if (qd < gn / 8) so_put(gv0 * 8, s4, o4);
+      stage_so(0, gn, qd + 4);
+    } else {
+      stage_so(0, gn, qd);
+    }
+    stage_x_rest(0, tid + NB * threads);
+  }
+
+  const uint16_t* xl[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xl[mt] = x_lds + min(16 * mt + r16, a.m - 1) * a.xstride + qd * 32;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr f16x8 kOnes = {1, 1, 1, 1, 1, 1, 1, 1};
+  const uint32_t magic = opaque(0x54005400u);
+
+  // one 128-K chunk: c = chunk index within the pass
+  // (passes hold whole groups, so the group of chunk c is c >> gq_shift)
+  auto chunk = [&](int c, u32x4 words) {
+    f32x4 xs[MT], d[MT];
+    f16x8 xa[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      d[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xa[mt][j] = *reinterpret_cast<const f16x8*>(xl[mt] + c * 128 + 8 * j);
+        xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], kOnes, xs[mt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x8 q = codes_f16(words[j], magic);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) d[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], q, d[mt], 0, 0, 0);
+    }
+    const uint32_t so = so_lds[r16 * sstride + (c >> a.gq_shift)];
+    const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
+    const float of = fmaf(-kCodeBias, sc,
+                          static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16))));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(of, xs[mt][e], fmaf(sc, d[mt][e], acc[mt][e]));
+  };
+  // pair q (slot s) of the pass starting at pair qa
+  auto consume = [&](int q, int s, int qa) {
+    u32x4 keep, recv;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      keep[t] = low ? ring[s][0][t] : ring[s][1][t];
+      recv[t] = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(
+          static_cast<int>(low ? ring[s][1][t] : ring[s][0][t]), 0x128, 0xF, 0xF, false));  // row_ror:8
+    }
+    chunk(2 * (q - qa), keep);
+    chunk(2 * (q - qa) + 1, recv);
+  };
+
+  // The pairs [qa, qe) of one x pass.  Full rounds (every refill a valid
+  // pair) are straight-line code, so the compiler waits per ring slot; a
+  // closing round of exactly P pairs is straight-line too.  Any other shape
+  // of the last rounds tests each slot.
+  auto run_pass = [&](int qa, int qe) {
+    int qb = qa;
+    for (; qb + P <= qe && qb + 2 * P <= npairs; qb += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        consume(qb + s, s, qa);
+        fetch(s, qb + s + P);
+        // keep the refill here: left to the scheduler, all refills of a
+        // round sank to its end and the ring drained once per round
+        __builtin_amdgcn_sched_barrier(0x78F);  // only vector-memory instructions stay put
+      }
+    }
+    if (qe == npairs && qb + P == qe) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) consume(qb + s, s, qa);
+      return;
+    }
+    for (; qb < qe; qb += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        if (qb + s < qe) {
+          consume(qb + s, s, qa);
+          if (qb + s + P < npairs) fetch(s, qb + s + P);
+        }
+      }
+    }
+  };
+  __syncthreads();
+  if constexpr (!kMulti) {
+    // one pass: the rounds follow the prologue directly.  (A second inlined
+    // copy of the rounds, or a loop around them, made the compiler copy the
+    // ring registers at loop entry -- a copy waits for every load in flight.)
+    run_pass(0, npairs);
+  } else {
+    run_pass(0, a.cpp);
+    for (int qa = a.cpp; qa < npairs; qa += a.cpp) {  // further x passes (workgroup-uniform)
+      __syncthreads();  // every wave is done with the previous pass's x and scales
+      stage_x_rest(qa, tid);
+      const int g0 = (qa * 2) >> a.gq_shift;
+      stage_so(g0, min(a.gpp, a.groups - g0), qd);
+      __syncthreads();
+      run_pass(qa, min(qa + a.cpp, npairs));
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) store_tile<MODE>(a, acc[mt], 16 * mt + 4 * qd, row, r16);
+}
+
 // LDS a workgroup may take: the device allows 160 KiB per workgroup.
 constexpr size_t kLdsBudget = 160 * 1024;
 constexpr int kNoFit = 1;  // launch(): the policy's smallest x pass exceeds the LDS budget
@@ -456,15 +683,81 @@ int launch(W4Args a, int wr_max, hipStream_t stream) {
   return RLK_OK;
 }
 
-// Launch policies (K-split ways, slots in flight per wave, most row waves per
-// workgroup, chunks per slot); entry 0 -- no split, 4 chunk pairs (8 chunks)
-// in flight -- is the default, the others are selectable for tuning sweeps
-// through RLK_TUNE_W4_CFG.  32-K chunks always use the single-chunk default.
+// The pair kernel's launch: x passes of cpp pairs (a multiple of P that holds
+// whole quantisation groups), as many as the LDS budget allows.
+template <int P, int MT, int MODE>
+int launch_pairs(W4Args a, hipStream_t stream) {
+  const int gq = a.group_size / 128;
+  if (a.nchunks % 2 != 0 || (gq & (gq - 1)) != 0) return kNoFit;
+  a.gq_shift = __builtin_ctz(gq);
+  const int npairs = a.nchunks / 2;
+  const int unit = std::max(P, gq / 2);  // both powers of two
+  const int tiles = (a.n + 15) / 16;
+  const int cus = compute_units();
+  const int nw = std::max(1, std::min(kMaxWaves, (tiles + cus - 1) / cus));
+  auto lds_for = [&](int cpp) {
+    const size_t gpp = static_cast<size_t>(cpp) * 2 / gq;
+    return static_cast<size_t>(nw) * 16 * (gpp + 1) * 4 +
+           static_cast<size_t>(a.m) * (static_cast<size_t>(cpp) * 256 + 8) * 2;
+  };
+  int cpp = (npairs + unit - 1) / unit * unit;
+  while (cpp > unit && lds_for(cpp) > kLdsBudget) cpp -= unit;
+  if (lds_for(cpp) > kLdsBudget) return kNoFit;
+  const int npass = (npairs + cpp - 1) / cpp;
+  cpp = ((npairs + npass - 1) / npass + unit - 1) / unit * unit;
+  a.cpp = cpp;
+  a.npass = npass;
+  a.gpp = cpp * 2 / gq;
+  a.xstride = cpp * 256 + 8;
+  const size_t lds = lds_for(cpp);
+  const int threads = 64 * nw;
+  const int xper = (a.m * (std::min(cpp * 256, a.k) / 8) + threads - 1) / threads;
+  auto go = [&](auto kernel) -> int {
+    if (lds > 64 * 1024) {
+      static size_t granted[64] = {0};  // per device, see launch()
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || granted[dev] < lds) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(kLdsBudget));
+        if (e != hipSuccess)
+          return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
+                      hipGetErrorString(e));
+        if (dev >= 0 && dev < 64) granted[dev] = kLdsBudget;
+      }
+    }
+    kernel<<<(tiles + nw - 1) / nw, threads, lds, stream>>>(a);
+    return RLK_OK;
+  };
+  if (npass > 1) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, true>);
+  if constexpr (P == 4 || P == 2) {  // the defaults: x staged by as many loads per thread as needed
+    if (xper <= 2) return go(gemv_w4_pairs_kernel<P, MT, MODE, 2, false>);
+    if (xper <= 4) return go(gemv_w4_pairs_kernel<P, MT, MODE, 4, false>);
+    if (xper <= 8) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, false>);
+    if (xper <= 12) return go(gemv_w4_pairs_kernel<P, MT, MODE, 12, false>);
+    if (xper <= 16) return go(gemv_w4_pairs_kernel<P, MT, MODE, 16, false>);
+    if (xper <= 20) return go(gemv_w4_pairs_kernel<P, MT, MODE, 20, false>);
+  }
+  return go(gemv_w4_pairs_kernel<P, MT, MODE, 24, false>);  // the rest in a loop
+}
+
+// Launch policies, selectable for tuning sweeps through RLK_TUNE_W4_CFG.
+// Entry 0, the default, is the pair kernel with 4 pairs in flight per wave up
+// to m = 8 and 2 above; 9, 10 and 11 are the pair kernel with 2, 8 and 4
+// pairs at every m; 8 is the slab kernel with 8
+// chunk pairs in flight; 1-7 are slab-kernel variants (K-split ways, slots in
+// flight per wave, most row waves per workgroup, chunks per slot).  Shapes the
+// pair kernel does not take (an odd chunk count, group_size / 128 not a power
+// of two) use the slab kernel; 32-K chunks always use its single-chunk form.
 template <int KC, int MT, int MODE>
 int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
   int st = kNoFit;
   if constexpr (KC == 128) {
     switch (cfg) {
+      case 8: st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s); break;
+      case 9: st = launch_pairs<2, MT, MODE>(a, s); break;
+      case 10: st = launch_pairs<8, MT, MODE>(a, s); break;
+      case 11: st = launch_pairs<4, MT, MODE>(a, s); break;
       case 1: st = launch<1, 8, KC, MT, MODE>(a, 8, s); break;
       case 2: st = launch<1, 4, KC, MT, MODE, 2>(a, 8, s); break;
       case 3: st = launch<1, 6, KC, MT, MODE, 2>(a, 8, s); break;
@@ -472,8 +765,11 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
       case 5: st = launch<1, 12, KC, MT, MODE>(a, 8, s); break;
       case 6: st = launch<1, 8, KC, MT, MODE, 2>(a, 4, s); break;
       case 7: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
-      default: st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s); break;
+      default:  // measured at the Llama-3.1-8B gate_up shape: 4 pairs in flight up to m = 8, 2 above
+        st = a.m <= 8 ? launch_pairs<4, MT, MODE>(a, s) : launch_pairs<2, MT, MODE>(a, s);
+        break;
     }
+    if (st == kNoFit) st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s);
   }
   (void)cfg;
   // single-chunk slots, then shallower rings when x passes do not fit
