@@ -345,6 +345,41 @@ def gemv_bench(torch, K, m, reps, n=2 * 14336, k=4096, g=128, unfused=True, eage
     return out
 
 
+def w8_bytes(m, n, k):
+    """Algorithmic bytes of one INT8 GEMV: codes, fp16 row scales, activations
+    read once, fp16 [m, n] written."""
+    return n * k + 2 * n + m * k * 2 + m * n * 2
+
+
+def w8_bench(torch, K, m, reps, n=2 * 14336, k=4096, eager_calls=0):
+    """INT8 weight-only GEMV (gemv_w8a16) at the Llama-3.1-8B gate_up shape
+    (n = 28672, k = 4096, 117 MB of codes), fp16 out, rotating over enough
+    weight sets to exceed 2x the Infinity Cache."""
+    nb = w8_bytes(m, n, k)
+    R = max(2, -(-(640 << 20) // nb))
+    gen = torch.Generator(device="cuda").manual_seed(100 + m)
+    sets = []
+    for _ in range(R):
+        w = torch.randint(-128, 128, (n, k), generator=gen, device="cuda", dtype=torch.int8)
+        sc = (torch.rand((n,), generator=gen, device="cuda") * 0.004 + 0.001).half()
+        x = torch.randn((m, k), generator=gen, device="cuda").half()
+        sets.append((x, w, sc, torch.empty((m, n), dtype=torch.float16, device="cuda")))
+    call = lambda c: K.gemv_w8a16(c[0], m, c[1], c[2], None, n, k, c[3])  # noqa: E731
+    if eager_calls:
+        for i in range(eager_calls):
+            call(sets[i % R])
+        torch.cuda.synchronize()
+        return None
+    gph = capture(torch, lambda: [call(c) for c in sets])
+    ms = time_graph(torch, gph, reps) / R
+    del gph, sets
+    gbs = nb / (ms * 1e-3) / 1e9
+    log(f"  gemv_w8a16 m={m:2d}: {ms * 1e3:8.2f} us {gbs:8.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:5.1f}%)")
+    return {"m": m, "n": n, "k": k, "us_per_call": round(ms * 1e3, 3), "gb_per_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": nb,
+            "rotating_input_sets": R}
+
+
 def cpu_baseline(torch, data, seconds=10.0):
     """The CPU oracle (oracle/oracle.c, single thread) on the same step:
     a bounded number of full steps over one input set, copied to host."""
@@ -427,6 +462,11 @@ def main():
             print(json.dumps({"workload": w.key, "int8_kv": int8, **r}), flush=True)
         return
 
+    if args.only == "gemv_w8a16" and not args.profile_calls:
+        for m in (1, 8, 16, 32):
+            print(json.dumps(w8_bench(torch, K, m, args.reps)), flush=True)
+        return
+
     if args.only == "gemv_w4a16_swiglu" and not args.profile_calls:
         res = []
         for m in (1, 8, 16, 32):
@@ -463,6 +503,9 @@ def main():
         if args.only in (None, "gemv_w4a16_swiglu"):
             for m in (1, 8, 16, 32):
                 gemv_bench(torch, K, m, 0, eager_calls=args.profile_calls)
+        if args.only in (None, "gemv_w8a16"):
+            for m in (1, 8, 16, 32):
+                w8_bench(torch, K, m, 0, eager_calls=args.profile_calls)
         src = torch.empty(128 << 20, dtype=torch.float16, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(args.profile_calls):
@@ -526,10 +569,13 @@ def main():
             del dx
             torch.cuda.empty_cache()
 
-    gemv = []
+    gemv, w8 = [], []
     if not args.no_gemv:
         for m in (1, 8, 16, 32):
             gemv.append(gemv_bench(torch, K, m, args.reps))
+            torch.cuda.empty_cache()
+        for m in (1, 8, 16, 32):
+            w8.append(w8_bench(torch, K, m, args.reps))
             torch.cuda.empty_cache()
 
     attention = {}
@@ -567,6 +613,7 @@ def main():
         "prefill": extra,
         "decode_attention": attention,
         "gemv_w4a16_swiglu": gemv,
+        "gemv_w8a16": w8,
         "copy_baseline_gb_per_s": copy,
         "launch_floor_us": floor,
     }

@@ -157,6 +157,17 @@ inline void paged_attention_decode(const AttentionParams& p, const DecodeAttenti
                                            stream));
 }
 
+// INT8 weight-only GEMV (kernels.h:157-163 of the reference): y = (x . W^T) *
+// scales (+ bias), one fp16 scale per row.  The reference chunks batches into
+// kGemvW8MaxM = 16 rows per launch; this library serves up to 32 in one launch.
+constexpr int kGemvW8MaxM = RLK_GEMV_W8_MAX_M;
+
+inline void gemv_w8a16(const half* x, int m, const int8_t* w, const half* scales, const half* bias,
+                       int n, int k, void* y, bool y_fp32, hipStream_t stream) {
+  detail::check(rlk_gemv_w8a16(detail::bits(x), m, w, detail::bits(scales), detail::bits(bias), n,
+                               k, y, y_fp32 ? 1 : 0, stream));
+}
+
 // INT4 weight-only GEMV (kernels.h:156-171 of the reference).  The reference
 // serves m <= kGemvW4MaxM = 16 per launch; this library serves up to
 // kGemvW4MaxM here (32) in one launch.

@@ -98,8 +98,20 @@ int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, u
  * x and w 16-byte aligned. */
 #define RLK_GEMV_W4_MAX_M 32
 
+/* INT8 weight-only GEMV (decode):
+ * y[m, n] = (x[m, k] . W[n, k]^T) * scales[n] (+ bias[n]), W int8 row-major
+ * with one fp16 scale per output row (the layout of quantize_int8_rows,
+ * random_model.cpp:99-115); fp32 accumulation.  y fp16 [m, n], or fp32 when
+ * y_fp32 != 0; bias fp16 [n] or NULL.  m <= 0: no-op.  m > RLK_GEMV_W8_MAX_M:
+ * RLK_EUNSUPPORTED (the reference serves m <= 16).  k % 16 != 0: RLK_EINVAL;
+ * x and w 16-byte aligned.
+ * Replaces kernels::gemv_w8a16, gemv_weight_only.cu:217-226 (kernels.h:162-163). */
+#define RLK_GEMV_W8_MAX_M 32
+int rlk_gemv_w8a16(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales,
+                   const uint16_t* bias, int n, int k, void* y, int y_fp32, hipStream_t stream);
+
 /* y fp16 [m, n], or fp32 when y_fp32 != 0; bias fp16 [n] or NULL.
- * Replaces kernels::gemv_w4a16, gemv_weight_only.cu:222-232 (kernels.h:164-168). */
+ * Replaces kernels::gemv_w4a16, gemv_weight_only.cu:228-239 (kernels.h:164-168). */
 int rlk_gemv_w4a16(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
                    const uint16_t* offsets, int group_size, const uint16_t* bias, int n, int k,
                    void* y, int y_fp32, hipStream_t stream);
@@ -107,7 +119,7 @@ int rlk_gemv_w4a16(const uint16_t* x, int m, const uint8_t* w, const uint16_t* s
 /* SwiGLU in the GEMV epilogue: rows (2i, 2i + 1) of w are (gate_i, up_i), the
  * loader's INT4 gate_up layout (weights.cpp:157-167); y fp16 [m, n/2] =
  * fp16(fp16(silu(fp16(gate))) * fp16(up)).  n must be even.
- * Replaces kernels::gemv_w4a16_swiglu, gemv_weight_only.cu:234-241 (kernels.h:169-171). */
+ * Replaces kernels::gemv_w4a16_swiglu, gemv_weight_only.cu:241-248 (kernels.h:169-171). */
 int rlk_gemv_w4a16_swiglu(const uint16_t* x, int m, const uint8_t* w, const uint16_t* scales,
                           const uint16_t* offsets, int group_size, int n, int k, uint16_t* y,
                           hipStream_t stream);

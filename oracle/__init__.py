@@ -51,6 +51,7 @@ def lib() -> C.CDLL:
                                                _P, _I, _I, _P, _I]
         L.orc_paged_attention_decode.argtypes = [_P, _I, _P, _I, C.c_float, _P, _P, _P, _P, _I,
                                                  _I, _I, _I, _P, _I, _P, _P, _P, _I]
+        L.orc_gemv_w8a16.argtypes = [_P, _I, _P, _P, _P, _I, _I, _P]
         L.orc_gemv_w4a16.argtypes = [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P]
         L.orc_gemv_w4a16_swiglu.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P]
         L.orc_layer_step.argtypes = [_P, _P, _I, _I, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P,
@@ -155,6 +156,19 @@ def silu_and_mul(gate_up, inter, interleaved=False):
     fn = lib().orc_silu_and_mul_interleaved if interleaved else lib().orc_silu_and_mul
     fn(p(gu), rows, inter, p(out))
     return out.view(np.float16)
+
+
+def gemv_w8a16(x, w, scales, bias=None):
+    """float64 y [m, n] of x [m, k] fp16 times the INT8 W [n, k] with per-row fp16 scales."""
+    x = _u16(x)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, np.int8)
+    n = w.shape[0]
+    assert w.shape[1] == k
+    y = np.empty((m, n), np.float64)
+    lib().orc_gemv_w8a16(p(x), m, p(w), p(_u16(scales)), p(None if bias is None else _u16(bias)),
+                         n, k, p(y))
+    return y
 
 
 def gemv_w4a16(x, w, scales, offsets, group_size, bias=None):

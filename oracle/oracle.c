@@ -31,6 +31,10 @@
  *                              gathered cache, q = 0 -> mean of V, a dominant key
  *                              -> its V, invariance under physical block moves,
  *                              INT8 == FP16 path on the dequantised cache.
+ *   orc_gemv_w8a16             numpy float64 matmul of x and the int8 codes, then
+ *                              scale and bias; a code KAT (-128, -1, 0, 1, 127:
+ *                              two's complement bytes), zero weight -> bias, one-hot
+ *                              x -> scaled column, scale linearity.
  *   orc_gemv_w4a16(_swiglu)    numpy float64 matmul against a weight matrix built
  *                              first and then packed (nibble order KAT from
  *                              tests/cuda/test_gemm.cu:40-45), q = 0 -> offset
@@ -194,6 +198,29 @@ void orc_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, 
     for (int i = 0; i < inter; ++i)
       out[(size_t)r * inter + i] = swiglu1(orc_h2f(g[2 * i]), orc_h2f(g[2 * i + 1]));
   }
+}
+
+/* ------------------------------------------------------ INT8 weight-only GEMV */
+
+/* y[m, n] = (x[m, k] . W[n, k]^T) * scale[n] (+ bias[n]), W int8 row-major with
+ * one fp16 scale per row: the reference sums x * code in fp32 over K and applies
+ * the per-channel scale and the bias once, to the sum (gemv_weight_only.cu:64-93,
+ * store_outputs :19-44 with per_channel_scale; weight layout and scales from
+ * quantize_int8_rows, random_model.cpp:99-115).  Every product and sum here is
+ * float64, so y is the exact value the kernels approximate. */
+void orc_gemv_w8a16(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales,
+                    const uint16_t* bias, int n, int k, double* y) {
+  double* xs = (double*)malloc(sizeof(double) * (size_t)k);
+  for (int i = 0; i < m; ++i) {
+    for (int c = 0; c < k; ++c) xs[c] = orc_h2f(x[(size_t)i * k + c]);
+    for (int r = 0; r < n; ++r) {
+      const int8_t* row = w + (size_t)r * k;
+      double acc = 0.0;
+      for (int c = 0; c < k; ++c) acc += xs[c] * (double)row[c];
+      y[(size_t)i * n + r] = acc * orc_h2f(scales[r]) + (bias ? orc_h2f(bias[r]) : 0.0);
+    }
+  }
+  free(xs);
 }
 
 /* ------------------------------------------------------ INT4 weight-only GEMV */

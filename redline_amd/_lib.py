@@ -113,6 +113,7 @@ _SIGNATURES = {
     "rlk_paged_attention_decode_ex": (_I, [C.POINTER(AttentionParams),
                                            C.POINTER(DecodeAttentionWork),
                                            C.POINTER(AttentionOptions), _P]),
+    "rlk_gemv_w8a16": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _I, _P]),
     "rlk_gemv_w4a16": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _I, _P]),
     "rlk_gemv_w4a16_swiglu": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]),
     "rlk_float_to_half_bits": (C.c_uint16, [C.c_float]),

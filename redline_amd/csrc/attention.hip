@@ -44,21 +44,6 @@ struct AttnArgs {
 };
 
 
-// 8 int8 codes to fp16, exactly: each code + 128 (the sign bit flipped)
-// becomes the low byte of an fp16 whose high byte is 0x64, i.e. the value
-// 1024 + code + 128 (fp16 spacing is 1 on [1024, 2048)); one packed fp16
-// subtract of 1152 leaves the code.  4 byte permutes + 4 packed subtracts
-// for 8 codes.
-__device__ __forceinline__ f16x8 codes_f16(u32x2 r) {
-  const uint32_t lo = r.x ^ 0x80808080u, hi = r.y ^ 0x80808080u;
-  // v_perm_b32 selectors: bytes 0-3 of the second source, 4 = byte 0 of the
-  // first (0x64)
-  const u32x4 w = {__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u),
-                   __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
-                   __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
-                   __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
-  return __builtin_bit_cast(f16x8, w) - static_cast<_Float16>(1152);
-}
 
 template <bool kInt8>
 struct Row;
@@ -80,7 +65,7 @@ struct Row<true> {  // 8 int8 codes, 8 bytes
     return __builtin_nontemporal_load(
         reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(base) + cell * D + e0));
   }
-  __device__ static f16x8 halves(Raw r) { return codes_f16(r); }
+  __device__ static f16x8 halves(Raw r) { return int8x8_to_f16(r); }
   __device__ static f32x8 floats(Raw r) {
     return __builtin_convertvector(__builtin_bit_cast(i8x8, r), f32x8);
   }
@@ -255,7 +240,7 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
       f16x8 a;
       if constexpr (kInt8) {
         const u32x4 w = kb.r[t][st / 2];
-        a = codes_f16(st % 2 ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
+        a = int8x8_to_f16(st % 2 ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
       } else {
         a = __builtin_bit_cast(f16x8, kb.r[t][st]);
       }

@@ -430,8 +430,16 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
 // Order of the prologue: x and scale loads, then the ring's first P pairs,
 // then the LDS stores of x and scales.  Wait counts retire in issue order, so
 // the stores wait for the staging loads only.
-template <int P, int MT, int MODE, int NB, bool kMulti>
+//
+// kW8: the same walk over an INT8 weight [n, k] with one fp16 scale per row
+// (gemv_w8a16): a pair is then 128 K, a chunk 64 K, the codes become exact
+// fp16 values by byte permutes (int8x8_to_f16), the MFMAs accumulate straight
+// into the output registers, and the row scale (and bias) apply once at the
+// end.  K need only be a multiple of 16: the staged x is zero past k, and
+// code loads past the end of a row are clamped to its last 16 bytes.
+template <int P, int MT, int MODE, int NB, bool kMulti, bool kW8 = false>
 __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a) {
+  constexpr int kKP = kW8 ? 128 : 256;  // K per chunk pair
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int threads = blockDim.x, nw = threads / 64;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -444,42 +452,61 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   uint16_t* x_lds = reinterpret_cast<uint16_t*>(lds + static_cast<size_t>(nw) * 16 * sstride * 4);
   const int row0 = (blockIdx.x * nw + wave) * 16;  // first row of this wave's tile
   const int row = row0 + r16;                       // this lane's output row
-  const size_t kb = static_cast<size_t>(a.k) / 2;
-  const uint8_t* wp0 = a.w + static_cast<size_t>(min(row0 + (low ? r16 : r16 - 8), a.n - 1)) * kb +
-                       (low ? qd : 4 + qd) * 16;
-  const uint8_t* wp1 = a.w + static_cast<size_t>(min(row0 + (low ? r16 + 8 : r16), a.n - 1)) * kb +
-                       (low ? 4 + qd : qd) * 16;
+  const int kb = kW8 ? a.k : a.k / 2;  // bytes per weight row
+  const int pc0 = (low ? qd : 4 + qd) * 16, pc1 = (low ? 4 + qd : qd) * 16;
+  const uint8_t* wp0 = a.w + static_cast<size_t>(min(row0 + (low ? r16 : r16 - 8), a.n - 1)) * kb;
+  const uint8_t* wp1 = a.w + static_cast<size_t>(min(row0 + (low ? r16 + 8 : r16), a.n - 1)) * kb;
   u32x4 ring[P][2];
   auto fetch = [&](int s, int q) {
-    ring[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp0 + q * 128));
-    ring[s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp1 + q * 128));
+    int o0 = q * 128 + pc0, o1 = q * 128 + pc1;
+    if constexpr (kW8) {  // pieces past the row end (x is zero there)
+      o0 = min(o0, kb - 16);
+      o1 = min(o1, kb - 16);
+    }
+    ring[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp0 + o0));
+    ring[s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp1 + o1));
   };
 
-  // x of pairs [qa, qa + cpp) -> LDS, permuted to the codes' order; vectors
-  // past the end re-load the last one (same value, no branch).
-  const int kpass = a.cpp * 256;
+  // x of pairs [qa, qa + cpp) -> LDS (INT4: permuted to the codes' order);
+  // vectors past the end re-load the last one (same value, no branch).
+  const int kpass = a.cpp * kKP;
+  auto xcvt = [](u32x4 v) {
+    if constexpr (kW8) return __builtin_bit_cast(f16x8, v);
+    else return x_perm(v);
+  };
   auto x_addr = [&](int v, int qa, int xvecs) {
     v = min(v, xvecs - 1);
-    const int per = min(kpass, a.k - qa * 256) / 8;  // vectors per row in this pass
+    const int per = min(kpass, a.k - qa * kKP) / 8;  // vectors per row in this pass
     const int r = quot(v, 1.0f / static_cast<float>(per)), e = v - r * per;
     return std::pair<const uint16_t*, uint16_t*>(
-        a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(qa) * 256 + e * 8,
+        a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(qa) * kKP + e * 8,
         x_lds + r * a.xstride + e * 8);
   };
   auto stage_x_rest = [&](int qa, int v_from) {  // in batches of 8 loads per thread
-    const int xvecs = a.m * (min(kpass, a.k - qa * 256) / 8);
+    const int xvecs = a.m * (min(kpass, a.k - qa * kKP) / 8);
     for (int v0 = v_from; v0 < xvecs; v0 += 8 * threads) {
       u32x4 val[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) val[u] = load16(x_addr(v0 + u * threads, qa, xvecs).first);
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        *reinterpret_cast<f16x8*>(x_addr(v0 + u * threads, qa, xvecs).second) = x_perm(val[u]);
+        *reinterpret_cast<f16x8*>(x_addr(v0 + u * threads, qa, xvecs).second) = xcvt(val[u]);
+    }
+  };
+  // INT8: zeros from k to the end of the last pair (LDS stores only)
+  auto zero_x_tail = [&](int qa, int qe) {
+    if constexpr (kW8) {
+      const int real = (a.k - qa * kKP) / 8, padded = (qe - qa) * (kKP / 8);
+      if (real >= padded) return;
+      for (int i = tid; i < a.m * (padded - real); i += threads) {
+        const int r = i / (padded - real), e = real + i % (padded - real);
+        *reinterpret_cast<u32x4*>(x_lds + r * a.xstride + e * 8) = u32x4{0u, 0u, 0u, 0u};
+      }
     }
   };
   // scales and offsets of this wave's rows for groups [g0, g0 + gn): lane
   // (qd, r16) takes row r16, 8 groups per 16-byte vector when aligned
-  const bool svec = (a.groups % 8) == 0 && (a.gpp % 8) == 0;
+  const bool svec = !kW8 && (a.groups % 8) == 0 && (a.gpp % 8) == 0;
   const size_t srow = static_cast<size_t>(min(row, a.n - 1)) * a.groups;
   auto so_put = [&](int gl, u32x4 s4, u32x4 o4) {
 #pragma unroll
@@ -490,6 +517,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   };
   // (vector path: vectors first_vec, first_vec + 4, ...; scalar path: groups qd, qd + 4, ...)
   auto stage_so = [&](int g0, int gn, int first_vec) {
+    if constexpr (kW8) return;
     if (svec) {
       for (int gv = first_vec; gv < gn / 8; gv += 4)
         so_put(gv * 8, load16(a.scales + srow + g0 + gv * 8), load16(a.offsets + srow + g0 + gv * 8));
@@ -500,11 +528,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
     }
   };
 
+  uint16_t row_scale = 0;  // INT8: this lane's row scale, requested before the ring
   {  // prologue of pass 0
     const int xvecs = a.m * (min(kpass, a.k) / 8);
     u32x4 xv[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) xv[u] = load16(x_addr(tid + u * threads, 0, xvecs).first);
+    if constexpr (kW8) row_scale = a.scales[min(row, a.n - 1)];
     const int gn = min(a.gpp, a.groups);
     const int gv0 = min(qd, gn / 8 - 1);  // first vector of this lane (clamped; vector path)
     u32x4 s4 = {0u, 0u, 0u, 0u}, o4 = {0u, 0u, 0u, 0u};
@@ -517,8 +547,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const auto pr = x_addr(tid + u * threads, 0, xvecs);
-      *reinterpret_cast<f16x8*>(pr.second) = x_perm(xv[u]);
+      *reinterpret_cast<f16x8*>(pr.second) = xcvt(xv[u]);
     }
+    if (!kMulti) zero_x_tail(0, npairs);
     if (svec) {
       if (qd < gn / 8) so_put(gv0 * 8, s4, o4);
       stage_so(0, gn, qd + 4);
@@ -531,7 +562,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   const uint16_t* xl[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    xl[mt] = x_lds + min(16 * mt + r16, a.m - 1) * a.xstride + qd * 32;
+    xl[mt] = x_lds + min(16 * mt + r16, a.m - 1) * a.xstride + qd * (kW8 ? 16 : 32);
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -541,6 +572,17 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   // one 128-K chunk: c = chunk index within the pass
   // (passes hold whole groups, so the group of chunk c is c >> gq_shift)
   auto chunk = [&](int c, u32x4 words) {
+    if constexpr (kW8) {  // 64 K: two MFMA steps of 8 codes per lane, into acc directly
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f16x8 q = int8x8_to_f16(u32x2{words[2 * j], words[2 * j + 1]});
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              *reinterpret_cast<const f16x8*>(xl[mt] + c * 64 + 8 * j), q, acc[mt], 0, 0, 0);
+      }
+      return;
+    }
     f32x4 xs[MT], d[MT];
     f16x8 xa[MT][4];
 #pragma unroll
@@ -623,11 +665,17 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
     for (int qa = a.cpp; qa < npairs; qa += a.cpp) {  // further x passes (workgroup-uniform)
       __syncthreads();  // every wave is done with the previous pass's x and scales
       stage_x_rest(qa, tid);
+      zero_x_tail(qa, min(qa + a.cpp, npairs));
       const int g0 = (qa * 2) >> a.gq_shift;
       stage_so(g0, min(a.gpp, a.groups - g0), qd);
       __syncthreads();
       run_pass(qa, min(qa + a.cpp, npairs));
     }
+  }
+  if constexpr (kW8) {
+    const float s = static_cast<float>(__builtin_bit_cast(_Float16, row_scale));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] *= s;  // acc * s + bias, as gemv_weight_only.cu:36
   }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) store_tile<MODE>(a, acc[mt], 16 * mt + 4 * qd, row, r16);
@@ -685,9 +733,10 @@ int launch(W4Args a, int wr_max, hipStream_t stream) {
 
 // The pair kernel's launch: x passes of cpp pairs (a multiple of P that holds
 // whole quantisation groups), as many as the LDS budget allows.
-template <int P, int MT, int MODE>
+template <int P, int MT, int MODE, bool kW8 = false>
 int launch_pairs(W4Args a, hipStream_t stream) {
-  const int gq = a.group_size / 128;
+  constexpr int kKP = kW8 ? 128 : 256;
+  const int gq = kW8 ? 1 : a.group_size / 128;
   if (a.nchunks % 2 != 0 || (gq & (gq - 1)) != 0) return kNoFit;
   a.gq_shift = __builtin_ctz(gq);
   const int npairs = a.nchunks / 2;
@@ -696,9 +745,9 @@ int launch_pairs(W4Args a, hipStream_t stream) {
   const int cus = compute_units();
   const int nw = std::max(1, std::min(kMaxWaves, (tiles + cus - 1) / cus));
   auto lds_for = [&](int cpp) {
-    const size_t gpp = static_cast<size_t>(cpp) * 2 / gq;
+    const size_t gpp = kW8 ? 0 : static_cast<size_t>(cpp) * 2 / gq;
     return static_cast<size_t>(nw) * 16 * (gpp + 1) * 4 +
-           static_cast<size_t>(a.m) * (static_cast<size_t>(cpp) * 256 + 8) * 2;
+           static_cast<size_t>(a.m) * (static_cast<size_t>(cpp) * kKP + 8) * 2;
   };
   int cpp = (npairs + unit - 1) / unit * unit;
   while (cpp > unit && lds_for(cpp) > kLdsBudget) cpp -= unit;
@@ -707,11 +756,11 @@ int launch_pairs(W4Args a, hipStream_t stream) {
   cpp = ((npairs + npass - 1) / npass + unit - 1) / unit * unit;
   a.cpp = cpp;
   a.npass = npass;
-  a.gpp = cpp * 2 / gq;
-  a.xstride = cpp * 256 + 8;
+  a.gpp = kW8 ? 0 : cpp * 2 / gq;
+  a.xstride = cpp * kKP + 8;
   const size_t lds = lds_for(cpp);
   const int threads = 64 * nw;
-  const int xper = (a.m * (std::min(cpp * 256, a.k) / 8) + threads - 1) / threads;
+  const int xper = (a.m * (std::min(cpp * kKP, a.k) / 8) + threads - 1) / threads;
   auto go = [&](auto kernel) -> int {
     if (lds > 64 * 1024) {
       static size_t granted[64] = {0};  // per device, see launch()
@@ -729,16 +778,16 @@ int launch_pairs(W4Args a, hipStream_t stream) {
     kernel<<<(tiles + nw - 1) / nw, threads, lds, stream>>>(a);
     return RLK_OK;
   };
-  if (npass > 1) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, true>);
+  if (npass > 1) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, true, kW8>);
   if constexpr (P == 4 || P == 2) {  // the defaults: x staged by as many loads per thread as needed
-    if (xper <= 2) return go(gemv_w4_pairs_kernel<P, MT, MODE, 2, false>);
-    if (xper <= 4) return go(gemv_w4_pairs_kernel<P, MT, MODE, 4, false>);
-    if (xper <= 8) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, false>);
-    if (xper <= 12) return go(gemv_w4_pairs_kernel<P, MT, MODE, 12, false>);
-    if (xper <= 16) return go(gemv_w4_pairs_kernel<P, MT, MODE, 16, false>);
-    if (xper <= 20) return go(gemv_w4_pairs_kernel<P, MT, MODE, 20, false>);
+    if (xper <= 2) return go(gemv_w4_pairs_kernel<P, MT, MODE, 2, false, kW8>);
+    if (xper <= 4) return go(gemv_w4_pairs_kernel<P, MT, MODE, 4, false, kW8>);
+    if (xper <= 8) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, false, kW8>);
+    if (xper <= 12) return go(gemv_w4_pairs_kernel<P, MT, MODE, 12, false, kW8>);
+    if (xper <= 16) return go(gemv_w4_pairs_kernel<P, MT, MODE, 16, false, kW8>);
+    if (xper <= 20) return go(gemv_w4_pairs_kernel<P, MT, MODE, 20, false, kW8>);
   }
-  return go(gemv_w4_pairs_kernel<P, MT, MODE, 24, false>);  // the rest in a loop
+  return go(gemv_w4_pairs_kernel<P, MT, MODE, 24, false, kW8>);  // the rest in a loop
 }
 
 // Launch policies, selectable for tuning sweeps through RLK_TUNE_W4_CFG.
@@ -831,6 +880,57 @@ int gemv_w4(const char* what, const uint16_t* x, int m, const uint8_t* w, const 
   return st != RLK_OK ? st : launch_status(what);
 }
 
+// INT8 weight-only GEMV (gemv_weight_only.cu:64-93): the pair kernel's INT8
+// form with P = 4 pairs in flight (measured at the Llama-3.1-8B gate_up shape,
+// m = 1..32: equal to or faster than 2 and 8); RLK_TUNE_W8_CFG = 1, 2, 3
+// selects P = 2, 4, 8 for sweeps.
+template <int MT, int MODE>
+int dispatch_w8(const W4Args& a, hipStream_t s) {
+  switch (tune_knob("RLK_TUNE_W8_CFG", 0)) {
+    case 1: return launch_pairs<2, MT, MODE, true>(a, s);
+    case 2: return launch_pairs<4, MT, MODE, true>(a, s);
+    case 3: return launch_pairs<8, MT, MODE, true>(a, s);
+    default: return launch_pairs<4, MT, MODE, true>(a, s);
+  }
+}
+
+int gemv_w8(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales, const uint16_t* bias,
+            int n, int k, void* y, int y_fp32, hipStream_t stream) {
+  const char* what = "gemv_w8a16";
+  if (m <= 0) return RLK_OK;
+  if (x == nullptr || w == nullptr || scales == nullptr || y == nullptr)
+    return fail(RLK_EINVAL, "%s: null pointer argument", what);
+  if (m > RLK_GEMV_W8_MAX_M)
+    return fail(RLK_EUNSUPPORTED, "%s: unsupported m=%d (at most %d)", what, m, RLK_GEMV_W8_MAX_M);
+  if (n <= 0 || k <= 0 || k % 16 != 0)
+    return fail(RLK_EINVAL, "%s needs K %% 16 == 0, got %d (n=%d)", what, k, n);
+  if (k > (1 << 20))
+    return fail(RLK_EUNSUPPORTED, "%s: k=%d exceeds %d", what, k, 1 << 20);
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
+    return fail(RLK_EINVAL, "%s: x and w must be 16-byte aligned", what);
+  W4Args a{};
+  a.x = x;
+  a.w = reinterpret_cast<const uint8_t*>(w);
+  a.scales = scales;
+  a.offsets = nullptr;
+  a.bias = bias;
+  a.y = y;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.group_size = 128;  // unused by the INT8 form
+  a.groups = 0;
+  a.nchunks = 2 * ((k + 127) / 128);  // 64-K chunks, a whole number of pairs
+  a.y_ld = n;
+  int st;
+  if (y_fp32)
+    st = m <= 16 ? dispatch_w8<1, kModeF32>(a, stream) : dispatch_w8<2, kModeF32>(a, stream);
+  else
+    st = m <= 16 ? dispatch_w8<1, kModeF16>(a, stream) : dispatch_w8<2, kModeF16>(a, stream);
+  if (st == kNoFit) return fail(RLK_EUNSUPPORTED, "%s: m=%d does not fit the LDS budget", what, m);
+  return st != RLK_OK ? st : launch_status(what);
+}
+
 }  // namespace
 }  // namespace rlk
 
@@ -849,4 +949,10 @@ extern "C" int rlk_gemv_w4a16_swiglu(const uint16_t* x, int m, const uint8_t* w,
                                      hipStream_t stream) {
   return gemv_w4("gemv_w4a16_swiglu", x, m, w, scales, offsets, group_size, nullptr, n, k, y,
                  kModeSwiglu, stream);
+}
+
+extern "C" int rlk_gemv_w8a16(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales,
+                              const uint16_t* bias, int n, int k, void* y, int y_fp32,
+                              hipStream_t stream) {
+  return gemv_w8(x, m, w, scales, bias, n, k, y, y_fp32, stream);
 }

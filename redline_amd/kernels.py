@@ -21,7 +21,7 @@ __all__ = [
     "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
     "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "paged_attention_decode_ex",
     "attention_params",
-    "decode_work", "DecodeWorkspace", "kDecodePartitionSize", "gemv_w4a16", "gemv_w4a16_swiglu",
+    "decode_work", "DecodeWorkspace", "kDecodePartitionSize", "gemv_w8a16", "gemv_w4a16", "gemv_w4a16_swiglu",
     "kGemvW4MaxM",
 ]
 
@@ -100,6 +100,19 @@ def silu_and_mul_interleaved(gate_up, rows, inter, out, stream=None):
         _need(gate_up, rows * 2 * inter, "gate_up"); _need(out, rows * inter, "out")
     check(lib().rlk_silu_and_mul_interleaved(_ptr(gate_up, torch.float16, "gate_up"), rows, inter,
                                              _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def gemv_w8a16(x, m, w, scales, bias, n, k, y, y_fp32=False, stream=None):
+    """y[m, n] = (x[m, k] . w^T) * scales (+ bias): INT8 weight [n, k] with one
+    fp16 scale per row; y fp16, or fp32 with y_fp32."""
+    if m > 0 and n > 0 and k > 0:
+        _need(x, m * k, "x"); _need(w, n * k, "w"); _need(scales, n, "scales"); _need(y, m * n, "y")
+        if bias is not None:
+            _need(bias, n, "bias")
+    check(lib().rlk_gemv_w8a16(
+        _ptr(x, torch.float16, "x"), m, _ptr(w, torch.int8, "w"), _ptr(scales, torch.float16, "scales"),
+        _ptr(bias, torch.float16, "bias", True), n, k,
+        _ptr(y, torch.float32 if y_fp32 else torch.float16, "y"), int(bool(y_fp32)), _stream(stream)))
 
 
 def _gemv_w4_need(x, m, w, scales, offsets, group_size, n, k):

@@ -53,6 +53,18 @@ def assert_bits_equal(got, want, what=""):
         raise AssertionError(f"{what}: {n} elements differ bitwise")
 
 
+def int8_linear(rng: np.random.Generator, n: int, k: int, std: float = 0.05):
+    """A per-row INT8 weight in the reference's GEMV layout, quantised the way
+    quantize_int8_rows does it (src/cpu/random_model.cpp:99-115): scale =
+    fp16(amax / 127), codes = clamp(rint(w / scale), -127, 127) against the stored
+    scale.  Returns (codes int8 [n, k], scales fp16 [n], float64 W = codes * scale)."""
+    w = (rng.standard_normal((n, k)) * std).astype(np.float32)
+    amax = np.abs(w).max(axis=1)
+    s = np.where(amax > 0, amax / np.float32(127), np.float32(1)).astype(np.float16)
+    q = np.clip(np.rint(w / s.astype(np.float32)[:, None]), -127, 127).astype(np.int8)
+    return q, s, q.astype(np.float64) * s.astype(np.float64)[:, None]
+
+
 def int4_linear(rng: np.random.Generator, n: int, k: int, group_size: int, dense: bool = True):
     """A group-quantised INT4 weight in the reference's GEMV layout.
 

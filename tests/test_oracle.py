@@ -460,6 +460,70 @@ def test_attention_int8_equals_dequantised_fp64():
     assert m.mean() > 0.98 and np.array_equal(got[m], to16(want)[m])
 
 
+# ------------------------------------------------------------- INT8 GEMV
+
+def test_gemv_w8_code_kat():
+    """Codes are two's complement bytes (int8), one fp16 scale per row applied to
+    the sum, then the bias (gemv_weight_only.cu:64-93, :19-44)."""
+    k = 32
+    w = np.zeros((2, k), np.int8)
+    w[0, :5] = [-128, -1, 0, 1, 127]
+    w[1, 7] = -7
+    s = np.array([0.5, 2.0], np.float16)
+    b = np.array([0.25, -1.0], np.float16)
+    x = np.zeros((6, k), np.float16)
+    for i in range(5):
+        x[i, i] = 1
+    x[5, 7] = 3
+    y = oracle.gemv_w8a16(x, w, s, b)
+    np.testing.assert_array_equal(y[:5, 0], [-64 + 0.25, -0.5 + 0.25, 0.25, 0.5 + 0.25, 63.5 + 0.25])
+    assert y[5, 1] == -7 * 3 * 2.0 - 1.0 and y[5, 0] == 0.25
+
+
+def test_gemv_w8_against_float64_matmul():
+    from tests._util import int8_linear
+    rng = np.random.default_rng(8)
+    n, k, m = 41, 272, 6
+    q, s, w = int8_linear(rng, n, k)
+    x = randn_f16(rng, (m, k))
+    bias = randn_f16(rng, (n,), 0.1)
+    want = x.astype(np.float64) @ w.T + bias.astype(np.float64)
+    np.testing.assert_allclose(oracle.gemv_w8a16(x, q, s, bias), want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oracle.gemv_w8a16(x, q, s), want - bias.astype(np.float64),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_gemv_w8_closed_forms():
+    """Zero weight -> bias; one-hot x -> the scaled column; doubling the scale
+    doubles y - bias."""
+    rng = np.random.default_rng(9)
+    n, k = 12, 64
+    q = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    s = rng.uniform(0.001, 0.01, n).astype(np.float16)
+    b = randn_f16(rng, (n,), 0.1)
+    x = randn_f16(rng, (3, k))
+    np.testing.assert_array_equal(oracle.gemv_w8a16(x, np.zeros_like(q), s, b),
+                                  np.broadcast_to(b.astype(np.float64), (3, n)))
+    for c in (0, 31, 63):
+        e = np.zeros((1, k), np.float16)
+        e[0, c] = 1
+        np.testing.assert_array_equal(oracle.gemv_w8a16(e, q, s)[0],
+                                      q[:, c].astype(np.float64) * s.astype(np.float64))
+    y1 = oracle.gemv_w8a16(x, q, s, b) - b.astype(np.float64)
+    y2 = oracle.gemv_w8a16(x, q, (2 * s.astype(np.float32)).astype(np.float16), b) - b.astype(np.float64)
+    np.testing.assert_allclose(y2, 2 * y1, rtol=1e-14, atol=0)
+
+
+def test_int8_linear_matches_the_reference_quantiser_rules():
+    """The test weights follow quantize_int8_rows: |code| <= 127, the row's
+    absmax maps to +-127, codes round half to even against the fp16 scale."""
+    from tests._util import int8_linear
+    q, s, w = int8_linear(np.random.default_rng(3), 16, 96)
+    assert np.abs(q.astype(int)).max() <= 127
+    assert np.all(np.abs(q.astype(int)).max(axis=1) >= 126)
+    assert w.shape == (16, 96) and s.dtype == np.float16
+
+
 # ------------------------------------------------------------- INT4 GEMV
 
 def test_gemv_w4_nibble_order_kat():
