@@ -235,6 +235,37 @@ int rlk_paged_attention_decode_ex(const rlk_attention_params* params,
                                   const rlk_decode_attention_work* work,
                                   const rlk_attention_options* options, hipStream_t stream);
 
+/* Field order and types of redline::kernels::PrefillAttentionWork
+ * (kernels.h:122-129).  max_q_tiles counts the reference's 32-row query tiles
+ * (kPrefillTileQ, kernels.h:130), as BatchBuilder writes it. */
+#define RLK_PREFILL_TILE_Q 32
+typedef struct rlk_prefill_attention_work {
+  const int32_t* seq_ids; /* [num_seqs] indices into the arrays below */
+  const int32_t* q_start; /* [*] first query row of each sequence */
+  const int32_t* q_len;   /* [*] number of new tokens */
+  const int32_t* ctx_len; /* [*] total context after this step */
+  int num_seqs;
+  int max_q_tiles;        /* ceil(max q_len / RLK_PREFILL_TILE_Q) */
+} rlk_prefill_attention_work;
+
+/* Prefill attention: causal attention of each sequence's new tokens (rows
+ * q_start .. q_start + q_len - 1 of q and out) over positions [0, past + i],
+ * past = ctx_len - q_len, through the paged cache (FP16, or INT8 with fp32
+ * per-cell scales, dequantised to fp16 as the reference does).  num_seqs <= 0 or
+ * max_q_tiles <= 0: no-op; head_dim not in {64, 128}: RLK_EUNSUPPORTED;
+ * num_heads not a multiple of num_kv_heads, a null pointer, or q rows that are
+ * not 16-byte aligned: RLK_EINVAL.
+ * Replaces kernels::paged_attention_prefill, attention.cu:423-431 (kernels.h:131-132). */
+int rlk_paged_attention_prefill(const rlk_attention_params* params,
+                                const rlk_prefill_attention_work* work, hipStream_t stream);
+
+/* Extension, no counterpart in the reference: prefill attention over an INT8
+ * cache whose scales rlk_rope_and_write_kv_ex stored as fp16 (options as for
+ * rlk_paged_attention_decode_ex). */
+int rlk_paged_attention_prefill_ex(const rlk_attention_params* params,
+                                   const rlk_prefill_attention_work* work,
+                                   const rlk_attention_options* options, hipStream_t stream);
+
 /* ------------------------------------------------------ host-side helpers */
 
 /* IEEE fp16 <-> fp32 with round-to-nearest-even.

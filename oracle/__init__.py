@@ -51,6 +51,8 @@ def lib() -> C.CDLL:
                                                _P, _I, _I, _P, _I]
         L.orc_paged_attention_decode.argtypes = [_P, _I, _P, _I, C.c_float, _P, _P, _P, _P, _I,
                                                  _I, _I, _I, _P, _I, _P, _P, _P, _I]
+        L.orc_paged_attention_prefill.argtypes = [_P, _I, _P, _I, C.c_float, _P, _P, _P, _P, _I, _I,
+                                                  _I, _I, _P, _I, _P, _P, _P, _P, _I]
         L.orc_gemv_w8a16.argtypes = [_P, _I, _P, _P, _P, _I, _I, _P]
         L.orc_gemv_w4a16.argtypes = [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P]
         L.orc_gemv_w4a16_swiglu.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P]
@@ -155,6 +157,26 @@ def silu_and_mul(gate_up, inter, interleaved=False):
     out = np.empty((rows, inter), np.uint16)
     fn = lib().orc_silu_and_mul_interleaved if interleaved else lib().orc_silu_and_mul
     fn(p(gu), rows, inter, p(out))
+    return out.view(np.float16)
+
+
+def paged_attention_prefill(q, q_stride, num_heads, scale, k_cache, v_cache, k_scale, v_scale,
+                            block_tables, seq_ids, q_start, q_len, ctx_len, num_tokens, int8=False):
+    """Returns out fp16 [num_tokens, num_heads * D]; rows of tokens outside the
+    prefill sequences are zero.  Caches are [num_blocks, Hkv, bs, D]."""
+    nb, hkv, bs, D = k_cache.shape
+    out = np.zeros((num_tokens, num_heads * D), np.uint16)
+    kc = k_cache.view(np.uint16) if k_cache.dtype == np.float16 else np.ascontiguousarray(k_cache)
+    vc = v_cache.view(np.uint16) if v_cache.dtype == np.float16 else np.ascontiguousarray(v_cache)
+    bt = np.ascontiguousarray(block_tables, np.int32)
+    sid = np.ascontiguousarray(seq_ids, np.int32)
+    i32 = lambda a: np.ascontiguousarray(a, np.int32)  # noqa: E731
+    lib().orc_paged_attention_prefill(
+        p(_u16(q)), q_stride, p(out), num_heads, scale, p(kc), p(vc),
+        p(None if k_scale is None else np.ascontiguousarray(k_scale, np.float32)),
+        p(None if v_scale is None else np.ascontiguousarray(v_scale, np.float32)), bs, hkv, D,
+        int(int8), p(bt), bt.shape[1], p(sid), p(i32(q_start)), p(i32(q_len)), p(i32(ctx_len)),
+        sid.size)
     return out.view(np.float16)
 
 

@@ -31,6 +31,11 @@
  *                              gathered cache, q = 0 -> mean of V, a dominant key
  *                              -> its V, invariance under physical block moves,
  *                              INT8 == FP16 path on the dequantised cache.
+ *   orc_paged_attention_prefill  numpy float64 causal softmax attention over the
+ *                              gathered, fp16-dequantised cache; a one-token
+ *                              chunk equals the decode oracle (FP16); the first
+ *                              new token of an empty context returns its own V;
+ *                              invariance under physical block moves.
  *   orc_gemv_w8a16             numpy float64 matmul of x and the int8 codes, then
  *                              scale and bias; a code KAT (-128, -1, 0, 1, 127:
  *                              two's complement bytes), zero weight -> bias, one-hot
@@ -397,6 +402,64 @@ void orc_paged_attention_decode(const uint16_t* q, int q_stride, uint16_t* out, 
       }
       for (int d = 0; d < D; ++d)
         out[(size_t)t * num_heads * D + (size_t)h * D + d] = orc_f2h((float)(acc[d] / den));
+    }
+    free(s);
+  }
+}
+
+/* Paged prefill attention (attention.cu:210-360, launcher :399-408, entry
+ * :423-431): sequence seq_ids[z] has q_len new tokens, query rows
+ * q_start .. q_start + q_len - 1, and ctx_len keys after this step; new token i
+ * sits at position past + i (past = ctx_len - q_len) and attends to positions
+ * [0, past + i] through the block table.  INT8 K and V are dequantised the way
+ * the reference's tile loader does it, fp16(float(code) * scale) (:266-274),
+ * and FP16 ones are read as they are.  Evaluated in double:
+ * s_j = (q . k_j) * scale, p = softmax(s), out = fp16(sum_j p_j v_j).  The
+ * kernel's tiling and online softmax are exact identities of this formula. */
+static double prefill_kv(const void* cache, const float* scl, size_t cell, int D, int d, int int8) {
+  if (!int8) return (double)orc_h2f(((const uint16_t*)cache)[cell * D + d]);
+  const float x = (float)((const int8_t*)cache)[cell * D + d] * scl[cell];
+  return (double)orc_h2f(orc_f2h(x));
+}
+
+void orc_paged_attention_prefill(const uint16_t* q, int q_stride, uint16_t* out, int num_heads,
+                                 float scale, const void* k_cache, const void* v_cache,
+                                 const float* k_scale, const float* v_scale, int bs, int Hkv,
+                                 int D, int int8, const int32_t* block_tables, int max_blocks,
+                                 const int32_t* seq_ids, const int32_t* q_start,
+                                 const int32_t* q_len, const int32_t* ctx_len, int num_seqs) {
+  const int G = num_heads / Hkv;
+  for (int z = 0; z < num_seqs; ++z) {
+    const int seq = seq_ids[z], n = q_len[seq], q0 = q_start[seq], ctx = ctx_len[seq];
+    const int past = ctx - n;
+    const int32_t* table = block_tables + (size_t)seq * max_blocks;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(ctx > 0 ? ctx : 1));
+    double acc[256];
+    for (int i = 0; i < n; ++i) {
+      const int keys = past + i + 1;
+      for (int h = 0; h < num_heads; ++h) {
+        const int kvh = h / G;
+        const uint16_t* qh = q + (size_t)(q0 + i) * q_stride + (size_t)h * D;
+        double mx = -INFINITY;
+        for (int j = 0; j < keys; ++j) {
+          const size_t cell = ((size_t)table[j / bs] * Hkv + kvh) * bs + j % bs;
+          double dot = 0.0;
+          for (int d = 0; d < D; ++d)
+            dot += (double)orc_h2f(qh[d]) * prefill_kv(k_cache, k_scale, cell, D, d, int8);
+          s[j] = dot * (double)scale;
+          if (s[j] > mx) mx = s[j];
+        }
+        double den = 0.0;
+        for (int d = 0; d < D; ++d) acc[d] = 0.0;
+        for (int j = 0; j < keys; ++j) {
+          const double e = exp(s[j] - mx);
+          den += e;
+          const size_t cell = ((size_t)table[j / bs] * Hkv + kvh) * bs + j % bs;
+          for (int d = 0; d < D; ++d) acc[d] += e * prefill_kv(v_cache, v_scale, cell, D, d, int8);
+        }
+        for (int d = 0; d < D; ++d)
+          out[(size_t)(q0 + i) * num_heads * D + (size_t)h * D + d] = orc_f2h((float)(acc[d] / den));
+      }
     }
     free(s);
   }

@@ -78,6 +78,13 @@ class DecodeAttentionWork(C.Structure):
                 ("ws_sum", C.c_void_p)]
 
 
+class PrefillAttentionWork(C.Structure):
+    """Mirror of rlk_prefill_attention_work / kernels::PrefillAttentionWork."""
+
+    _fields_ = [("seq_ids", C.c_void_p), ("q_start", C.c_void_p), ("q_len", C.c_void_p),
+                ("ctx_len", C.c_void_p), ("num_seqs", C.c_int), ("max_q_tiles", C.c_int)]
+
+
 class BatchShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in (
         "num_tokens", "num_seqs", "num_logit_rows", "num_decode_items",
@@ -113,6 +120,11 @@ _SIGNATURES = {
     "rlk_paged_attention_decode_ex": (_I, [C.POINTER(AttentionParams),
                                            C.POINTER(DecodeAttentionWork),
                                            C.POINTER(AttentionOptions), _P]),
+    "rlk_paged_attention_prefill": (_I, [C.POINTER(AttentionParams),
+                                         C.POINTER(PrefillAttentionWork), _P]),
+    "rlk_paged_attention_prefill_ex": (_I, [C.POINTER(AttentionParams),
+                                            C.POINTER(PrefillAttentionWork),
+                                            C.POINTER(AttentionOptions), _P]),
     "rlk_gemv_w8a16": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _I, _P]),
     "rlk_gemv_w4a16": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _I, _P]),
     "rlk_gemv_w4a16_swiglu": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]),

@@ -20,7 +20,8 @@ LIB = PKG / "librlk.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["elementwise.hip", "rope_kv.hip", "attention.hip", "gemv_w4.hip", "host.cpp", "status.cpp"]
+SOURCES = ["elementwise.hip", "rope_kv.hip", "attention.hip", "prefill.hip", "gemv_w4.hip", "host.cpp",
+           "status.cpp"]
 
 COMMON = [
     "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wextra",

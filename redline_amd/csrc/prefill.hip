@@ -1,0 +1,325 @@
+// Paged prefill attention over the block-structured KV cache, for gfx950.
+//
+// Causal (flash-attention style) attention for sequences that process several
+// new tokens against cached + new keys, with the reference's work contract
+// (src/cuda/kernels/attention.cu:210-360, launcher :399-408, entry :423-431 in
+// Neil456/Redline): sequence seq_ids[z] has q_len new tokens at query rows
+// q_start .. q_start + q_len - 1; new token i sits at position
+// past + i = ctx_len - q_len + i and attends to positions [0, past + i].
+//
+// The mapping is wave64 and matrix-core first:
+//   * a workgroup of 4 waves takes (sequence, 64 query rows, head); a wave owns
+//     16 query rows and keeps their q in registers as MFMA B operands;
+//   * K and V tiles of 64 keys are staged once per workgroup in LDS (K
+//     row-major, V transposed), with the next tile's loads in flight while the
+//     current one is computed; INT8 codes are dequantised on the way, to
+//     fp16(float(code) * scale) as the reference's tile loader does;
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_f16: the output gives each lane one
+//     query row (its column) and 16 keys of the tile, so the online softmax
+//     (max, sum, rescale) is per lane with one cross-row reduction;
+//   * O^T = V^T P^T on the same instruction: the probabilities a lane holds are
+//     exactly its B operand (the keys of a 32-key step taken in the order the
+//     S^T output hands them over), and the output again gives each lane its
+//     own query row, so the running max and sum never leave the lane.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+#include <type_traits>
+
+#include "device.hpp"
+#include "redline_amd/rlk.h"
+#include "status.hpp"
+
+namespace rlk {
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPfThreads = 256;  // 4 waves
+constexpr int kBQ = 64;          // query rows per workgroup (16 per wave)
+constexpr int kBK = 64;          // keys per tile
+constexpr int kKPad = 8;         // halves of padding per K row
+constexpr int kVPad = 8;         // halves of padding per V^T row
+
+struct PrefillArgs {
+  rlk_attention_params p;
+  rlk_prefill_attention_work w;
+  int scale16;  // INT8 scales stored as fp16 (extension)
+};
+
+template <int D, bool kInt8>
+struct PfTile {
+  // per thread: K chunks (8 dims of one key) and V chunk pairs (8 dims of two keys)
+  static constexpr int kKChunks = kBK * D / 8 / kPfThreads;
+  static constexpr int kVPairs = kKChunks / 2;
+  using Raw = typename std::conditional<kInt8, u32x2, u32x4>::type;
+  Raw k[kKChunks];
+  float ks[kKChunks];
+  Raw v[kVPairs][2];
+  float vs[kVPairs][2];
+};
+
+template <bool kInt8>
+__device__ __forceinline__ f16x8 dequant8(typename std::conditional<kInt8, u32x2, u32x4>::type r,
+                                          float s) {
+  if constexpr (kInt8) {
+    // fp16(float(code) * scale), as attention.cu:266-274
+    const uint32_t w[2] = {r.x, r.y};
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int code = static_cast<int8_t>((w[i / 4] >> (8 * (i % 4))) & 0xFF);
+      h[i] = static_cast<_Float16>(static_cast<float>(code) * s);
+    }
+    return h;
+  } else {
+    (void)s;
+    return __builtin_bit_cast(f16x8, r);
+  }
+}
+
+template <int D, bool kInt8>
+__global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillArgs a) {
+  using Tile = PfTile<D, kInt8>;
+  constexpr int kSteps = D / 32, kDTiles = D / 16, kChunksPerRow = D / 8;
+  __shared__ __attribute__((aligned(16))) _Float16 k_lds[kBK][D + kKPad];
+  __shared__ __attribute__((aligned(16))) _Float16 vt_lds[D][kBK + kVPad];
+
+  const rlk_attention_params& p = a.p;
+  const rlk_prefill_attention_work& w = a.w;
+  const int qt = blockIdx.x, h = blockIdx.y;
+  const int seq = w.seq_ids[blockIdx.z];
+  const int q_len = w.q_len[seq];
+  if (qt * kBQ >= q_len) return;  // workgroup-uniform
+  const int q0 = w.q_start[seq], ctx = w.ctx_len[seq];
+  const int past = ctx - q_len;
+  const int hkv = p.kv.num_kv_heads, bs = p.kv.block_size;
+  const int kvh = h / (p.num_heads / hkv);
+  const int32_t* table = p.block_tables + static_cast<size_t>(seq) * p.max_blocks_per_seq;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, qd = lane >> 4;
+  const int qi = qt * kBQ + wave * 16 + c16;  // this lane's query row (index among the new tokens)
+  const bool qvalid = qi < q_len;
+  const int qpos = past + qi;
+  const int kv_end = past + min(q_len, (qt + 1) * kBQ);
+  const int wave_rows = min(q_len, qt * kBQ + wave * 16 + 16) - (qt * kBQ + wave * 16);
+  const int wave_kv_end = wave_rows > 0 ? past + qt * kBQ + wave * 16 + wave_rows : 0;
+
+  // q of this lane's row as B operands: lane (qd, c16) holds dims 32 ks + 8 qd .. + 8
+  f16x8 qb[kSteps];
+#pragma unroll
+  for (int ks = 0; ks < kSteps; ++ks) {
+    qb[ks] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (qvalid)
+      qb[ks] = __builtin_bit_cast(
+          f16x8, load16(p.q + static_cast<size_t>(q0 + qi) * p.q_stride + h * D + 32 * ks + 8 * qd));
+  }
+
+  const float* kscale32 = p.kv.k_scale;
+  const float* vscale32 = p.kv.v_scale;
+  auto cell_of = [&](int pos) {
+    return (static_cast<size_t>(table[pos / bs]) * hkv + kvh) * bs + pos % bs;
+  };
+  auto scale_at = [&](const float* s32, size_t cell) {
+    if (a.scale16)
+      return static_cast<float>(__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t*>(s32)[cell]));
+    return s32[cell];
+  };
+  auto load_row = [&](const void* base, size_t cell, int ch) {
+    if constexpr (kInt8)
+      return *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(base) + cell * D + ch * 8);
+    else
+      return load16(static_cast<const uint16_t*>(base) + cell * D + ch * 8);
+  };
+  auto zero_raw = []() {
+    if constexpr (kInt8) return u32x2{0u, 0u};
+    else return u32x4{0u, 0u, 0u, 0u};
+  };
+
+  // keys past kv_end are zero (never attended: they lie past every row's position)
+  Tile st;
+  auto stage_load = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < Tile::kKChunks; ++u) {
+      const int i = tid + kPfThreads * u, r = i / kChunksPerRow, ch = i % kChunksPerRow;
+      const int pos = k0 + r;
+      st.k[u] = zero_raw();
+      st.ks[u] = 0.f;
+      if (pos < kv_end) {
+        const size_t cell = cell_of(pos);
+        st.k[u] = load_row(p.kv.k, cell, ch);
+        if constexpr (kInt8) st.ks[u] = scale_at(kscale32, cell);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < Tile::kVPairs; ++u) {
+      const int i = tid + kPfThreads * u, kp = i / kChunksPerRow, ch = i % kChunksPerRow;
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int pos = k0 + 2 * kp + x;
+        st.v[u][x] = zero_raw();
+        st.vs[u][x] = 0.f;
+        if (pos < kv_end) {
+          const size_t cell = cell_of(pos);
+          st.v[u][x] = load_row(p.kv.v, cell, ch);
+          if constexpr (kInt8) st.vs[u][x] = scale_at(vscale32, cell);
+        }
+      }
+    }
+  };
+  auto stage_store = [&]() {
+#pragma unroll
+    for (int u = 0; u < Tile::kKChunks; ++u) {
+      const int i = tid + kPfThreads * u, r = i / kChunksPerRow, ch = i % kChunksPerRow;
+      *reinterpret_cast<f16x8*>(&k_lds[r][ch * 8]) = dequant8<kInt8>(st.k[u], st.ks[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < Tile::kVPairs; ++u) {
+      const int i = tid + kPfThreads * u, kp = i / kChunksPerRow, ch = i % kChunksPerRow;
+      const f16x8 v0 = dequant8<kInt8>(st.v[u][0], st.vs[u][0]);
+      const f16x8 v1 = dequant8<kInt8>(st.v[u][1], st.vs[u][1]);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {  // V^T[dim][key pair]
+        const f16x2 pr = {v0[d], v1[d]};
+        *reinterpret_cast<f16x2*>(&vt_lds[ch * 8 + d][2 * kp]) = pr;
+      }
+    }
+  };
+
+  f32x4 o[kDTiles];
+#pragma unroll
+  for (int dt = 0; dt < kDTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -FLT_MAX, l_run = 0.f;
+
+  auto compute = [&](int k0) {
+    // S^T for 4 subtiles of 16 keys: lane (qd, c16) gets keys k0 + 16 t + 4 qd + e of row c16
+    f32x4 s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks)
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            *reinterpret_cast<const f16x8*>(&k_lds[16 * t + c16][32 * ks + 8 * qd]), qb[ks], s[t], 0,
+            0, 0);
+    }
+    float mt = -FLT_MAX;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kp = k0 + 16 * t + 4 * qd + e;
+        s[t][e] = (qvalid && kp <= qpos) ? s[t][e] * p.scale : -FLT_MAX;
+        mt = fmaxf(mt, s[t][e]);
+      }
+    mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = m_run == -FLT_MAX ? 0.f : __expf(m_run - m_new);
+    float ts = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[t][e] = s[t][e] == -FLT_MAX ? 0.f : __expf(s[t][e] - m_new);
+        ts += s[t][e];
+      }
+    ts = rows_sum<true>(rows_sum<false>(ts));
+    l_run = l_run * alpha + ts;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) o[dt] *= alpha;
+    // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
+    // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const f16x8 pb = {static_cast<_Float16>(s[2 * j][0]), static_cast<_Float16>(s[2 * j][1]),
+                        static_cast<_Float16>(s[2 * j][2]), static_cast<_Float16>(s[2 * j][3]),
+                        static_cast<_Float16>(s[2 * j + 1][0]), static_cast<_Float16>(s[2 * j + 1][1]),
+                        static_cast<_Float16>(s[2 * j + 1][2]), static_cast<_Float16>(s[2 * j + 1][3])};
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(&vt_lds[16 * dt + c16][32 * j + 4 * qd]);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(&vt_lds[16 * dt + c16][32 * j + 16 + 4 * qd]);
+        const f16x8 va = __builtin_bit_cast(f16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[dt], 0, 0, 0);
+      }
+    }
+  };
+
+  const int ntiles = (kv_end + kBK - 1) / kBK;
+  stage_load(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();  // the previous tile is consumed
+    stage_store();
+    __syncthreads();
+    if (t + 1 < ntiles) stage_load((t + 1) * kBK);  // in flight during this tile
+    if (t * kBK < wave_kv_end) compute(t * kBK);
+  }
+
+  if (qvalid) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    uint16_t* out = p.out + static_cast<size_t>(q0 + qi) * p.num_heads * D + h * D + 4 * qd;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      // lane (qd, c16) holds dims 16 dt + 4 qd + e of row c16
+      const f16x4 r = {static_cast<_Float16>(o[dt][0] * inv), static_cast<_Float16>(o[dt][1] * inv),
+                       static_cast<_Float16>(o[dt][2] * inv), static_cast<_Float16>(o[dt][3] * inv)};
+      *reinterpret_cast<f16x4*>(out + 16 * dt) = r;
+    }
+  }
+}
+
+int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work* work,
+            int scale16, hipStream_t stream) {
+  const char* what = "paged_attention_prefill";
+  if (params == nullptr || work == nullptr) return fail(RLK_EINVAL, "%s: null argument", what);
+  const rlk_attention_params& p = *params;
+  const rlk_prefill_attention_work& w = *work;
+  if (w.num_seqs <= 0 || w.max_q_tiles <= 0) return RLK_OK;
+  if (p.kv.num_kv_heads <= 0 || p.num_heads <= 0 || p.num_heads % p.kv.num_kv_heads != 0)
+    return fail(RLK_EINVAL, "%s: num_heads must be a multiple of num_kv_heads", what);
+  if (p.kv.head_dim != 64 && p.kv.head_dim != 128)
+    return fail(RLK_EUNSUPPORTED, "%s: unsupported head_dim %d", what, p.kv.head_dim);
+  if (p.kv.block_size <= 0) return fail(RLK_EINVAL, "%s: bad block_size %d", what, p.kv.block_size);
+  const bool int8 = p.kv.dtype == RLK_KV_INT8;
+  if (p.q == nullptr || p.out == nullptr || p.kv.k == nullptr || p.kv.v == nullptr ||
+      p.block_tables == nullptr || w.seq_ids == nullptr || w.q_start == nullptr ||
+      w.q_len == nullptr || w.ctx_len == nullptr ||
+      (int8 && (p.kv.k_scale == nullptr || p.kv.v_scale == nullptr)))
+    return fail(RLK_EINVAL, "%s: null pointer argument", what);
+  if (reinterpret_cast<uintptr_t>(p.q) % 16 != 0 || p.q_stride % 8 != 0)
+    return fail(RLK_EINVAL, "%s: q rows must be 16-byte aligned (q_stride %d)", what, p.q_stride);
+  PrefillArgs a{p, w, scale16};
+  // the work's tiles are the reference's 32-row tiles (kPrefillTileQ); ours hold 64 rows
+  const dim3 grid((w.max_q_tiles * RLK_PREFILL_TILE_Q + kBQ - 1) / kBQ, p.num_heads, w.num_seqs);
+  if (p.kv.head_dim == 64) {
+    if (int8) prefill_attention_kernel<64, true><<<grid, kPfThreads, 0, stream>>>(a);
+    else prefill_attention_kernel<64, false><<<grid, kPfThreads, 0, stream>>>(a);
+  } else {
+    if (int8) prefill_attention_kernel<128, true><<<grid, kPfThreads, 0, stream>>>(a);
+    else prefill_attention_kernel<128, false><<<grid, kPfThreads, 0, stream>>>(a);
+  }
+  return launch_status(what);
+}
+
+}  // namespace
+}  // namespace rlk
+
+using namespace rlk;
+
+extern "C" int rlk_paged_attention_prefill(const rlk_attention_params* params,
+                                           const rlk_prefill_attention_work* work,
+                                           hipStream_t stream) {
+  return prefill(params, work, 0, stream);
+}
+
+extern "C" int rlk_paged_attention_prefill_ex(const rlk_attention_params* params,
+                                              const rlk_prefill_attention_work* work,
+                                              const rlk_attention_options* options,
+                                              hipStream_t stream) {
+  const int s16 = options != nullptr && options->scale_dtype == RLK_SCALE_F16;
+  return prefill(params, work, s16, stream);
+}

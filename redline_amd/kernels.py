@@ -21,7 +21,8 @@ __all__ = [
     "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
     "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "paged_attention_decode_ex",
     "attention_params",
-    "decode_work", "DecodeWorkspace", "kDecodePartitionSize", "gemv_w8a16", "gemv_w4a16", "gemv_w4a16_swiglu",
+    "decode_work", "prefill_work", "paged_attention_prefill", "paged_attention_prefill_ex",
+    "DecodeWorkspace", "kDecodePartitionSize", "gemv_w8a16", "gemv_w4a16", "gemv_w4a16_swiglu",
     "kGemvW4MaxM",
 ]
 
@@ -211,6 +212,28 @@ def decode_work(item_token, item_seq, num_items, max_partitions, workspace=None)
         num_items, max_partitions,
         None if ws is None else ws.out.data_ptr(), None if ws is None else ws.max.data_ptr(),
         None if ws is None else ws.sum.data_ptr())
+
+
+def prefill_work(seq_ids, q_start, q_len, ctx_len, num_seqs, max_q_tiles):
+    """kernels::PrefillAttentionWork (max_q_tiles in 32-row tiles, as BatchBuilder writes it)."""
+    return _lib.PrefillAttentionWork(
+        _ptr(seq_ids, torch.int32, "seq_ids"), _ptr(q_start, torch.int32, "q_start"),
+        _ptr(q_len, torch.int32, "q_len"), _ptr(ctx_len, torch.int32, "ctx_len"), num_seqs,
+        max_q_tiles)
+
+
+def paged_attention_prefill(params: _lib.AttentionParams, work: _lib.PrefillAttentionWork,
+                            stream=None):
+    """Causal paged prefill attention (kernels::paged_attention_prefill)."""
+    check(lib().rlk_paged_attention_prefill(C.byref(params), C.byref(work), _stream(stream)))
+
+
+def paged_attention_prefill_ex(params: _lib.AttentionParams, work: _lib.PrefillAttentionWork,
+                               scale_dtype=SCALE_F32, stream=None):
+    """Extension: prefill attention over an INT8 cache with fp16 scales."""
+    opt = _lib.AttentionOptions(scale_dtype)
+    check(lib().rlk_paged_attention_prefill_ex(C.byref(params), C.byref(work), C.byref(opt),
+                                               _stream(stream)))
 
 
 class DecodeWorkspace:

@@ -460,6 +460,93 @@ def test_attention_int8_equals_dequantised_fp64():
     assert m.mean() > 0.98 and np.array_equal(got[m], to16(want)[m])
 
 
+# ------------------------------------------------------------- prefill attention
+
+def _prefill_case(rng, chunks, hq, hkv, D, bs=16, int8=False):
+    """Sequences given as (past, q_len): random paged caches holding past + q_len
+    positions each; the new tokens' q rows are packed one sequence after the other."""
+    lens = [a + b for a, b in chunks]
+    q, kc, vc, ks, vs, tables, _ = _attn_case(rng, lens, hq, hkv, D, bs, int8)
+    q_len = np.array([b for _, b in chunks], np.int32)
+    q_start = np.concatenate([[0], np.cumsum(q_len)[:-1]]).astype(np.int32)
+    T = int(q_len.sum())
+    q = randn_f16(rng, (T, hq * D))
+    return q, kc, vc, ks, vs, tables, q_start, q_len, np.array(lens, np.int32), T
+
+
+def _prefill_numpy(q, kc, vc, ks, vs, tables, q_start, q_len, ctx, hq, hkv, D, scale, bs=16):
+    """float64 causal attention; INT8 dequantised through fp16 as the reference's tile loader does."""
+    from scipy.special import softmax
+    G = hq // hkv
+    if ks is None:
+        K, V = kc.astype(np.float64), vc.astype(np.float64)
+    else:
+        K = (kc.astype(np.float32) * ks[..., None]).astype(np.float16).astype(np.float64)
+        V = (vc.astype(np.float32) * vs[..., None]).astype(np.float16).astype(np.float64)
+    out = np.zeros((q.shape[0], hq * D))
+    for s_ in range(len(q_len)):
+        past = ctx[s_] - q_len[s_]
+        for i in range(q_len[s_]):
+            js = np.arange(past + i + 1)
+            blk = tables[s_, js // bs]
+            row = q_start[s_] + i
+            for h in range(hq):
+                k, v = K[blk, h // G, js % bs], V[blk, h // G, js % bs]
+                sc = (q[row, h * D:(h + 1) * D].astype(np.float64) @ k.T) * np.float64(np.float32(scale))
+                out[row, h * D:(h + 1) * D] = softmax(sc) @ v
+    return out
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_prefill_attention_against_scipy_softmax(int8):
+    rng = np.random.default_rng(30 + int8)
+    hq, hkv, D = 4, 2, 64
+    chunks = [(0, 37), (50, 20), (0, 1), (16, 16)]
+    q, kc, vc, ks, vs, tables, q_start, q_len, ctx, T = _prefill_case(rng, chunks, hq, hkv, D, int8=int8)
+    scale = 1 / np.sqrt(D)
+    sid = np.arange(len(chunks))
+    got = oracle.paged_attention_prefill(q, hq * D, hq, scale, kc, vc, ks, vs, tables, sid, q_start,
+                                         q_len, ctx, T, int8)
+    want = _prefill_numpy(q, kc, vc, ks, vs, tables, q_start, q_len, ctx, hq, hkv, D, scale)
+    m = safe(want)
+    assert m.mean() > 0.98 and np.array_equal(got[m], to16(want)[m])
+
+
+def test_prefill_attention_closed_forms_and_decode_equivalence():
+    """A one-token chunk at position p equals decode attention at p (FP16
+    cache); the first token of an empty context returns its own V row; moving
+    blocks to other physical slots (and the table with them) changes nothing;
+    only the rows of the listed sequences are written."""
+    rng = np.random.default_rng(31)
+    hq, hkv, D, bs = 8, 2, 128, 16
+    chunks = [(40, 1), (0, 5), (100, 1)]
+    q, kc, vc, ks, vs, tables, q_start, q_len, ctx, T = _prefill_case(rng, chunks, hq, hkv, D, bs)
+    scale = 0.125
+    sid = np.arange(3)
+    got = oracle.paged_attention_prefill(q, hq * D, hq, scale, kc, vc, None, None, tables, sid,
+                                         q_start, q_len, ctx, T)
+    for s_, row in ((0, 0), (2, 6)):
+        dec = oracle.paged_attention_decode(q, hq * D, hq, scale, kc, vc, None, None, tables,
+                                            np.array([ctx[s_] - 1] * T, np.int32),
+                                            np.array([row]), np.array([s_]), T)
+        np.testing.assert_array_equal(got[row].view(np.uint16), dec[row].view(np.uint16))
+    blk0 = tables[1, 0]
+    for h in range(hq):
+        np.testing.assert_array_equal(got[1, h * D:(h + 1) * D].view(np.uint16),
+                                      vc[blk0, h // (hq // hkv), 0].view(np.uint16))
+    # physical moves: permute every block id and the cache rows with them
+    perm = np.concatenate([[0], rng.permutation(np.arange(1, kc.shape[0]))])
+    kc2, vc2 = np.empty_like(kc), np.empty_like(vc)
+    kc2[perm], vc2[perm] = kc, vc
+    moved = oracle.paged_attention_prefill(q, hq * D, hq, scale, kc2, vc2, None, None, perm[tables],
+                                           sid, q_start, q_len, ctx, T)
+    np.testing.assert_array_equal(moved.view(np.uint16), got.view(np.uint16))
+    only = oracle.paged_attention_prefill(q, hq * D, hq, scale, kc, vc, None, None, tables,
+                                          np.array([1]), q_start, q_len, ctx, T)
+    assert not only[[0, 6]].view(np.uint16).any()
+    np.testing.assert_array_equal(only[1:6].view(np.uint16), got[1:6].view(np.uint16))
+
+
 # ------------------------------------------------------------- INT8 GEMV
 
 def test_gemv_w8_code_kat():
