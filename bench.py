@@ -294,6 +294,73 @@ def attention_bench(torch, K, w, int8, reps, rotations=3, seed=0, eager_calls=0)
             "bytes_per_call": int(nbytes / rotations)}
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix-core peak
+
+
+def prefill_flops(w):
+    """Algorithmic flops of the workload's prefill attention: every causal
+    (query, key) pair costs 2 D for q . k and 2 D for p . v, per query head."""
+    m = w.model
+    pairs = sum(s.n * s.start + s.n * (s.n + 1) // 2 for s in w.segments if s.n > 1)
+    return 4 * m.head_dim * m.hq * pairs
+
+
+def prefill_attention_bench(torch, K, w, reps, rotations=2, seed=0, eager_calls=0):
+    """Prefill attention over the workload's prefill sequences (q_len > 1) in
+    the workload's cache format, rotating over `rotations` batches drawn from
+    one KV pool filled at random; reported against the fp16 MFMA peak."""
+    from redline_amd.configs import build_batch
+    m = w.model
+    D = m.head_dim
+    int8 = w.kv_int8
+    sdt = K.SCALE_F16 if (int8 and w.kv_scale_f16) else K.SCALE_F32
+    cache = K.KVCache(1, w.num_blocks, m.hkv, D, w.block_size,
+                      K.KVDType.kINT8 if int8 else K.KVDType.kFP16)
+    k, v, ks, vs = cache.tensors(0)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    if int8:
+        k.copy_(torch.randint(-127, 128, k.shape, generator=g, device="cuda", dtype=torch.int8))
+        v.copy_(torch.randint(-127, 128, v.shape, generator=g, device="cuda", dtype=torch.int8))
+        if sdt == K.SCALE_F16:
+            ks.view(torch.float16).fill_(0.01)
+            vs.view(torch.float16).fill_(0.01)
+        else:
+            ks.fill_(0.01)
+            vs.fill_(0.01)
+    else:
+        k.normal_(generator=g)
+        v.normal_(generator=g)
+    calls = []
+    for r in range(rotations):
+        meta, shape, lay, tables = build_batch(w, np.random.default_rng(seed * 100 + r + 11))
+        T = w.num_tokens
+        d_meta = torch.from_numpy(meta[:lay["total_words"]]).cuda()
+        qkv = torch.randn((T, m.qkv_cols), generator=g, device="cuda").half()
+        out = torch.empty((T, m.hq * D), dtype=torch.float16, device="cuda")
+        sl = lambda name: d_meta[lay[name]:]  # noqa: E731
+        p = K.attention_params(qkv, m.qkv_cols, out, m.hq, D ** -0.5, cache.layer(0),
+                               sl("block_tables"), max(len(t) for t in tables), sl("positions"))
+        wk = K.prefill_work(sl("prefill_seq"), sl("seq_q_start"), sl("seq_q_len"), sl("seq_ctx_len"),
+                            shape.num_prefill_seqs, shape.max_prefill_q_tiles)
+        calls.append((p, wk, qkv, out, d_meta))
+    run = lambda c: K.paged_attention_prefill_ex(c[0], c[1], sdt)  # noqa: E731
+    if eager_calls:
+        for i in range(eager_calls):
+            run(calls[i % rotations])
+        torch.cuda.synchronize()
+        return None
+    gph = capture(torch, lambda: [run(c) for c in calls])
+    ms = time_graph(torch, gph, reps) / rotations
+    del gph
+    fl = prefill_flops(w)
+    tfs = fl / (ms * 1e-3) / 1e12
+    log(f"  {w.key} paged_attention_prefill {'INT8' if int8 else 'FP16'} KV: {ms * 1e3:9.1f} us "
+        f"{tfs:7.1f} TFLOP/s ({100 * tfs / MFMA_F16_PEAK_TFLOPS:5.1f}% of the fp16 MFMA peak)")
+    return {"us_per_call": round(ms * 1e3, 2), "tflop_per_s": round(tfs, 1),
+            "frac_of_mfma_f16_peak": round(tfs / MFMA_F16_PEAK_TFLOPS, 4), "flops_per_call": fl,
+            "kv": "int8" + ("_f16scale" if sdt == K.SCALE_F16 else "") if int8 else "fp16"}
+
+
 def gemv_bytes(m, n, k, g):
     """Algorithmic bytes of one INT4 GEMV with SwiGLU epilogue: codes, fp16
     scales and offsets, activations read once, fp16 [m, n/2] written."""
@@ -462,6 +529,13 @@ def main():
             print(json.dumps({"workload": w.key, "int8_kv": int8, **r}), flush=True)
         return
 
+    if args.only == "paged_attention_prefill" and not args.profile_calls:
+        for key in ("C3", "C4", "C5"):
+            r = prefill_attention_bench(torch, K, make_workload(key), max(3, args.reps // 4))
+            print(json.dumps({"workload": key, **r}), flush=True)
+            torch.cuda.empty_cache()
+        return
+
     if args.only == "gemv_w8a16" and not args.profile_calls:
         for m in (1, 8, 16, 32):
             print(json.dumps(w8_bench(torch, K, m, args.reps)), flush=True)
@@ -506,6 +580,9 @@ def main():
         if args.only in (None, "gemv_w8a16"):
             for m in (1, 8, 16, 32):
                 w8_bench(torch, K, m, 0, eager_calls=args.profile_calls)
+        if args.only in (None, "paged_attention_prefill"):
+            for key in ("C3", "C4", "C5"):
+                prefill_attention_bench(torch, K, make_workload(key), 0, eager_calls=2)
         src = torch.empty(128 << 20, dtype=torch.float16, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(args.profile_calls):
@@ -578,6 +655,11 @@ def main():
             w8.append(w8_bench(torch, K, m, args.reps))
             torch.cuda.empty_cache()
 
+    prefill = {}
+    if not args.no_attention:
+        for key in ("C3", "C4", "C5"):
+            prefill[key] = prefill_attention_bench(torch, K, make_workload(key), max(3, args.reps // 4))
+            torch.cuda.empty_cache()
     attention = {}
     if not args.no_attention:
         for int8 in (False, True):
@@ -612,6 +694,7 @@ def main():
         "kernels": kern,
         "prefill": extra,
         "decode_attention": attention,
+        "prefill_attention": prefill,
         "gemv_w4a16_swiglu": gemv,
         "gemv_w8a16": w8,
         "copy_baseline_gb_per_s": copy,
