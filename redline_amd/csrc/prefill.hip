@@ -37,8 +37,13 @@ namespace {
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPfThreads = 256;  // 4 waves
-constexpr int kBQ = 64;          // query rows per workgroup (16 per wave)
+constexpr int kQS = 1;           // 16-row query sets per wave (each LDS fragment feeds kQS MFMAs)
+constexpr int kBQ = 4 * 16 * kQS;  // query rows per workgroup
 constexpr int kBK = 64;          // keys per tile
+// Four waves per SIMD (at most 128 VGPRs): the kernel is latency-bound, and
+// this beat the compiler's own register choice (~200 VGPRs, two waves per
+// SIMD) by 20-35% at C3-C5.
+constexpr int kPfWavesPerSimd = 4;
 constexpr int kKPad = 8;         // halves of padding per K row
 constexpr int kVPad = 8;         // halves of padding per V^T row
 
@@ -60,6 +65,15 @@ struct PfTile {
   float vs[kVPairs][2];
 };
 
+// Column of key k (0..63) in a V^T row: within each 32-key step, keys
+// 4 q + e and 16 + 4 q + e (q, e = 0..3) sit at 8 q + e and 8 q + 4 + e, the
+// order in which the P . V operands take them; a pair (k, k + 1) with k even
+// stays adjacent.
+__device__ __forceinline__ int vt_col(int k) {
+  const int r = k % 32;
+  return (k - r) + 8 * ((r % 16) / 4) + 4 * (r / 16) + r % 4;
+}
+
 template <bool kInt8>
 __device__ __forceinline__ f16x8 dequant8(typename std::conditional<kInt8, u32x2, u32x4>::type r,
                                           float s) {
@@ -80,18 +94,22 @@ __device__ __forceinline__ f16x8 dequant8(typename std::conditional<kInt8, u32x2
 }
 
 template <int D, bool kInt8>
-__global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads, kPfWavesPerSimd) void prefill_attention_kernel(PrefillArgs a) {
   using Tile = PfTile<D, kInt8>;
   constexpr int kSteps = D / 32, kDTiles = D / 16, kChunksPerRow = D / 8;
+  constexpr int kWaveRows = 16 * kQS;
   __shared__ __attribute__((aligned(16))) _Float16 k_lds[kBK][D + kKPad];
   __shared__ __attribute__((aligned(16))) _Float16 vt_lds[D][kBK + kVPad];
 
   const rlk_attention_params& p = a.p;
   const rlk_prefill_attention_work& w = a.w;
-  const int qt = blockIdx.x, h = blockIdx.y;
+  const int h = blockIdx.y;
   const int seq = w.seq_ids[blockIdx.z];
   const int q_len = w.q_len[seq];
-  if (qt * kBQ >= q_len) return;  // workgroup-uniform
+  // query tiles in reverse dispatch order: the last rows have the most keys,
+  // so the longest workgroups start first and the causal tail is short
+  const int qt = (q_len + kBQ - 1) / kBQ - 1 - static_cast<int>(blockIdx.x);
+  if (qt < 0) return;  // workgroup-uniform
   const int q0 = w.q_start[seq], ctx = w.ctx_len[seq];
   const int past = ctx - q_len;
   const int hkv = p.kv.num_kv_heads, bs = p.kv.block_size;
@@ -101,22 +119,26 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, qd = lane >> 4;
-  const int qi = qt * kBQ + wave * 16 + c16;  // this lane's query row (index among the new tokens)
-  const bool qvalid = qi < q_len;
-  const int qpos = past + qi;
+  const int row0 = qt * kBQ + wave * kWaveRows;  // first query row of this wave
   const int kv_end = past + min(q_len, (qt + 1) * kBQ);
-  const int wave_rows = min(q_len, qt * kBQ + wave * 16 + 16) - (qt * kBQ + wave * 16);
-  const int wave_kv_end = wave_rows > 0 ? past + qt * kBQ + wave * 16 + wave_rows : 0;
-
-  // q of this lane's row as B operands: lane (qd, c16) holds dims 32 ks + 8 qd .. + 8
-  f16x8 qb[kSteps];
+  const int wave_rows = min(q_len - row0, kWaveRows);
+  const int wave_kv_end = wave_rows > 0 ? past + row0 + wave_rows : 0;
+  // query set qs of this lane: row row0 + 16 qs + c16 (index among the new tokens)
+  int qi[kQS];
 #pragma unroll
-  for (int ks = 0; ks < kSteps; ++ks) {
-    qb[ks] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (qvalid)
-      qb[ks] = __builtin_bit_cast(
-          f16x8, load16(p.q + static_cast<size_t>(q0 + qi) * p.q_stride + h * D + 32 * ks + 8 * qd));
-  }
+  for (int qs = 0; qs < kQS; ++qs) qi[qs] = row0 + 16 * qs + c16;
+
+  // q of this lane's rows as B operands: lane (qd, c16) holds dims 32 ks + 8 qd .. + 8
+  f16x8 qb[kQS][kSteps];
+#pragma unroll
+  for (int qs = 0; qs < kQS; ++qs)
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      qb[qs][ks] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (qi[qs] < q_len)
+        qb[qs][ks] = __builtin_bit_cast(
+            f16x8, load16(p.q + static_cast<size_t>(q0 + qi[qs]) * p.q_stride + h * D + 32 * ks + 8 * qd));
+    }
 
   const float* kscale32 = p.kv.k_scale;
   const float* vscale32 = p.kv.v_scale;
@@ -182,71 +204,99 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
       const f16x8 v0 = dequant8<kInt8>(st.v[u][0], st.vs[u][0]);
       const f16x8 v1 = dequant8<kInt8>(st.v[u][1], st.vs[u][1]);
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {  // V^T[dim][key pair]
+      for (int d = 0; d < 8; ++d) {  // V^T[dim][key pair], keys permuted within 32
         const f16x2 pr = {v0[d], v1[d]};
-        *reinterpret_cast<f16x2*>(&vt_lds[ch * 8 + d][2 * kp]) = pr;
+        *reinterpret_cast<f16x2*>(&vt_lds[ch * 8 + d][vt_col(2 * kp)]) = pr;
       }
     }
   };
 
-  f32x4 o[kDTiles];
+  // Online softmax state per query set, in raw-score units; the scale is
+  // folded into the exponent: e^((s - m) scale) = 2^(s c - m c), c = scale log2(e).
+  const float c = p.scale * 1.44269504088896340736f;
+  f32x4 o[kQS][kDTiles];
+  float m_run[kQS], l_run[kQS];
 #pragma unroll
-  for (int dt = 0; dt < kDTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -FLT_MAX, l_run = 0.f;
+  for (int qs = 0; qs < kQS; ++qs) {
+    m_run[qs] = -FLT_MAX;
+    l_run[qs] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) o[qs][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto compute = [&](int k0) {
-    // S^T for 4 subtiles of 16 keys: lane (qd, c16) gets keys k0 + 16 t + 4 qd + e of row c16
-    f32x4 s[4];
+    // S^T for 4 subtiles of 16 keys: lane (qd, c16) gets keys k0 + 16 t + 4 qd + e of its
+    // rows; each K fragment read from LDS feeds every query set
+    f32x4 s[kQS][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < kSteps; ++ks)
-        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            *reinterpret_cast<const f16x8*>(&k_lds[16 * t + c16][32 * ks + 8 * qd]), qb[ks], s[t], 0,
-            0, 0);
+      for (int qs = 0; qs < kQS; ++qs) s[qs][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks) {
+        const f16x8 ka = *reinterpret_cast<const f16x8*>(&k_lds[16 * t + c16][32 * ks + 8 * qd]);
+#pragma unroll
+        for (int qs = 0; qs < kQS; ++qs)
+          s[qs][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[qs][ks], s[qs][t], 0, 0, 0);
+      }
     }
-    float mt = -FLT_MAX;
+    // masks only where the tile reaches past a row's position (the diagonal,
+    // the context end) or the wave has rows past q_len
+    const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < kWaveRows;
+    bool grew = false;
+    f16x8 pb[kQS][2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int qs = 0; qs < kQS; ++qs) {
+      float mt = -FLT_MAX;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kp = k0 + 16 * t + 4 * qd + e;
-        s[t][e] = (qvalid && kp <= qpos) ? s[t][e] * p.scale : -FLT_MAX;
-        mt = fmaxf(mt, s[t][e]);
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (masked) {
+            const int kp = k0 + 16 * t + 4 * qd + e;
+            if (!(qi[qs] < q_len && kp <= past + qi[qs])) s[qs][t][e] = -FLT_MAX;
+          }
+          mt = fmaxf(mt, s[qs][t][e]);
+        }
+      mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
+      const float m_new = fmaxf(m_run[qs], mt);
+      const float alpha = m_run[qs] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f((m_run[qs] - m_new) * c);
+      grew |= m_new > m_run[qs];
+      const float mc = m_new * c;
+      float ts = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
+          ts += s[qs][t][e];
+        }
+      ts = rows_sum<true>(rows_sum<false>(ts));
+      l_run[qs] = l_run[qs] * alpha + ts;
+      m_run[qs] = m_new;
+      if (__any(grew)) {  // rescale only when some row's max moved
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) o[qs][dt] *= alpha;
       }
-    mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = m_run == -FLT_MAX ? 0.f : __expf(m_run - m_new);
-    float ts = 0.f;
+      grew = false;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[t][e] = s[t][e] == -FLT_MAX ? 0.f : __expf(s[t][e] - m_new);
-        ts += s[t][e];
-      }
-    ts = rows_sum<true>(rows_sum<false>(ts));
-    l_run = l_run * alpha + ts;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) o[dt] *= alpha;
+      for (int j = 0; j < 2; ++j)
+        pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
+                          static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
+                          static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
+                          static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
+    }
     // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
     // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const f16x8 pb = {static_cast<_Float16>(s[2 * j][0]), static_cast<_Float16>(s[2 * j][1]),
-                        static_cast<_Float16>(s[2 * j][2]), static_cast<_Float16>(s[2 * j][3]),
-                        static_cast<_Float16>(s[2 * j + 1][0]), static_cast<_Float16>(s[2 * j + 1][1]),
-                        static_cast<_Float16>(s[2 * j + 1][2]), static_cast<_Float16>(s[2 * j + 1][3])};
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int dt = 0; dt < kDTiles; ++dt) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(&vt_lds[16 * dt + c16][32 * j + 4 * qd]);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(&vt_lds[16 * dt + c16][32 * j + 16 + 4 * qd]);
-        const f16x8 va = __builtin_bit_cast(f16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[dt], 0, 0, 0);
+        const f16x8 va = *reinterpret_cast<const f16x8*>(&vt_lds[16 * dt + c16][32 * j + 8 * qd]);
+#pragma unroll
+        for (int qs = 0; qs < kQS; ++qs)
+          o[qs][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qs][j], o[qs][dt], 0, 0, 0);
       }
-    }
   };
 
   const int ntiles = (kv_end + kBK - 1) / kBK;
@@ -259,14 +309,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
     if (t * kBK < wave_kv_end) compute(t * kBK);
   }
 
-  if (qvalid) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    uint16_t* out = p.out + static_cast<size_t>(q0 + qi) * p.num_heads * D + h * D + 4 * qd;
+#pragma unroll
+  for (int qs = 0; qs < kQS; ++qs) {
+    if (qi[qs] >= q_len) continue;
+    const float inv = l_run[qs] > 0.f ? 1.f / l_run[qs] : 0.f;
+    uint16_t* out = p.out + static_cast<size_t>(q0 + qi[qs]) * p.num_heads * D + h * D + 4 * qd;
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
-      // lane (qd, c16) holds dims 16 dt + 4 qd + e of row c16
-      const f16x4 r = {static_cast<_Float16>(o[dt][0] * inv), static_cast<_Float16>(o[dt][1] * inv),
-                       static_cast<_Float16>(o[dt][2] * inv), static_cast<_Float16>(o[dt][3] * inv)};
+      // lane (qd, c16) holds dims 16 dt + 4 qd + e of its row
+      const f16x4 r = {static_cast<_Float16>(o[qs][dt][0] * inv), static_cast<_Float16>(o[qs][dt][1] * inv),
+                       static_cast<_Float16>(o[qs][dt][2] * inv), static_cast<_Float16>(o[qs][dt][3] * inv)};
       *reinterpret_cast<f16x4*>(out + 16 * dt) = r;
     }
   }
