@@ -8,8 +8,9 @@
 // past + i = ctx_len - q_len + i and attends to positions [0, past + i].
 //
 // The mapping is wave64 and matrix-core first:
-//   * a workgroup of 4 waves takes (sequence, 64 query rows, head); a wave owns
-//     16 query rows and keeps their q in registers as MFMA B operands;
+//   * a workgroup of 4 waves takes (sequence, 64 or 128 query rows, head); a
+//     wave owns 16 or 32 query rows and keeps their q in registers as MFMA B
+//     operands;
 //   * K and V tiles of 64 keys are staged once per workgroup in LDS (K
 //     row-major, V transposed), with the next tile's loads in flight while the
 //     current one is computed; INT8 codes are dequantised on the way, to
@@ -37,13 +38,21 @@ namespace {
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPfThreads = 256;  // 4 waves
-constexpr int kQS = 1;           // 16-row query sets per wave (each LDS fragment feeds kQS MFMAs)
-constexpr int kBQ = 4 * 16 * kQS;  // query rows per workgroup
 constexpr int kBK = 64;          // keys per tile
-// Four waves per SIMD (at most 128 VGPRs): the kernel is latency-bound, and
-// this beat the compiler's own register choice (~200 VGPRs, two waves per
-// SIMD) by 20-35% at C3-C5.
-constexpr int kPfWavesPerSimd = 4;
+// Query rows per wave and waves per SIMD, per cache dtype (measured at the
+// C3-C5 shapes).  The kernel is latency- and LDS-bound: every wave reads the
+// whole K and V tile from LDS, so more query rows per wave (QS 16-row sets,
+// each LDS fragment feeding QS MFMAs) save LDS bandwidth but cost registers
+// and with them waves per SIMD.  FP16: QS = 2 at two waves per SIMD beat
+// QS = 1 at four by 6-8%; INT8 (dequantised during staging, which wants the
+// more waves) the other way round by 14%.  Left to itself, the compiler took
+// ~200 VGPRs at QS = 1 (two waves per SIMD), 20-35% slower than four.
+template <bool kInt8>
+struct PfShape {
+  static constexpr int kQS = kInt8 ? 1 : 2;
+  static constexpr int kWavesPerSimd = kInt8 ? 4 : 2;
+  static constexpr int kBQ = 4 * 16 * kQS;  // query rows per workgroup
+};
 constexpr int kKPad = 8;         // halves of padding per K row
 constexpr int kVPad = 8;         // halves of padding per V^T row
 
@@ -94,8 +103,10 @@ __device__ __forceinline__ f16x8 dequant8(typename std::conditional<kInt8, u32x2
 }
 
 template <int D, bool kInt8>
-__global__ __launch_bounds__(kPfThreads, kPfWavesPerSimd) void prefill_attention_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void prefill_attention_kernel(
+    PrefillArgs a) {
   using Tile = PfTile<D, kInt8>;
+  constexpr int kQS = PfShape<kInt8>::kQS, kBQ = PfShape<kInt8>::kBQ;
   constexpr int kSteps = D / 32, kDTiles = D / 16, kChunksPerRow = D / 8;
   constexpr int kWaveRows = 16 * kQS;
   __shared__ __attribute__((aligned(16))) _Float16 k_lds[kBK][D + kKPad];
@@ -345,8 +356,9 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
   if (reinterpret_cast<uintptr_t>(p.q) % 16 != 0 || p.q_stride % 8 != 0)
     return fail(RLK_EINVAL, "%s: q rows must be 16-byte aligned (q_stride %d)", what, p.q_stride);
   PrefillArgs a{p, w, scale16};
-  // the work's tiles are the reference's 32-row tiles (kPrefillTileQ); ours hold 64 rows
-  const dim3 grid((w.max_q_tiles * RLK_PREFILL_TILE_Q + kBQ - 1) / kBQ, p.num_heads, w.num_seqs);
+  // the work's tiles are the reference's 32-row tiles (kPrefillTileQ); ours hold kBQ rows
+  const int rows = w.max_q_tiles * RLK_PREFILL_TILE_Q, bq = PfShape<false>::kBQ, bq8 = PfShape<true>::kBQ;
+  const dim3 grid((rows + (int8 ? bq8 : bq) - 1) / (int8 ? bq8 : bq), p.num_heads, w.num_seqs);
   if (p.kv.head_dim == 64) {
     if (int8) prefill_attention_kernel<64, true><<<grid, kPfThreads, 0, stream>>>(a);
     else prefill_attention_kernel<64, false><<<grid, kPfThreads, 0, stream>>>(a);
