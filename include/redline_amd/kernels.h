@@ -91,6 +91,24 @@ static_assert(offsetof(AttentionParams, positions) == offsetof(rlk_attention_par
 static_assert(sizeof(DecodeAttentionWork) == sizeof(rlk_decode_attention_work),
               "DecodeAttentionWork layout");
 
+// Prefill attention: tiled causal attention for sequences processing several
+// new tokens, attending to cached + new keys (kernels.h:118-132 of the reference).
+struct PrefillAttentionWork {
+  const int32_t* seq_ids = nullptr;  // [num_seqs] indices into the arrays below
+  const int32_t* q_start = nullptr;  // [*] first token row of each sequence
+  const int32_t* q_len = nullptr;    // [*] number of new tokens
+  const int32_t* ctx_len = nullptr;  // [*] total context after this step
+  int num_seqs = 0;
+  int max_q_tiles = 0;
+};
+constexpr int kPrefillTileQ = RLK_PREFILL_TILE_Q;
+
+static_assert(sizeof(PrefillAttentionWork) == sizeof(rlk_prefill_attention_work),
+              "PrefillAttentionWork layout");
+static_assert(offsetof(PrefillAttentionWork, max_q_tiles) ==
+                  offsetof(rlk_prefill_attention_work, max_q_tiles),
+              "PrefillAttentionWork layout");
+
 namespace detail {
 
 inline void check(int status) {
@@ -155,6 +173,14 @@ inline void paged_attention_decode(const AttentionParams& p, const DecodeAttenti
   detail::check(rlk_paged_attention_decode(reinterpret_cast<const rlk_attention_params*>(&p),
                                            reinterpret_cast<const rlk_decode_attention_work*>(&w),
                                            stream));
+}
+
+// Paged prefill attention (causal, tiled on the matrix cores).
+inline void paged_attention_prefill(const AttentionParams& p, const PrefillAttentionWork& w,
+                                    hipStream_t stream) {
+  detail::check(rlk_paged_attention_prefill(reinterpret_cast<const rlk_attention_params*>(&p),
+                                            reinterpret_cast<const rlk_prefill_attention_work*>(&w),
+                                            stream));
 }
 
 // INT8 weight-only GEMV (kernels.h:157-163 of the reference): y = (x . W^T) *

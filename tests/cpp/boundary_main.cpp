@@ -46,6 +46,25 @@ int main() {
   expect_throw("gemv_w4 swiglu n", [&] { kernels::gemv_w4a16_swiglu(hx, 2, dummy, hx, hx, 128, 7, 256, hy, nullptr); },
                "even");
   kernels::gemv_w4a16_swiglu(hx, 0, dummy, hx, hx, 128, 8, 256, hy, nullptr);
+  const int8_t* w8 = reinterpret_cast<const int8_t*>(dummy);
+  expect_throw("gemv_w8 k", [&] { kernels::gemv_w8a16(hx, 1, w8, hx, nullptr, 8, 200, hy, false, nullptr); },
+               "K % 16");
+  expect_throw("gemv_w8 m", [&] { kernels::gemv_w8a16(hx, kernels::kGemvW8MaxM + 1, w8, hx, nullptr, 8, 256, hy, true, nullptr); },
+               "unsupported m");
+  kernels::gemv_w8a16(hx, 0, w8, hx, nullptr, 8, 256, hy, false, nullptr);
+  kernels::AttentionParams ap;
+  ap.num_heads = 4;
+  ap.kv.num_kv_heads = 2;
+  ap.kv.head_dim = 96;
+  ap.kv.block_size = 16;
+  kernels::PrefillAttentionWork pw;
+  kernels::paged_attention_prefill(ap, pw, nullptr);  // no sequences: no-op
+  pw.num_seqs = 1;
+  pw.max_q_tiles = 1;
+  expect_throw("prefill head_dim", [&] { kernels::paged_attention_prefill(ap, pw, nullptr); },
+               "unsupported head_dim 96");
+  ap.kv.head_dim = 64;
+  expect_throw("prefill null", [&] { kernels::paged_attention_prefill(ap, pw, nullptr); }, "null pointer");
   // n <= 0 is a silent no-op, as in the reference.
   kernels::embedding_lookup(nullptr, nullptr, 0, 12, nullptr, nullptr);
   kernels::rope_and_write_kv(nullptr, nullptr, nullptr, 0, 4, nullptr, nullptr, kv, nullptr);
