@@ -53,7 +53,9 @@ struct PfShape {
   static constexpr int kWavesPerSimd = kInt8 ? 4 : 2;
   static constexpr int kBQ = 4 * 16 * kQS;  // query rows per workgroup
 };
-constexpr int kKPad = 8;         // halves of padding per K row
+// K row padding: 16 halves measured half the bank conflicts of 8 (rocprofv3
+// SQ_LDS_BANK_CONFLICT); the V^T padding made no difference.
+constexpr int kKPad = 16;        // halves of padding per K row
 constexpr int kVPad = 8;         // halves of padding per V^T row
 
 struct PrefillArgs {
@@ -81,6 +83,39 @@ struct PfTile {
 __device__ __forceinline__ int vt_col(int k) {
   const int r = k % 32;
   return (k - r) + 8 * ((r % 16) / 4) + 4 * (r / 16) + r % 4;
+}
+
+// Physical column of V^T[row][col]: the 16-byte chunks of a row are XOR-ed
+// with (row / 8) % 8.  A staging write puts each lane's key pair (one dword)
+// into the row of one of its 8 dims, rows 8 apart across the 8-dim chunks of V:
+// unswizzled, every lane of an instruction fell in one bank (rocprofv3: 76% of
+// the LDS-active cycles were bank conflicts).  With the XOR, and the lanes of
+// each 32-lane half covering 8 dim chunks x 4 key pairs whose columns are the
+// 4 dwords of one chunk (vt_item), the 32 lanes hit 32 banks.  The P . V
+// operand reads take 8 consecutive rows at one chunk per 128 bytes and stay
+// conflict-free and 16-byte contiguous.
+__device__ __forceinline__ int vt_phys(int row, int col) {
+  return (((col >> 3) ^ ((row >> 3) & 7)) << 3) | (col & 7);
+}
+
+// Key pair kp (keys 2 kp, 2 kp + 1) and 8-dim chunk ch that thread tid stages
+// in V round u: lane bits 0-2 (and bit 5 when D = 128) pick the chunk, bits
+// 3-4 the offset {0, 1, 8, 9} within a group of key pairs (the 4 dwords of one
+// V^T chunk), the rest the group; the 16 lanes of one key pair read its
+// 256-byte (D = 128) row contiguously.
+template <int D>
+__device__ __forceinline__ void vt_item(int tid, int u, int& kp, int& ch) {
+  const int l = tid & 63, wv = tid >> 6;
+  int bi;
+  if constexpr (D == 128) {
+    ch = ((l >> 5) << 3) | (l & 7);
+    bi = (wv << 1) | u;
+  } else {
+    ch = l & 7;
+    bi = ((l >> 5) << 2) | wv;
+  }
+  constexpr int kOff[4] = {0, 1, 8, 9};
+  kp = 2 * (bi & 3) + 16 * (bi >> 2) + kOff[(l >> 3) & 3];
 }
 
 template <bool kInt8>
@@ -189,7 +224,8 @@ __global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void pre
     }
 #pragma unroll
     for (int u = 0; u < Tile::kVPairs; ++u) {
-      const int i = tid + kPfThreads * u, kp = i / kChunksPerRow, ch = i % kChunksPerRow;
+      int kp, ch;
+      vt_item<D>(tid, u, kp, ch);
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         const int pos = k0 + 2 * kp + x;
@@ -211,13 +247,14 @@ __global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void pre
     }
 #pragma unroll
     for (int u = 0; u < Tile::kVPairs; ++u) {
-      const int i = tid + kPfThreads * u, kp = i / kChunksPerRow, ch = i % kChunksPerRow;
+      int kp, ch;
+      vt_item<D>(tid, u, kp, ch);
       const f16x8 v0 = dequant8<kInt8>(st.v[u][0], st.vs[u][0]);
       const f16x8 v1 = dequant8<kInt8>(st.v[u][1], st.vs[u][1]);
 #pragma unroll
       for (int d = 0; d < 8; ++d) {  // V^T[dim][key pair], keys permuted within 32
         const f16x2 pr = {v0[d], v1[d]};
-        *reinterpret_cast<f16x2*>(&vt_lds[ch * 8 + d][vt_col(2 * kp)]) = pr;
+        *reinterpret_cast<f16x2*>(&vt_lds[ch * 8 + d][vt_phys(ch * 8 + d, vt_col(2 * kp))]) = pr;
       }
     }
   };
@@ -303,7 +340,8 @@ __global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void pre
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int dt = 0; dt < kDTiles; ++dt) {
-        const f16x8 va = *reinterpret_cast<const f16x8*>(&vt_lds[16 * dt + c16][32 * j + 8 * qd]);
+        const f16x8 va =
+            *reinterpret_cast<const f16x8*>(&vt_lds[16 * dt + c16][vt_phys(16 * dt + c16, 32 * j + 8 * qd)]);
 #pragma unroll
         for (int qs = 0; qs < kQS; ++qs)
           o[qs][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qs][j], o[qs][dt], 0, 0, 0);
