@@ -37,21 +37,24 @@ namespace {
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPfThreads = 256;  // 4 waves
 constexpr int kBK = 64;          // keys per tile
-// Query rows per wave and waves per SIMD, per cache dtype (measured at the
-// C3-C5 shapes).  The kernel is latency- and LDS-bound: every wave reads the
-// whole K and V tile from LDS, so more query rows per wave (QS 16-row sets,
-// each LDS fragment feeding QS MFMAs) save LDS bandwidth but cost registers
-// and with them waves per SIMD.  FP16: QS = 2 at two waves per SIMD beat
-// QS = 1 at four by 6-8%; INT8 (dequantised during staging, which wants the
-// more waves) the other way round by 14%.  Left to itself, the compiler took
-// ~200 VGPRs at QS = 1 (two waves per SIMD), 20-35% slower than four.
-template <bool kInt8>
+// Workgroup shape per head dim and cache dtype (measured at the C3-C5 shapes).
+// The kernel waits on its K/V tile loads, which are in flight only while the
+// previous tile is computed: more query rows per loaded tile (more waves per
+// workgroup, QS 16-row query sets per wave) and more waves per SIMD both hide
+// more of that.  8 waves per workgroup (256 query rows FP16, 128 INT8) beat 4
+// by 20% (FP16, C5) and 16% (INT8, C4).  FP16: QS = 2 at two waves per SIMD
+// beat QS = 1 at four by 6-8%; INT8 (dequantised during staging, which wants
+// the more waves) the other way round.  Left to itself, the compiler took
+// ~200 VGPRs at QS = 1 (two waves per SIMD), 20-35% slower than four.  D = 64
+// keeps 4 waves: its V tile has only 256 staging items.
+template <int D, bool kInt8>
 struct PfShape {
   static constexpr int kQS = kInt8 ? 1 : 2;
   static constexpr int kWavesPerSimd = kInt8 ? 4 : 2;
-  static constexpr int kBQ = 4 * 16 * kQS;  // query rows per workgroup
+  static constexpr int kWaves = D == 128 ? 8 : 4;  // waves per workgroup
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBQ = kWaves * 16 * kQS;  // query rows per workgroup
 };
 // K row padding: 16 halves measured half the bank conflicts of 8 (rocprofv3
 // SQ_LDS_BANK_CONFLICT); the V^T padding made no difference.
@@ -67,7 +70,7 @@ struct PrefillArgs {
 template <int D, bool kInt8>
 struct PfTile {
   // per thread: K chunks (8 dims of one key) and V chunk pairs (8 dims of two keys)
-  static constexpr int kKChunks = kBK * D / 8 / kPfThreads;
+  static constexpr int kKChunks = kBK * D / 8 / PfShape<D, kInt8>::kThreads;
   static constexpr int kVPairs = kKChunks / 2;
   using Raw = typename std::conditional<kInt8, u32x2, u32x4>::type;
   Raw k[kKChunks];
@@ -103,11 +106,15 @@ __device__ __forceinline__ int vt_phys(int row, int col) {
 // 3-4 the offset {0, 1, 8, 9} within a group of key pairs (the 4 dwords of one
 // V^T chunk), the rest the group; the 16 lanes of one key pair read its
 // 256-byte (D = 128) row contiguously.
-template <int D>
+template <int D, int kThreads>
 __device__ __forceinline__ void vt_item(int tid, int u, int& kp, int& ch) {
   const int l = tid & 63, wv = tid >> 6;
   int bi;
-  if constexpr (D == 128) {
+  if constexpr (D == 128 && kThreads == 512) {
+    ch = ((l >> 5) << 3) | (l & 7);
+    bi = wv;
+    (void)u;
+  } else if constexpr (D == 128) {
     ch = ((l >> 5) << 3) | (l & 7);
     bi = (wv << 1) | u;
   } else {
@@ -138,10 +145,11 @@ __device__ __forceinline__ f16x8 dequant8(typename std::conditional<kInt8, u32x2
 }
 
 template <int D, bool kInt8>
-__global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void prefill_attention_kernel(
-    PrefillArgs a) {
+__global__ __launch_bounds__((PfShape<D, kInt8>::kThreads), (PfShape<D, kInt8>::kWavesPerSimd)) void
+prefill_attention_kernel(PrefillArgs a) {
   using Tile = PfTile<D, kInt8>;
-  constexpr int kQS = PfShape<kInt8>::kQS, kBQ = PfShape<kInt8>::kBQ;
+  constexpr int kQS = PfShape<D, kInt8>::kQS, kBQ = PfShape<D, kInt8>::kBQ;
+  constexpr int kPfThreads = PfShape<D, kInt8>::kThreads;
   constexpr int kSteps = D / 32, kDTiles = D / 16, kChunksPerRow = D / 8;
   constexpr int kWaveRows = 16 * kQS;
   __shared__ __attribute__((aligned(16))) _Float16 k_lds[kBK][D + kKPad];
@@ -225,7 +233,7 @@ __global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void pre
 #pragma unroll
     for (int u = 0; u < Tile::kVPairs; ++u) {
       int kp, ch;
-      vt_item<D>(tid, u, kp, ch);
+      vt_item<D, kPfThreads>(tid, u, kp, ch);
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         const int pos = k0 + 2 * kp + x;
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(kPfThreads, PfShape<kInt8>::kWavesPerSimd) void pre
 #pragma unroll
     for (int u = 0; u < Tile::kVPairs; ++u) {
       int kp, ch;
-      vt_item<D>(tid, u, kp, ch);
+      vt_item<D, kPfThreads>(tid, u, kp, ch);
       const f16x8 v0 = dequant8<kInt8>(st.v[u][0], st.vs[u][0]);
       const f16x8 v1 = dequant8<kInt8>(st.v[u][1], st.vs[u][1]);
 #pragma unroll
@@ -395,14 +403,18 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
     return fail(RLK_EINVAL, "%s: q rows must be 16-byte aligned (q_stride %d)", what, p.q_stride);
   PrefillArgs a{p, w, scale16};
   // the work's tiles are the reference's 32-row tiles (kPrefillTileQ); ours hold kBQ rows
-  const int rows = w.max_q_tiles * RLK_PREFILL_TILE_Q, bq = PfShape<false>::kBQ, bq8 = PfShape<true>::kBQ;
-  const dim3 grid((rows + (int8 ? bq8 : bq) - 1) / (int8 ? bq8 : bq), p.num_heads, w.num_seqs);
+  const int rows = w.max_q_tiles * RLK_PREFILL_TILE_Q;
+  auto go = [&](auto kernel, auto shape) {
+    using S = decltype(shape);
+    const dim3 grid((rows + S::kBQ - 1) / S::kBQ, p.num_heads, w.num_seqs);
+    kernel<<<grid, S::kThreads, 0, stream>>>(a);
+  };
   if (p.kv.head_dim == 64) {
-    if (int8) prefill_attention_kernel<64, true><<<grid, kPfThreads, 0, stream>>>(a);
-    else prefill_attention_kernel<64, false><<<grid, kPfThreads, 0, stream>>>(a);
+    if (int8) go(prefill_attention_kernel<64, true>, PfShape<64, true>{});
+    else go(prefill_attention_kernel<64, false>, PfShape<64, false>{});
   } else {
-    if (int8) prefill_attention_kernel<128, true><<<grid, kPfThreads, 0, stream>>>(a);
-    else prefill_attention_kernel<128, false><<<grid, kPfThreads, 0, stream>>>(a);
+    if (int8) go(prefill_attention_kernel<128, true>, PfShape<128, true>{});
+    else go(prefill_attention_kernel<128, false>, PfShape<128, false>{});
   }
   return launch_status(what);
 }
