@@ -144,13 +144,138 @@ __device__ __forceinline__ f16x8 dequant8(typename std::conditional<kInt8, u32x2
   }
 }
 
+// Online-softmax state of a wave's query rows (QS sets of 16), in raw-score
+// units; the scale is folded into the exponent: e^((s - m) scale) = 2^(s c - m c),
+// c = scale log2(e).  Lane (qd, c16) holds output dims 16 dt + 4 qd + e of row
+// c16 of each set.
+template <int D, int QS>
+struct PfState {
+  f32x4 o[QS][D / 16];
+  float m_run[QS], l_run[QS];
+  float c;
+  __device__ explicit PfState(float scale) : c(scale * 1.44269504088896340736f) {
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+      m_run[qs] = -FLT_MAX;
+      l_run[qs] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) o[qs][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __device__ void store(const rlk_attention_params& p, int q0, const int (&qi)[QS], int q_len, int h,
+                        int qd) const {
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+      if (qi[qs] >= q_len) continue;
+      const float inv = l_run[qs] > 0.f ? 1.f / l_run[qs] : 0.f;
+      uint16_t* out = p.out + static_cast<size_t>(q0 + qi[qs]) * p.num_heads * D + h * D + 4 * qd;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const f16x4 r = {static_cast<_Float16>(o[qs][dt][0] * inv), static_cast<_Float16>(o[qs][dt][1] * inv),
+                         static_cast<_Float16>(o[qs][dt][2] * inv), static_cast<_Float16>(o[qs][dt][3] * inv)};
+        *reinterpret_cast<f16x4*>(out + 16 * dt) = r;
+      }
+    }
+  }
+};
+
+// One 64-key tile for a wave's query rows.  kfrag(t, ks): the A operand of
+// S^T subtile t (keys 16 t .. + 15 of the tile), step ks (dims 32 ks .. + 31):
+// lane (qd, c16) gets key 16 t + c16, dims 32 ks + 8 qd .. + 7.  vfrag(j, dt):
+// the A operand of O^T step j, dim tile dt: lane (qd, c16) gets dim 16 dt +
+// c16 of keys 32 j + 4 qd + e and then 32 j + 16 + 4 qd + e (e = 0..3).
+// vready(va) runs after the fragments of a step are requested and before the
+// MFMAs use them (a wait for reads the compiler does not track).
+template <int D, int QS, class KFrag, class VFrag, class VReady>
+__device__ __forceinline__ void attend_tile(PfState<D, QS>& st, int k0, const f16x8 (&qb)[QS][D / 32],
+                                            const int (&qi)[QS], int q_len, int past, int row0,
+                                            int wave_rows, int qd, KFrag kfrag, VFrag vfrag,
+                                            VReady vready) {
+  constexpr int kSteps = D / 32, kDTiles = D / 16;
+  // S^T for 4 subtiles of 16 keys: lane (qd, c16) gets keys k0 + 16 t + 4 qd + e of its
+  // rows; each K fragment read from LDS feeds every query set
+  f32x4 s[QS][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) s[qs][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      const f16x8 ka = kfrag(t, ks);
+#pragma unroll
+      for (int qs = 0; qs < QS; ++qs)
+        s[qs][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[qs][ks], s[qs][t], 0, 0, 0);
+    }
+  }
+  // masks only where the tile reaches past a row's position (the diagonal,
+  // the context end) or the wave has rows past q_len
+  const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < 16 * QS;
+  const float c = st.c;
+  f16x8 pb[QS][2];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    float mt = -FLT_MAX;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (masked) {
+          const int kp = k0 + 16 * t + 4 * qd + e;
+          if (!(qi[qs] < q_len && kp <= past + qi[qs])) s[qs][t][e] = -FLT_MAX;
+        }
+        mt = fmaxf(mt, s[qs][t][e]);
+      }
+    mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
+    const float m_new = fmaxf(st.m_run[qs], mt);
+    const float alpha =
+        st.m_run[qs] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
+    const bool grew = m_new > st.m_run[qs];
+    const float mc = m_new * c;
+    float ts = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
+        ts += s[qs][t][e];
+      }
+    ts = rows_sum<true>(rows_sum<false>(ts));
+    st.l_run[qs] = st.l_run[qs] * alpha + ts;
+    st.m_run[qs] = m_new;
+    if (__any(grew)) {  // rescale only when some row's max moved
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) st.o[qs][dt] *= alpha;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
+                        static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
+                        static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
+                        static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
+  }
+  // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
+  // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    f16x8 va[kDTiles];
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) va[dt] = vfrag(j, dt);
+    vready(va);
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt)
+#pragma unroll
+      for (int qs = 0; qs < QS; ++qs)
+        st.o[qs][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], pb[qs][j], st.o[qs][dt], 0, 0, 0);
+  }
+}
+
 template <int D, bool kInt8>
 __global__ __launch_bounds__((PfShape<D, kInt8>::kThreads), (PfShape<D, kInt8>::kWavesPerSimd)) void
 prefill_attention_kernel(PrefillArgs a) {
   using Tile = PfTile<D, kInt8>;
   constexpr int kQS = PfShape<D, kInt8>::kQS, kBQ = PfShape<D, kInt8>::kBQ;
   constexpr int kPfThreads = PfShape<D, kInt8>::kThreads;
-  constexpr int kSteps = D / 32, kDTiles = D / 16, kChunksPerRow = D / 8;
+  constexpr int kSteps = D / 32, kChunksPerRow = D / 8;
   constexpr int kWaveRows = 16 * kQS;
   __shared__ __attribute__((aligned(16))) _Float16 k_lds[kBK][D + kKPad];
   __shared__ __attribute__((aligned(16))) _Float16 vt_lds[D][kBK + kVPad];
@@ -267,93 +392,18 @@ prefill_attention_kernel(PrefillArgs a) {
     }
   };
 
-  // Online softmax state per query set, in raw-score units; the scale is
-  // folded into the exponent: e^((s - m) scale) = 2^(s c - m c), c = scale log2(e).
-  const float c = p.scale * 1.44269504088896340736f;
-  f32x4 o[kQS][kDTiles];
-  float m_run[kQS], l_run[kQS];
-#pragma unroll
-  for (int qs = 0; qs < kQS; ++qs) {
-    m_run[qs] = -FLT_MAX;
-    l_run[qs] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) o[qs][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
+  PfState<D, kQS> stt(p.scale);
   auto compute = [&](int k0) {
-    // S^T for 4 subtiles of 16 keys: lane (qd, c16) gets keys k0 + 16 t + 4 qd + e of its
-    // rows; each K fragment read from LDS feeds every query set
-    f32x4 s[kQS][4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int qs = 0; qs < kQS; ++qs) s[qs][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kSteps; ++ks) {
-        const f16x8 ka = *reinterpret_cast<const f16x8*>(&k_lds[16 * t + c16][32 * ks + 8 * qd]);
-#pragma unroll
-        for (int qs = 0; qs < kQS; ++qs)
-          s[qs][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[qs][ks], s[qs][t], 0, 0, 0);
-      }
-    }
-    // masks only where the tile reaches past a row's position (the diagonal,
-    // the context end) or the wave has rows past q_len
-    const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < kWaveRows;
-    bool grew = false;
-    f16x8 pb[kQS][2];
-#pragma unroll
-    for (int qs = 0; qs < kQS; ++qs) {
-      float mt = -FLT_MAX;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (masked) {
-            const int kp = k0 + 16 * t + 4 * qd + e;
-            if (!(qi[qs] < q_len && kp <= past + qi[qs])) s[qs][t][e] = -FLT_MAX;
-          }
-          mt = fmaxf(mt, s[qs][t][e]);
-        }
-      mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
-      const float m_new = fmaxf(m_run[qs], mt);
-      const float alpha = m_run[qs] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f((m_run[qs] - m_new) * c);
-      grew |= m_new > m_run[qs];
-      const float mc = m_new * c;
-      float ts = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
-          ts += s[qs][t][e];
-        }
-      ts = rows_sum<true>(rows_sum<false>(ts));
-      l_run[qs] = l_run[qs] * alpha + ts;
-      m_run[qs] = m_new;
-      if (__any(grew)) {  // rescale only when some row's max moved
-#pragma unroll
-        for (int dt = 0; dt < kDTiles; ++dt) o[qs][dt] *= alpha;
-      }
-      grew = false;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
-                          static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
-                          static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
-                          static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
-    }
-    // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
-    // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) {
-        const f16x8 va =
-            *reinterpret_cast<const f16x8*>(&vt_lds[16 * dt + c16][vt_phys(16 * dt + c16, 32 * j + 8 * qd)]);
-#pragma unroll
-        for (int qs = 0; qs < kQS; ++qs)
-          o[qs][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qs][j], o[qs][dt], 0, 0, 0);
-      }
+    attend_tile<D, kQS>(
+        stt, k0, qb, qi, q_len, past, row0, wave_rows, qd,
+        [&](int t, int ks) {
+          return *reinterpret_cast<const f16x8*>(&k_lds[16 * t + c16][32 * ks + 8 * qd]);
+        },
+        [&](int j, int dt) {
+          return *reinterpret_cast<const f16x8*>(
+              &vt_lds[16 * dt + c16][vt_phys(16 * dt + c16, 32 * j + 8 * qd)]);
+        },
+        [](f16x8(&)[D / 16]) {});
   };
 
   const int ntiles = (kv_end + kBK - 1) / kBK;
@@ -366,19 +416,172 @@ prefill_attention_kernel(PrefillArgs a) {
     if (t * kBK < wave_kv_end) compute(t * kBK);
   }
 
-#pragma unroll
-  for (int qs = 0; qs < kQS; ++qs) {
-    if (qi[qs] >= q_len) continue;
-    const float inv = l_run[qs] > 0.f ? 1.f / l_run[qs] : 0.f;
-    uint16_t* out = p.out + static_cast<size_t>(q0 + qi[qs]) * p.num_heads * D + h * D + 4 * qd;
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      // lane (qd, c16) holds dims 16 dt + 4 qd + e of its row
-      const f16x4 r = {static_cast<_Float16>(o[qs][dt][0] * inv), static_cast<_Float16>(o[qs][dt][1] * inv),
-                       static_cast<_Float16>(o[qs][dt][2] * inv), static_cast<_Float16>(o[qs][dt][3] * inv)};
-      *reinterpret_cast<f16x4*>(out + 16 * dt) = r;
-    }
+  stt.store(p, q0, qi, q_len, h, qd);
+}
+
+// FP16 cache: tiles go from HBM to LDS by the load-to-LDS path (no register
+// staging, no VGPRs held by loads in flight), three stages with two tiles in
+// flight while the third is consumed.  Each wave instruction writes 1 KiB of
+// LDS contiguously, 16 bytes per lane, so the layouts are swizzled on the
+// source side: LDS chunk c (16 bytes) of key row r holds K chunk c ^ (r & 7)
+// and V chunk c ^ ((r & 3) << 1).  K fragments are then read 8 rows by 8
+// distinct bank groups; V^T fragments come from the transposing LDS read
+// (ds_read_tr16_b64), four key rows per 16 lanes at four distinct bank
+// groups.  The block table of the sequence is copied to LDS first so that
+// the loop issues no other global load (whose wait would also drain the
+// tiles in flight).
+constexpr int kDmaStages = 3;
+constexpr int kDmaTableCap = 4096;  // block-table entries staged in LDS
+
+#define RLK_LDS __attribute__((address_space(3)))
+
+template <int D>
+struct PfDma {
+  static constexpr int kBQ = PfShape<D, false>::kBQ;
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kTileBytes = kBK * kRowBytes;  // one K or V tile
+  static constexpr int kStageBytes = 2 * kTileBytes;
+  static constexpr int kThreads = PfShape<D, false>::kThreads;
+  static constexpr int kWaves = kThreads / 64;
+  static constexpr int kOpsPerTile = kTileBytes / 1024;
+  static constexpr int kOps = 2 * kOpsPerTile / kWaves;  // instructions per wave per stage
+  static_assert(kOpsPerTile % kWaves == 0, "whole instructions per wave");
+  static size_t lds_bytes(int table_entries) {
+    return static_cast<size_t>(kDmaStages) * kStageBytes + 4 * ((table_entries + 3) & ~3);
   }
+};
+
+// s_waitcnt vmcnt(N): the compiler does not count load-to-LDS instructions
+// against the LDS reads that follow them, so the wait is explicit
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int D>
+__global__ __launch_bounds__((PfShape<D, false>::kThreads), (PfShape<D, false>::kWavesPerSimd)) void
+prefill_dma_kernel(PrefillArgs a) {
+  using G = PfDma<D>;
+  constexpr int kQS = PfShape<D, false>::kQS, kBQ = PfShape<D, false>::kBQ;
+  constexpr int kSteps = D / 32, kWaveRows = 16 * kQS;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[];
+  int32_t* tab_lds = reinterpret_cast<int32_t*>(pf_lds + kDmaStages * G::kStageBytes);
+
+  const rlk_attention_params& p = a.p;
+  const rlk_prefill_attention_work& w = a.w;
+  const int h = blockIdx.y;
+  const int seq = w.seq_ids[blockIdx.z];
+  const int q_len = w.q_len[seq];
+  const int qt = (q_len + kBQ - 1) / kBQ - 1 - static_cast<int>(blockIdx.x);
+  if (qt < 0) return;  // workgroup-uniform
+  const int q0 = w.q_start[seq], ctx = w.ctx_len[seq];
+  const int past = ctx - q_len;
+  const int hkv = p.kv.num_kv_heads, bs = p.kv.block_size;
+  const int kvh = h / (p.num_heads / hkv);
+  const int32_t* table = p.block_tables + static_cast<size_t>(seq) * p.max_blocks_per_seq;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, qd = lane >> 4;
+  const int row0 = qt * kBQ + wave * kWaveRows;
+  const int kv_end = past + min(q_len, (qt + 1) * kBQ);
+  const int wave_rows = min(q_len - row0, kWaveRows);
+  const int wave_kv_end = wave_rows > 0 ? past + row0 + wave_rows : 0;
+  int qi[kQS];
+#pragma unroll
+  for (int qs = 0; qs < kQS; ++qs) qi[qs] = row0 + 16 * qs + c16;
+
+  f16x8 qb[kQS][kSteps];
+#pragma unroll
+  for (int qs = 0; qs < kQS; ++qs)
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      qb[qs][ks] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (qi[qs] < q_len)
+        qb[qs][ks] = __builtin_bit_cast(
+            f16x8, load16(p.q + static_cast<size_t>(q0 + qi[qs]) * p.q_stride + h * D + 32 * ks + 8 * qd));
+    }
+  const int nblk = min((kv_end + bs - 1) / bs, kDmaTableCap);
+  for (int i = tid; i < nblk; i += G::kThreads) tab_lds[i] = table[i];
+  // q is consumed here so that no wait for it lands inside the tile loop
+#pragma unroll
+  for (int qs = 0; qs < kQS; ++qs)
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) asm volatile("" : "+v"(qb[qs][ks]));
+  __syncthreads();
+
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.kv.k);
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.kv.v);
+  // keys past kv_end read the last key again: finite, and masked out of every row
+  auto issue = [&](int tile, int stage) {
+    const int k0 = tile * kBK;
+    unsigned char* sb = pf_lds + stage * G::kStageBytes;
+#pragma unroll
+    for (int u = 0; u < G::kOps; ++u) {
+      constexpr int kHalf = G::kOps / 2;
+      const bool isv = u >= kHalf;
+      const int op = wave + G::kWaves * (isv ? u - kHalf : u);  // 1 KiB piece of the tile
+      const int byte = op * 1024 + lane * 16;
+      const int r = byte / G::kRowBytes, c = (byte % G::kRowBytes) / 16;
+      const int pos = min(k0 + r, kv_end - 1);
+      const int src_c = isv ? c ^ ((r & 3) << 1) : c ^ (r & 7);
+      const size_t cell = (static_cast<size_t>(tab_lds[pos / bs]) * hkv + kvh) * bs + pos % bs;
+      const uint16_t* src = (isv ? vbase : kbase) + cell * D + src_c * 8;
+      __builtin_amdgcn_global_load_lds(
+          src, (RLK_LDS void*)(sb + (isv ? G::kTileBytes : 0) + op * 1024), 16, 0, 0);
+    }
+  };
+
+  PfState<D, kQS> stt(p.scale);
+  const int tk = c16 >> 2, tm = c16 & 3;  // transposing read: key row and dim quad of this lane
+  auto compute = [&](int k0, int stage) {
+    const unsigned char* kt = pf_lds + stage * G::kStageBytes;
+    const uint32_t vt_addr = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((RLK_LDS const unsigned char*)(kt + G::kTileBytes)));
+    attend_tile<D, kQS>(
+        stt, k0, qb, qi, q_len, past, row0, wave_rows, qd,
+        [&](int t, int ks) {
+          const int row = 16 * t + c16;
+          return *reinterpret_cast<const f16x8*>(kt + row * G::kRowBytes +
+                                                 (((4 * ks + qd) ^ (c16 & 7)) << 4));
+        },
+        [&](int j, int dt) {
+          // the transposing reads are issued as inline asm: the compiler's
+          // own form of them waits for every load-to-LDS in flight
+          const int off = ((((2 * dt + (tm >> 1)) ^ (tk << 1)) << 4) | ((tm & 1) << 3));
+          const uint32_t addr = vt_addr + (32 * j + 4 * qd + tk) * G::kRowBytes + off;
+          u32x2 lo, hi;
+          asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %2 offset:%3"
+                       : "=v"(lo), "=v"(hi)
+                       : "v"(addr), "n"(16 * G::kRowBytes));
+          return __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        },
+        [](f16x8(&va)[D / 16]) {
+          if constexpr (D == 128)
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]), "+v"(va[4]),
+                           "+v"(va[5]), "+v"(va[6]), "+v"(va[7]));
+          else
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]));
+        });
+  };
+
+  const int ntiles = (kv_end + kBK - 1) / kBK;
+  issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) wait_vmem<G::kOps>();
+    else wait_vmem<0>();
+    // tile t is in LDS for every wave; tile t - 1 is consumed (its LDS reads
+    // fed MFMAs before this point).  A bare barrier: __syncthreads() would
+    // also drain the tiles still in flight.
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + 2 < ntiles) issue(t + 2, (t + 2) % kDmaStages);
+    if (t * kBK < wave_kv_end) compute(t * kBK, t % kDmaStages);
+  }
+
+  stt.store(p, q0, qi, q_len, h, qd);
 }
 
 int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work* work,
@@ -409,6 +612,31 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
     const dim3 grid((rows + S::kBQ - 1) / S::kBQ, p.num_heads, w.num_seqs);
     kernel<<<grid, S::kThreads, 0, stream>>>(a);
   };
+  // FP16 caches take the load-to-LDS kernel when the block table fits its LDS
+  // copy; RLK_TUNE_PREFILL_DMA=0 forces the register-staged kernel
+  if (!int8 && p.max_blocks_per_seq <= kDmaTableCap && tune_knob("RLK_TUNE_PREFILL_DMA", 1) != 0) {
+    auto dma = [&](auto kernel, auto geo) -> int {
+      using G = decltype(geo);
+      const size_t lds = G::lds_bytes(p.max_blocks_per_seq);
+      static size_t granted[64] = {0};
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || granted[dev] < lds) {
+        const size_t want = G::lds_bytes(kDmaTableCap);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(want));
+        if (e != hipSuccess)
+          return fail(RLK_EUNSUPPORTED, "%s: %zu bytes of LDS refused (%s)", what, want,
+                      hipGetErrorString(e));
+        if (dev >= 0 && dev < 64) granted[dev] = want;
+      }
+      const dim3 grid((rows + G::kBQ - 1) / G::kBQ, p.num_heads, w.num_seqs);
+      kernel<<<grid, G::kThreads, lds, stream>>>(a);
+      return launch_status(what);
+    };
+    return p.kv.head_dim == 64 ? dma(prefill_dma_kernel<64>, PfDma<64>{})
+                               : dma(prefill_dma_kernel<128>, PfDma<128>{});
+  }
   if (p.kv.head_dim == 64) {
     if (int8) go(prefill_attention_kernel<64, true>, PfShape<64, true>{});
     else go(prefill_attention_kernel<64, false>, PfShape<64, false>{});

@@ -14,7 +14,12 @@ then (1) every sequence is prefilled from position 0, and (2) chunked prefill:
 the second half of each sequence attends to the cached first half, with its q
 rows gathered into a compact buffer.  Larger cases cover several 64-row query
 tiles and 64-key tiles, contexts that are not multiples of either, fp16-stored
-INT8 scales, and the Llama-3.1-8B C3 chunks at full size (sampled rows)."""
+INT8 scales, and the Llama-3.1-8B C3 chunks at full size (sampled rows).
+
+FP16 caches have two kernels: one that copies tiles to LDS with load-to-LDS
+instructions (the default when the block table fits its LDS copy) and one that
+stages them through registers (RLK_TUNE_PREFILL_DMA=0, and every INT8 cache);
+each test runs under both settings."""
 import numpy as np
 import pytest
 
@@ -27,6 +32,12 @@ pytestmark = pytest.mark.gpu
 REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
              (6, 2, 128, False, [700]), (8, 1, 64, False, [48, 17]),
              (8, 2, 128, True, [33, 280]), (4, 2, 64, True, [520])]
+
+
+@pytest.fixture(autouse=True, params=["dma", "reg"])
+def kernel_path(request, monkeypatch):
+    monkeypatch.setenv("RLK_TUNE_PREFILL_DMA", "1" if request.param == "dma" else "0")
+    return request.param
 
 
 @pytest.fixture(scope="module")
@@ -139,21 +150,25 @@ def test_prefill_attention_reference_geometries(torch_cuda, hq, hkv, D, int8, le
 
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("kv", ["fp16", "int8", "int8_f16scale"])
-def test_prefill_attention_random_cache_many_tiles(torch_cuda, D, kv):
+@pytest.mark.parametrize("bs,pad", [(16, 0), (7, 0), (16, 4100)])
+def test_prefill_attention_random_cache_many_tiles(torch_cuda, D, kv, bs, pad, kernel_path):
     """Several query and key tiles per sequence, GQA 4, random cache contents,
-    chunks with and without cached context (lengths not multiples of 64)."""
+    chunks with and without cached context (lengths not multiples of 64).
+    Block size 7 puts block boundaries at odd keys inside a tile; a block
+    table padded past 4096 columns exceeds the load-to-LDS kernel's LDS copy
+    of it (the register-staged kernel runs)."""
     torch = torch_cuda
     from redline_amd import kernels as K
-    say(f"prefill random D={D} kv={kv}")
-    rng = np.random.default_rng(D + len(kv))
-    hq, hkv, bs = 8, 2, 16
+    say(f"prefill random D={D} kv={kv} bs={bs} pad={pad} path={kernel_path}")
+    rng = np.random.default_rng(D + len(kv) + bs)
+    hq, hkv = 8, 2
     int8 = kv != "fp16"
     chunks = [(0, 190), (333, 75), (64, 64), (0, 1), (1000, 130)]
     lens = [a + b for a, b in chunks]
     S = len(chunks)
     nblk = 1 + sum((L + bs - 1) // bs for L in lens)
     ids = rng.permutation(np.arange(1, nblk)).astype(np.int32)
-    maxb = max((L + bs - 1) // bs for L in lens)
+    maxb = max((L + bs - 1) // bs for L in lens) + pad
     tables = np.zeros((S, maxb), np.int32)
     nxt = 0
     for i, L in enumerate(lens):
