@@ -179,6 +179,60 @@ struct PfState {
   }
 };
 
+// Online softmax of one 64-key tile: s holds raw scores (lane (qd, c16): keys
+// k0 + 16 t + 4 qd + e of query row qi[qs]), turned into the probabilities
+// pb (fp16, the B operands of the O^T steps); the running max, sum and output
+// are updated.  kMasked: keys past a row's position get probability 0.
+template <bool kMasked, int D, int QS>
+__device__ __forceinline__ void softmax_tile(PfState<D, QS>& st, f32x4 (&s)[QS][4], f16x8 (&pb)[QS][2],
+                                             int k0, const int (&qi)[QS], int q_len, int past, int qd) {
+  const float c = st.c;
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    if constexpr (kMasked) {
+      // keys k0 + 16 t + 4 qd + e <= past + qi: e <= lim - 16 t
+      const int lim = qi[qs] < q_len ? past + qi[qs] - k0 - 4 * qd : -1000;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (16 * t + e > lim) s[qs][t][e] = -FLT_MAX;
+    }
+    float mt = -FLT_MAX;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[qs][t][e]);
+    mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
+    const float m_new = fmaxf(st.m_run[qs], mt);
+    const float alpha =
+        st.m_run[qs] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
+    const bool grew = m_new > st.m_run[qs];
+    const float mc = m_new * c;
+    float ts = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
+        ts += s[qs][t][e];
+      }
+    ts = rows_sum<true>(rows_sum<false>(ts));
+    st.l_run[qs] = st.l_run[qs] * alpha + ts;
+    st.m_run[qs] = m_new;
+    if (__any(grew)) {  // rescale only when some row's max moved
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) st.o[qs][dt] *= alpha;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
+                        static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
+                        static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
+                        static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
+  }
+}
+
 // One 64-key tile for a wave's query rows.  kfrag(t, ks): the A operand of
 // S^T subtile t (keys 16 t .. + 15 of the tile), step ks (dims 32 ks .. + 31):
 // lane (qd, c16) gets key 16 t + c16, dims 32 ks + 8 qd .. + 7.  vfrag(j, dt):
@@ -209,64 +263,28 @@ __device__ __forceinline__ void attend_tile(PfState<D, QS>& st, int k0, const f1
   }
   // masks only where the tile reaches past a row's position (the diagonal,
   // the context end) or the wave has rows past q_len
-  const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < 16 * QS;
-  const float c = st.c;
   f16x8 pb[QS][2];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    float mt = -FLT_MAX;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (masked) {
-          const int kp = k0 + 16 * t + 4 * qd + e;
-          if (!(qi[qs] < q_len && kp <= past + qi[qs])) s[qs][t][e] = -FLT_MAX;
-        }
-        mt = fmaxf(mt, s[qs][t][e]);
-      }
-    mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
-    const float m_new = fmaxf(st.m_run[qs], mt);
-    const float alpha =
-        st.m_run[qs] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
-    const bool grew = m_new > st.m_run[qs];
-    const float mc = m_new * c;
-    float ts = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
-        ts += s[qs][t][e];
-      }
-    ts = rows_sum<true>(rows_sum<false>(ts));
-    st.l_run[qs] = st.l_run[qs] * alpha + ts;
-    st.m_run[qs] = m_new;
-    if (__any(grew)) {  // rescale only when some row's max moved
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) st.o[qs][dt] *= alpha;
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
-                        static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
-                        static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
-                        static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
-  }
+  if (k0 + kBK - 1 > past + row0 || wave_rows < 16 * QS)
+    softmax_tile<true>(st, s, pb, k0, qi, q_len, past, qd);
+  else
+    softmax_tile<false>(st, s, pb, k0, qi, q_len, past, qd);
   // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
   // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  // (j is passed to vfrag as a compile-time constant)
+  auto step = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
     f16x8 va[kDTiles];
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) va[dt] = vfrag(j, dt);
+    for (int dt = 0; dt < kDTiles; ++dt) va[dt] = vfrag(jc, dt);
     vready(va);
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt)
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs)
         st.o[qs][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], pb[qs][j], st.o[qs][dt], 0, 0, 0);
-  }
+  };
+  step(std::integral_constant<int, 0>{});
+  step(std::integral_constant<int, 1>{});
 }
 
 template <int D, bool kInt8>
@@ -423,11 +441,12 @@ prefill_attention_kernel(PrefillArgs a) {
 // staging, no VGPRs held by loads in flight), three stages with two tiles in
 // flight while the third is consumed.  Each wave instruction writes 1 KiB of
 // LDS contiguously, 16 bytes per lane, so the layouts are swizzled on the
-// source side: LDS chunk c (16 bytes) of key row r holds K chunk c ^ (r & 7)
-// and V chunk c ^ ((r & 3) << 1).  K fragments are then read 8 rows by 8
-// distinct bank groups; V^T fragments come from the transposing LDS read
-// (ds_read_tr16_b64), four key rows per 16 lanes at four distinct bank
-// groups.  The block table of the sequence is copied to LDS first so that
+// source side: LDS chunk c (16 bytes) of key row r holds K chunk c ^ kswz(r)
+// and V chunk c ^ vswz(r).  The swizzles make every LDS read conflict-free
+// with 64 banks of 4 bytes: a 16-byte K read covers 16 key rows at 16
+// distinct 16-byte slots of 256 bytes, and a transposing V read
+// (ds_read_tr16_b64, 8 bytes a lane) covers 8 key rows at 8 distinct 32-byte
+// slots.  The block table of the sequence is copied to LDS first so that
 // the loop issues no other global load (whose wait would also drain the
 // tiles in flight).
 constexpr int kDmaStages = 3;
@@ -446,6 +465,10 @@ struct PfDma {
   static constexpr int kOpsPerTile = kTileBytes / 1024;
   static constexpr int kOps = 2 * kOpsPerTile / kWaves;  // instructions per wave per stage
   static_assert(kOpsPerTile % kWaves == 0, "whole instructions per wave");
+  // row pitch 256 bytes (D = 128): 16 slots a row; 128 bytes (D = 64): a
+  // 256-byte span holds rows r and r ^ 1
+  __device__ static int kswz(int r) { return D == 128 ? r & 15 : (r >> 1) & 7; }
+  __device__ static int vswz(int r) { return D == 128 ? (r & 7) << 1 : ((r >> 1) & 3) << 1; }
   static size_t lds_bytes(int table_entries) {
     return static_cast<size_t>(kDmaStages) * kStageBytes + 4 * ((table_entries + 3) & ~3);
   }
@@ -510,30 +533,75 @@ prefill_dma_kernel(PrefillArgs a) {
     for (int ks = 0; ks < kSteps; ++ks) asm volatile("" : "+v"(qb[qs][ks]));
   __syncthreads();
 
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.kv.k);
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.kv.v);
+  // Each lane's piece u of a tile: key row r_u and 16-byte chunk c_u of the
+  // LDS image, fixed for the whole loop.
+  constexpr int kHalf = G::kOps / 2;
+  int lr[kHalf], lc[kHalf];
+#pragma unroll
+  for (int u = 0; u < kHalf; ++u) {
+    const int byte = (wave + G::kWaves * u) * 1024 + lane * 16;
+    lr[u] = byte / G::kRowBytes;
+    lc[u] = (byte % G::kRowBytes) / 16;
+  }
+  const unsigned char* kbase = static_cast<const unsigned char*>(p.kv.k);
+  const unsigned char* vbase = static_cast<const unsigned char*>(p.kv.v);
+  auto dma = [&](unsigned char* sb, int u, bool isv, const unsigned char* src) {
+    __builtin_amdgcn_global_load_lds(
+        src, (RLK_LDS void*)(sb + (isv ? G::kTileBytes : 0) + (wave + G::kWaves * u) * 1024), 16, 0, 0);
+  };
+  // Block sizes that are powers of two: a whole tile inside the context takes
+  // the block of each piece from a lane constant (row >> log2 bs) plus the
+  // tile's first block, and the byte offset inside the block from a lane
+  // constant plus the tile's offset into its block (non-zero for bs > 64).
+  const bool pow2 = (bs & (bs - 1)) == 0;
+  const int lbs = __builtin_ctz(bs);
+  const uint32_t block_bytes = static_cast<uint32_t>(hkv) * bs * G::kRowBytes;
+  int lblk[kHalf];
+  uint32_t lk_off[kHalf], lv_off[kHalf];
+#pragma unroll
+  for (int u = 0; u < kHalf; ++u) {
+    const int r = lr[u];
+    lblk[u] = r >> lbs;
+    const uint32_t row_off = static_cast<uint32_t>(kvh * bs + (r & (bs - 1))) * G::kRowBytes;
+    lk_off[u] = row_off + ((lc[u] ^ G::kswz(r)) << 4);
+    lv_off[u] = row_off + ((lc[u] ^ G::vswz(r)) << 4);
+  }
   // keys past kv_end read the last key again: finite, and masked out of every row
   auto issue = [&](int tile, int stage) {
     const int k0 = tile * kBK;
     unsigned char* sb = pf_lds + stage * G::kStageBytes;
+    if (pow2 && k0 + kBK <= kv_end) {
+      const int blk0 = k0 >> lbs;
+      const uint32_t koff = static_cast<uint32_t>(k0 & (bs - 1)) * G::kRowBytes;
 #pragma unroll
-    for (int u = 0; u < G::kOps; ++u) {
-      constexpr int kHalf = G::kOps / 2;
-      const bool isv = u >= kHalf;
-      const int op = wave + G::kWaves * (isv ? u - kHalf : u);  // 1 KiB piece of the tile
-      const int byte = op * 1024 + lane * 16;
-      const int r = byte / G::kRowBytes, c = (byte % G::kRowBytes) / 16;
+      for (int u = 0; u < kHalf; ++u) {
+        const uint64_t bb = static_cast<uint64_t>(static_cast<uint32_t>(tab_lds[blk0 + lblk[u]])) * block_bytes;
+        dma(sb, u, false, kbase + bb + (lk_off[u] + koff));
+        dma(sb, u, true, vbase + bb + (lv_off[u] + koff));
+      }
+      return;
+    }
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) {
+      const int r = lr[u];
       const int pos = min(k0 + r, kv_end - 1);
-      const int src_c = isv ? c ^ ((r & 3) << 1) : c ^ (r & 7);
-      const size_t cell = (static_cast<size_t>(tab_lds[pos / bs]) * hkv + kvh) * bs + pos % bs;
-      const uint16_t* src = (isv ? vbase : kbase) + cell * D + src_c * 8;
-      __builtin_amdgcn_global_load_lds(
-          src, (RLK_LDS void*)(sb + (isv ? G::kTileBytes : 0) + op * 1024), 16, 0, 0);
+      const int blk = pos / bs, off = pos - blk * bs;
+      const size_t cell = (static_cast<size_t>(tab_lds[blk]) * hkv + kvh) * bs + off;
+      dma(sb, u, false, kbase + cell * G::kRowBytes + ((lc[u] ^ G::kswz(r)) << 4));
+      dma(sb, u, true, vbase + cell * G::kRowBytes + ((lc[u] ^ G::vswz(r)) << 4));
     }
   };
 
   PfState<D, kQS> stt(p.scale);
-  const int tk = c16 >> 2, tm = c16 & 3;  // transposing read: key row and dim quad of this lane
+  // transposing V reads: lane (qd, c16) reads key row 4 qd + tk (+ 32 j, + 16)
+  // at dims 16 dt + 4 tm; byte offsets inside a V tile, for j = 0
+  const int tk = c16 >> 2, tm = c16 & 3;
+  uint32_t vrd[D / 16];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) {
+    const int row = 4 * qd + tk;  // row + 32 j and row + 16 share its swizzle
+    vrd[dt] = row * G::kRowBytes + ((((2 * dt + (tm >> 1)) ^ G::vswz(row)) << 4) | ((tm & 1) << 3));
+  }
   auto compute = [&](int k0, int stage) {
     const unsigned char* kt = pf_lds + stage * G::kStageBytes;
     const uint32_t vt_addr = static_cast<uint32_t>(
@@ -543,17 +611,17 @@ prefill_dma_kernel(PrefillArgs a) {
         [&](int t, int ks) {
           const int row = 16 * t + c16;
           return *reinterpret_cast<const f16x8*>(kt + row * G::kRowBytes +
-                                                 (((4 * ks + qd) ^ (c16 & 7)) << 4));
+                                                 (((4 * ks + qd) ^ G::kswz(c16)) << 4));
         },
-        [&](int j, int dt) {
+        [&](auto jc, int dt) {
           // the transposing reads are issued as inline asm: the compiler's
           // own form of them waits for every load-to-LDS in flight
-          const int off = ((((2 * dt + (tm >> 1)) ^ (tk << 1)) << 4) | ((tm & 1) << 3));
-          const uint32_t addr = vt_addr + (32 * j + 4 * qd + tk) * G::kRowBytes + off;
+          constexpr int kOff = 32 * decltype(jc)::value * G::kRowBytes;
+          const uint32_t addr = vt_addr + vrd[dt];
           u32x2 lo, hi;
-          asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %2 offset:%3"
+          asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
                        : "=v"(lo), "=v"(hi)
-                       : "v"(addr), "n"(16 * G::kRowBytes));
+                       : "v"(addr), "n"(kOff), "n"(kOff + 16 * G::kRowBytes));
           return __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
         },
         [](f16x8(&va)[D / 16]) {
@@ -614,7 +682,11 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
   };
   // FP16 caches take the load-to-LDS kernel when the block table fits its LDS
   // copy; RLK_TUNE_PREFILL_DMA=0 forces the register-staged kernel
-  if (!int8 && p.max_blocks_per_seq <= kDmaTableCap && tune_knob("RLK_TUNE_PREFILL_DMA", 1) != 0) {
+  // (the kernel keeps byte offsets inside a cache block in 32 bits)
+  const bool dma_fits = p.max_blocks_per_seq <= kDmaTableCap &&
+                        static_cast<uint64_t>(p.kv.num_kv_heads) * p.kv.block_size * p.kv.head_dim * 2 <
+                            (uint64_t{1} << 32);
+  if (!int8 && dma_fits && tune_knob("RLK_TUNE_PREFILL_DMA", 1) != 0) {
     auto dma = [&](auto kernel, auto geo) -> int {
       using G = decltype(geo);
       const size_t lds = G::lds_bytes(p.max_blocks_per_seq);
