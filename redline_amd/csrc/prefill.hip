@@ -182,14 +182,17 @@ struct PfState {
 // Online softmax of one 64-key tile: s holds raw scores (lane (qd, c16): keys
 // k0 + 16 t + 4 qd + e of query row qi[qs]), turned into the probabilities
 // pb (fp16, the B operands of the O^T steps); the running max, sum and output
-// are updated.  kMasked: keys past a row's position get probability 0.
-template <bool kMasked, int D, int QS>
+// are updated.  Keys past a row's position get probability 0 where masked
+// (kMask 1: always, 0: never, 2: as the runtime flag says; 2 keeps one copy
+// of the code for kernels short of registers).
+template <int kMask, int D, int QS>
 __device__ __forceinline__ void softmax_tile(PfState<D, QS>& st, f32x4 (&s)[QS][4], f16x8 (&pb)[QS][2],
-                                             int k0, const int (&qi)[QS], int q_len, int past, int qd) {
+                                             int k0, const int (&qi)[QS], int q_len, int past, int qd,
+                                             bool masked = true) {
   const float c = st.c;
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
-    if constexpr (kMasked) {
+    if (kMask == 1 || (kMask == 2 && masked)) {
       // keys k0 + 16 t + 4 qd + e <= past + qi: e <= lim - 16 t
       const int lim = qi[qs] < q_len ? past + qi[qs] - k0 - 4 * qd : -1000;
 #pragma unroll
@@ -204,11 +207,17 @@ __device__ __forceinline__ void softmax_tile(PfState<D, QS>& st, f32x4 (&s)[QS][
 #pragma unroll
       for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[qs][t][e]);
     mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
+    // The reference max moves only when the tile's max exceeds it by more
+    // than 2^8 in probability: below that, probabilities up to 256 are exact
+    // enough in fp16 and the output and sum need no rescale.
     const float m_new = fmaxf(st.m_run[qs], mt);
-    const float alpha =
-        st.m_run[qs] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
-    const bool grew = m_new > st.m_run[qs];
-    const float mc = m_new * c;
+    const bool grew = (m_new - st.m_run[qs]) * c > 8.f;  // first valid tile: always
+    const float alpha = !grew ? 1.f
+                        : st.m_run[qs] == -FLT_MAX
+                            ? 0.f
+                            : __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
+    if (grew) st.m_run[qs] = m_new;
+    const float mc = st.m_run[qs] * c;
     float ts = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -219,8 +228,7 @@ __device__ __forceinline__ void softmax_tile(PfState<D, QS>& st, f32x4 (&s)[QS][
       }
     ts = rows_sum<true>(rows_sum<false>(ts));
     st.l_run[qs] = st.l_run[qs] * alpha + ts;
-    st.m_run[qs] = m_new;
-    if (__any(grew)) {  // rescale only when some row's max moved
+    if (__any(grew)) {  // rescale only when some row's reference max moved
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) st.o[qs][dt] *= alpha;
     }
@@ -240,7 +248,8 @@ __device__ __forceinline__ void softmax_tile(PfState<D, QS>& st, f32x4 (&s)[QS][
 // c16 of keys 32 j + 4 qd + e and then 32 j + 16 + 4 qd + e (e = 0..3).
 // vready(va) runs after the fragments of a step are requested and before the
 // MFMAs use them (a wait for reads the compiler does not track).
-template <int D, int QS, class KFrag, class VFrag, class VReady>
+// kSplitMask: separate code for masked and unmasked tiles.
+template <int D, int QS, bool kSplitMask, class KFrag, class VFrag, class VReady>
 __device__ __forceinline__ void attend_tile(PfState<D, QS>& st, int k0, const f16x8 (&qb)[QS][D / 32],
                                             const int (&qi)[QS], int q_len, int past, int row0,
                                             int wave_rows, int qd, KFrag kfrag, VFrag vfrag,
@@ -264,10 +273,13 @@ __device__ __forceinline__ void attend_tile(PfState<D, QS>& st, int k0, const f1
   // masks only where the tile reaches past a row's position (the diagonal,
   // the context end) or the wave has rows past q_len
   f16x8 pb[QS][2];
-  if (k0 + kBK - 1 > past + row0 || wave_rows < 16 * QS)
-    softmax_tile<true>(st, s, pb, k0, qi, q_len, past, qd);
-  else
-    softmax_tile<false>(st, s, pb, k0, qi, q_len, past, qd);
+  const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < 16 * QS;
+  if constexpr (kSplitMask) {
+    if (masked) softmax_tile<1>(st, s, pb, k0, qi, q_len, past, qd);
+    else softmax_tile<0>(st, s, pb, k0, qi, q_len, past, qd);
+  } else {
+    softmax_tile<2>(st, s, pb, k0, qi, q_len, past, qd, masked);
+  }
   // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
   // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
   // (j is passed to vfrag as a compile-time constant)
@@ -412,7 +424,7 @@ prefill_attention_kernel(PrefillArgs a) {
 
   PfState<D, kQS> stt(p.scale);
   auto compute = [&](int k0) {
-    attend_tile<D, kQS>(
+    attend_tile<D, kQS, false>(
         stt, k0, qb, qi, q_len, past, row0, wave_rows, qd,
         [&](int t, int ks) {
           return *reinterpret_cast<const f16x8*>(&k_lds[16 * t + c16][32 * ks + 8 * qd]);
@@ -606,7 +618,7 @@ prefill_dma_kernel(PrefillArgs a) {
     const unsigned char* kt = pf_lds + stage * G::kStageBytes;
     const uint32_t vt_addr = static_cast<uint32_t>(
         reinterpret_cast<uintptr_t>((RLK_LDS const unsigned char*)(kt + G::kTileBytes)));
-    attend_tile<D, kQS>(
+    attend_tile<D, kQS, true>(
         stt, k0, qb, qi, q_len, past, row0, wave_rows, qd,
         [&](int t, int ks) {
           const int row = 16 * t + c16;

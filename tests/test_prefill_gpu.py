@@ -293,3 +293,50 @@ def test_prefill_attention_errors(torch_cuda):
         K.paged_attention_prefill(p, K.prefill_work(z, z, z, z, 1, 1))
     torch.cuda.synchronize()
     assert not out.any()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_attention_rising_scores(torch_cuda, D, kernel_path):
+    """Scores that rise with the key position by about 40 (natural units) over
+    the context, plus noise: the running max of every row moves again and
+    again, past and within the kernel's rescale threshold."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    say(f"prefill rising scores D={D} path={kernel_path}")
+    rng = np.random.default_rng(77 + D)
+    hq, hkv, bs = 4, 2, 16
+    past, ql = 700, 300
+    L = past + ql
+    nblk = 1 + (L + bs - 1) // bs
+    tables = rng.permutation(np.arange(1, nblk)).astype(np.int32)[None, :]
+    u = np.zeros(D, np.float32)
+    u[:8] = 1 / np.sqrt(8)
+    scale = 1 / np.sqrt(D)
+    drift = 40.0 / scale / 4.0  # q . k grows by 40 / scale over the context
+    kc = np.zeros((nblk, hkv, bs, D), np.float16)
+    vc = randn_f16(rng, (nblk, hkv, bs, D))
+    for pos in range(L):
+        b, o = tables[0, pos // bs], pos % bs
+        kc[b, :, o] = (rng.standard_normal((hkv, D)) * 0.5 + (pos / L) * drift * u).astype(np.float16)
+    q = (rng.standard_normal((ql, hq * D)) * 0.5).astype(np.float32)
+    for h in range(hq):
+        q[:, h * D:(h + 1) * D] += 4.0 * u
+    q = q.astype(np.float16)
+    sid = np.zeros(1, np.int32)
+    q_start, q_len, ctx = np.zeros(1, np.int32), np.array([ql], np.int32), np.array([L], np.int32)
+    want = oracle.paged_attention_prefill(q, hq * D, hq, scale, kc, vc, None, None, tables, sid,
+                                          q_start, q_len, ctx, ql, False)
+    cache = K.KVCache(1, nblk, hkv, D, bs, K.KVDType.kFP16)
+    k, v, _, _ = cache.tensors(0)
+    k.copy_(dev(torch, kc))
+    v.copy_(dev(torch, vc))
+    out = torch.zeros((ql, hq * D), dtype=torch.float16, device="cuda")
+    d = {name: dev(torch, a) for name, a in (("q", q), ("tables", tables), ("pos", np.zeros(ql, np.int32)),
+                                            ("sid", sid), ("q_start", q_start), ("q_len", q_len),
+                                            ("ctx", ctx))}
+    p = K.attention_params(d["q"], hq * D, out, hq, scale, cache.layer(0), d["tables"], tables.shape[1],
+                           d["pos"])
+    w = K.prefill_work(d["sid"], d["q_start"], d["q_len"], d["ctx"], 1, (ql + 31) // 32)
+    K.paged_attention_prefill(p, w)
+    torch.cuda.synchronize()
+    assert_close_f16(out.cpu().numpy(), want, what="prefill rising scores")
