@@ -181,122 +181,188 @@ struct PfState {
 
 // Online softmax of one 64-key tile: s holds raw scores (lane (qd, c16): keys
 // k0 + 16 t + 4 qd + e of query row qi[qs]), turned into the probabilities
-// pb (fp16, the B operands of the O^T steps); the running max, sum and output
-// are updated.  Keys past a row's position get probability 0 where masked
+// pb (fp16, the B operands of the O^T steps); the running max and sum are
+// updated, and alpha[qs] is the factor the output of query set qs takes (the
+// function returns whether any lane's differs from 1: rescale_output).  Keys past a row's position get probability 0 where masked
 // (kMask 1: always, 0: never, 2: as the runtime flag says; 2 keeps one copy
 // of the code for kernels short of registers).
 template <int kMask, int D, int QS>
-__device__ __forceinline__ void softmax_tile(PfState<D, QS>& st, f32x4 (&s)[QS][4], f16x8 (&pb)[QS][2],
-                                             int k0, const int (&qi)[QS], int q_len, int past, int qd,
-                                             bool masked = true) {
+__device__ __forceinline__ bool softmax_max(PfState<D, QS>& st, f32x4 (&s)[QS][4], int qs, float& alpha,
+                                            int k0, const int (&qi)[QS], int q_len, int past, int qd,
+                                            bool masked) {
   const float c = st.c;
+  if (kMask == 1 || (kMask == 2 && masked)) {
+    // keys k0 + 16 t + 4 qd + e <= past + qi: e <= lim - 16 t
+    const int lim = qi[qs] < q_len ? past + qi[qs] - k0 - 4 * qd : -1000;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (16 * t + e > lim) s[qs][t][e] = -FLT_MAX;
+  }
+  float mt = -FLT_MAX;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[qs][t][e]);
+  mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
+  // The reference max moves only when the tile's max exceeds it by more
+  // than 2^8 in probability: below that, probabilities up to 256 are exact
+  // enough in fp16 and the output and sum need no rescale.
+  const float m_new = fmaxf(st.m_run[qs], mt);
+  const bool grew = (m_new - st.m_run[qs]) * c > 8.f;  // first valid tile: always
+  // branch-free: 2^((-FLT_MAX - m) c) flushes to 0 for the first valid tile
+  const float e = __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
+  alpha = grew ? e : 1.f;
+  if (grew) st.m_run[qs] = m_new;
+  return grew;
+}
+
+template <int D, int QS>
+__device__ __forceinline__ void softmax_exp(PfState<D, QS>& st, f32x4 (&s)[QS][4], f16x8 (&pb)[QS][2],
+                                            int qs, float alpha) {
+  const float c = st.c, mc = st.m_run[qs] * c;
+  float ts = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
+      ts += s[qs][t][e];
+    }
+  ts = rows_sum<true>(rows_sum<false>(ts));
+  st.l_run[qs] = st.l_run[qs] * alpha + ts;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
+                      static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
+                      static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
+                      static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
+}
+
+template <int kMask, int D, int QS>
+__device__ __forceinline__ bool softmax_core(PfState<D, QS>& st, f32x4 (&s)[QS][4], f16x8 (&pb)[QS][2],
+                                             float (&alpha)[QS], int k0, const int (&qi)[QS], int q_len,
+                                             int past, int qd, bool masked = true) {
+  bool any_grew = false;
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
-    if (kMask == 1 || (kMask == 2 && masked)) {
-      // keys k0 + 16 t + 4 qd + e <= past + qi: e <= lim - 16 t
-      const int lim = qi[qs] < q_len ? past + qi[qs] - k0 - 4 * qd : -1000;
+    any_grew |= softmax_max<kMask>(st, s, qs, alpha[qs], k0, qi, q_len, past, qd, masked);
+    softmax_exp(st, s, pb, qs, alpha[qs]);
+  }
+  return __any(any_grew);
+}
+
+template <int D, int QS>
+__device__ __forceinline__ void rescale_output(PfState<D, QS>& st, const float (&alpha)[QS]) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+  for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (16 * t + e > lim) s[qs][t][e] = -FLT_MAX;
-    }
-    float mt = -FLT_MAX;
+    for (int dt = 0; dt < D / 16; ++dt) st.o[qs][dt] *= alpha[qs];
+}
+
+// S^T of one tile for a wave's query sets: lane (qd, c16) gets the raw scores
+// of keys 16 t + 4 qd + e of its rows; each K fragment feeds every query set.
+// kfrag(t, ks): the A operand of subtile t (keys 16 t .. + 15 of the tile),
+// step ks (dims 32 ks .. + 31): lane (qd, c16) gets key 16 t + c16, dims
+// 32 ks + 8 qd .. + 7.
+template <int D, int QS, class KFrag>
+__device__ __forceinline__ void score_sub(f32x4 (&s)[QS][4], const f16x8 (&qb)[QS][D / 32], KFrag kfrag,
+                                          int t) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+  for (int qs = 0; qs < QS; ++qs) s[qs][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[qs][t][e]);
-    mt = rows_max<true>(rows_max<false>(mt));  // the 4 lanes of this query row
-    // The reference max moves only when the tile's max exceeds it by more
-    // than 2^8 in probability: below that, probabilities up to 256 are exact
-    // enough in fp16 and the output and sum need no rescale.
-    const float m_new = fmaxf(st.m_run[qs], mt);
-    const bool grew = (m_new - st.m_run[qs]) * c > 8.f;  // first valid tile: always
-    const float alpha = !grew ? 1.f
-                        : st.m_run[qs] == -FLT_MAX
-                            ? 0.f
-                            : __builtin_amdgcn_exp2f((st.m_run[qs] - m_new) * c);
-    if (grew) st.m_run[qs] = m_new;
-    const float mc = st.m_run[qs] * c;
-    float ts = 0.f;
+  for (int ks = 0; ks < D / 32; ++ks) {
+    const f16x8 ka = kfrag(t, ks);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
-        ts += s[qs][t][e];
-      }
-    ts = rows_sum<true>(rows_sum<false>(ts));
-    st.l_run[qs] = st.l_run[qs] * alpha + ts;
-    if (__any(grew)) {  // rescale only when some row's reference max moved
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) st.o[qs][dt] *= alpha;
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      pb[qs][j] = f16x8{static_cast<_Float16>(s[qs][2 * j][0]), static_cast<_Float16>(s[qs][2 * j][1]),
-                        static_cast<_Float16>(s[qs][2 * j][2]), static_cast<_Float16>(s[qs][2 * j][3]),
-                        static_cast<_Float16>(s[qs][2 * j + 1][0]), static_cast<_Float16>(s[qs][2 * j + 1][1]),
-                        static_cast<_Float16>(s[qs][2 * j + 1][2]), static_cast<_Float16>(s[qs][2 * j + 1][3])};
+    for (int qs = 0; qs < QS; ++qs)
+      s[qs][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[qs][ks], s[qs][t], 0, 0, 0);
   }
 }
 
-// One 64-key tile for a wave's query rows.  kfrag(t, ks): the A operand of
-// S^T subtile t (keys 16 t .. + 15 of the tile), step ks (dims 32 ks .. + 31):
-// lane (qd, c16) gets key 16 t + c16, dims 32 ks + 8 qd .. + 7.  vfrag(j, dt):
-// the A operand of O^T step j, dim tile dt: lane (qd, c16) gets dim 16 dt +
-// c16 of keys 32 j + 4 qd + e and then 32 j + 16 + 4 qd + e (e = 0..3).
-// vready(va) runs after the fragments of a step are requested and before the
-// MFMAs use them (a wait for reads the compiler does not track).
-// kSplitMask: separate code for masked and unmasked tiles.
+template <int D, int QS, class KFrag>
+__device__ __forceinline__ void score_tile(f32x4 (&s)[QS][4], const f16x8 (&qb)[QS][D / 32], KFrag kfrag) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) score_sub<D, QS>(s, qb, kfrag, t);
+}
+
+// The softmax of one tile (scores sc) interleaved with the scores of the
+// next (into sn): four sections, each one subtile of MFMAs beside one phase
+// of the softmax (max of set 0, exponentials of set 0, then set 1); the
+// scheduling barriers keep each section's registers bounded.
+template <int kMask, int D, class KFrag>
+__device__ __forceinline__ bool softmax_beside_scores(PfState<D, 2>& st, f32x4 (&sc)[2][4], f16x8 (&pb)[2][2],
+                                                      float (&alpha)[2], f32x4 (&sn)[2][4],
+                                                      const f16x8 (&qb)[2][D / 32], KFrag kf, int k0,
+                                                      const int (&qi)[2], int q_len, int past, int qd) {
+  bool grew = false;
+  score_sub<D, 2>(sn, qb, kf, 0);
+  grew |= softmax_max<kMask>(st, sc, 0, alpha[0], k0, qi, q_len, past, qd, true);
+  __builtin_amdgcn_sched_barrier(0);
+  score_sub<D, 2>(sn, qb, kf, 1);
+  softmax_exp(st, sc, pb, 0, alpha[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  score_sub<D, 2>(sn, qb, kf, 2);
+  grew |= softmax_max<kMask>(st, sc, 1, alpha[1], k0, qi, q_len, past, qd, true);
+  __builtin_amdgcn_sched_barrier(0);
+  score_sub<D, 2>(sn, qb, kf, 3);
+  softmax_exp(st, sc, pb, 1, alpha[1]);
+  return __any(grew);
+}
+
+// O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
+// (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands.
+// vfrag(j, dt) (j a compile-time constant): the A operand of step j, dim tile
+// dt: lane (qd, c16) gets dim 16 dt + c16 of those keys.  vready(va) runs
+// after a group of fragments is requested and before the MFMAs use them (a
+// wait for reads the compiler does not track).
+template <int D, int QS, class VFrag, class VReady>
+__device__ __forceinline__ void value_tile(PfState<D, QS>& st, const f16x8 (&pb)[QS][2], VFrag vfrag,
+                                           VReady vready) {
+  // fragments are requested kGroup dim tiles at a time (fewer live registers)
+  constexpr int kGroup = D == 128 ? 4 : D / 16;
+  auto step = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+#pragma unroll
+    for (int g = 0; g < D / 16; g += kGroup) {
+      f16x8 va[kGroup];
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i) va[i] = vfrag(jc, g + i);
+      vready(va);
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i)
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+          st.o[qs][g + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[i], pb[qs][j], st.o[qs][g + i], 0, 0, 0);
+    }
+  };
+  step(std::integral_constant<int, 0>{});
+  step(std::integral_constant<int, 1>{});
+}
+
+// One 64-key tile for a wave's query rows (score_tile, softmax_core,
+// value_tile).  kSplitMask: separate code for masked and unmasked tiles.
 template <int D, int QS, bool kSplitMask, class KFrag, class VFrag, class VReady>
 __device__ __forceinline__ void attend_tile(PfState<D, QS>& st, int k0, const f16x8 (&qb)[QS][D / 32],
                                             const int (&qi)[QS], int q_len, int past, int row0,
                                             int wave_rows, int qd, KFrag kfrag, VFrag vfrag,
                                             VReady vready) {
-  constexpr int kSteps = D / 32, kDTiles = D / 16;
-  // S^T for 4 subtiles of 16 keys: lane (qd, c16) gets keys k0 + 16 t + 4 qd + e of its
-  // rows; each K fragment read from LDS feeds every query set
   f32x4 s[QS][4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs) s[qs][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) {
-      const f16x8 ka = kfrag(t, ks);
-#pragma unroll
-      for (int qs = 0; qs < QS; ++qs)
-        s[qs][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[qs][ks], s[qs][t], 0, 0, 0);
-    }
-  }
+  score_tile<D, QS>(s, qb, kfrag);
   // masks only where the tile reaches past a row's position (the diagonal,
   // the context end) or the wave has rows past q_len
   f16x8 pb[QS][2];
+  float alpha[QS];
   const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < 16 * QS;
+  bool grew;
   if constexpr (kSplitMask) {
-    if (masked) softmax_tile<1>(st, s, pb, k0, qi, q_len, past, qd);
-    else softmax_tile<0>(st, s, pb, k0, qi, q_len, past, qd);
+    if (masked) grew = softmax_core<1>(st, s, pb, alpha, k0, qi, q_len, past, qd);
+    else grew = softmax_core<0>(st, s, pb, alpha, k0, qi, q_len, past, qd);
   } else {
-    softmax_tile<2>(st, s, pb, k0, qi, q_len, past, qd, masked);
+    grew = softmax_core<2>(st, s, pb, alpha, k0, qi, q_len, past, qd, masked);
   }
-  // O^T += V^T P^T over two 32-key steps; step j takes keys 32 j + 4 qd + e
-  // (subtile 2 j) then 32 j + 16 + 4 qd + e (subtile 2 j + 1) in both operands
-  // (j is passed to vfrag as a compile-time constant)
-  auto step = [&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    f16x8 va[kDTiles];
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) va[dt] = vfrag(jc, dt);
-    vready(va);
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt)
-#pragma unroll
-      for (int qs = 0; qs < QS; ++qs)
-        st.o[qs][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], pb[qs][j], st.o[qs][dt], 0, 0, 0);
-  };
-  step(std::integral_constant<int, 0>{});
-  step(std::integral_constant<int, 1>{});
+  if (grew) rescale_output(st, alpha);  // only when some row's reference max moved
+  value_tile<D, QS>(st, pb, vfrag, vready);
 }
 
 template <int D, bool kInt8>
@@ -433,7 +499,7 @@ prefill_attention_kernel(PrefillArgs a) {
           return *reinterpret_cast<const f16x8*>(
               &vt_lds[16 * dt + c16][vt_phys(16 * dt + c16, 32 * j + 8 * qd)]);
         },
-        [](f16x8(&)[D / 16]) {});
+        [](auto&) {});
   };
 
   const int ntiles = (kv_end + kBK - 1) / kBK;
@@ -461,7 +527,7 @@ prefill_attention_kernel(PrefillArgs a) {
 // slots.  The block table of the sequence is copied to LDS first so that
 // the loop issues no other global load (whose wait would also drain the
 // tiles in flight).
-constexpr int kDmaStages = 3;
+constexpr int kDmaStages = 4;
 constexpr int kDmaTableCap = 4096;  // block-table entries staged in LDS
 
 #define RLK_LDS __attribute__((address_space(3)))
@@ -545,16 +611,18 @@ prefill_dma_kernel(PrefillArgs a) {
     for (int ks = 0; ks < kSteps; ++ks) asm volatile("" : "+v"(qb[qs][ks]));
   __syncthreads();
 
-  // Each lane's piece u of a tile: key row r_u and 16-byte chunk c_u of the
-  // LDS image, fixed for the whole loop.
+  // Piece u of a tile for this lane: key row and 16-byte chunk of the LDS
+  // image (recomputed at each use: cheaper than holding registers).
   constexpr int kHalf = G::kOps / 2;
-  int lr[kHalf], lc[kHalf];
-#pragma unroll
-  for (int u = 0; u < kHalf; ++u) {
-    const int byte = (wave + G::kWaves * u) * 1024 + lane * 16;
-    lr[u] = byte / G::kRowBytes;
-    lc[u] = (byte % G::kRowBytes) / 16;
-  }
+  auto piece = [&](int u, int& r, int& c) {
+    // the lane index passes through an empty asm so that the compiler
+    // recomputes these few values per tile instead of keeping them live
+    int l16 = lane * 16;
+    asm volatile("" : "+v"(l16));
+    const int byte = (wave + G::kWaves * u) * 1024 + l16;
+    r = byte / G::kRowBytes;
+    c = (byte % G::kRowBytes) / 16;
+  };
   const unsigned char* kbase = static_cast<const unsigned char*>(p.kv.k);
   const unsigned char* vbase = static_cast<const unsigned char*>(p.kv.v);
   auto dma = [&](unsigned char* sb, int u, bool isv, const unsigned char* src) {
@@ -562,45 +630,40 @@ prefill_dma_kernel(PrefillArgs a) {
         src, (RLK_LDS void*)(sb + (isv ? G::kTileBytes : 0) + (wave + G::kWaves * u) * 1024), 16, 0, 0);
   };
   // Block sizes that are powers of two: a whole tile inside the context takes
-  // the block of each piece from a lane constant (row >> log2 bs) plus the
-  // tile's first block, and the byte offset inside the block from a lane
-  // constant plus the tile's offset into its block (non-zero for bs > 64).
+  // the block of each piece from its row (row >> log2 bs) plus the tile's
+  // first block, and the byte offset inside the block from the row plus the
+  // tile's offset into its block (non-zero for bs > 64).
   const bool pow2 = (bs & (bs - 1)) == 0;
   const int lbs = __builtin_ctz(bs);
   const uint32_t block_bytes = static_cast<uint32_t>(hkv) * bs * G::kRowBytes;
-  int lblk[kHalf];
-  uint32_t lk_off[kHalf], lv_off[kHalf];
-#pragma unroll
-  for (int u = 0; u < kHalf; ++u) {
-    const int r = lr[u];
-    lblk[u] = r >> lbs;
-    const uint32_t row_off = static_cast<uint32_t>(kvh * bs + (r & (bs - 1))) * G::kRowBytes;
-    lk_off[u] = row_off + ((lc[u] ^ G::kswz(r)) << 4);
-    lv_off[u] = row_off + ((lc[u] ^ G::vswz(r)) << 4);
-  }
+  const uint32_t head_bytes = static_cast<uint32_t>(kvh) * bs * G::kRowBytes;
   // keys past kv_end read the last key again: finite, and masked out of every row
   auto issue = [&](int tile, int stage) {
     const int k0 = tile * kBK;
     unsigned char* sb = pf_lds + stage * G::kStageBytes;
     if (pow2 && k0 + kBK <= kv_end) {
       const int blk0 = k0 >> lbs;
-      const uint32_t koff = static_cast<uint32_t>(k0 & (bs - 1)) * G::kRowBytes;
+      const uint32_t koff = head_bytes + static_cast<uint32_t>(k0 & (bs - 1)) * G::kRowBytes;
 #pragma unroll
       for (int u = 0; u < kHalf; ++u) {
-        const uint64_t bb = static_cast<uint64_t>(static_cast<uint32_t>(tab_lds[blk0 + lblk[u]])) * block_bytes;
-        dma(sb, u, false, kbase + bb + (lk_off[u] + koff));
-        dma(sb, u, true, vbase + bb + (lv_off[u] + koff));
+        int r, c;
+        piece(u, r, c);
+        const uint64_t bb = static_cast<uint64_t>(static_cast<uint32_t>(tab_lds[blk0 + (r >> lbs)])) * block_bytes;
+        const uint32_t row_off = koff + static_cast<uint32_t>(r & (bs - 1)) * G::kRowBytes;
+        dma(sb, u, false, kbase + bb + (row_off + ((c ^ G::kswz(r)) << 4)));
+        dma(sb, u, true, vbase + bb + (row_off + ((c ^ G::vswz(r)) << 4)));
       }
       return;
     }
 #pragma unroll
     for (int u = 0; u < kHalf; ++u) {
-      const int r = lr[u];
+      int r, c;
+      piece(u, r, c);
       const int pos = min(k0 + r, kv_end - 1);
       const int blk = pos / bs, off = pos - blk * bs;
       const size_t cell = (static_cast<size_t>(tab_lds[blk]) * hkv + kvh) * bs + off;
-      dma(sb, u, false, kbase + cell * G::kRowBytes + ((lc[u] ^ G::kswz(r)) << 4));
-      dma(sb, u, true, vbase + cell * G::kRowBytes + ((lc[u] ^ G::vswz(r)) << 4));
+      dma(sb, u, false, kbase + cell * G::kRowBytes + ((c ^ G::kswz(r)) << 4));
+      dma(sb, u, true, vbase + cell * G::kRowBytes + ((c ^ G::vswz(r)) << 4));
     }
   };
 
@@ -608,58 +671,90 @@ prefill_dma_kernel(PrefillArgs a) {
   // transposing V reads: lane (qd, c16) reads key row 4 qd + tk (+ 32 j, + 16)
   // at dims 16 dt + 4 tm; byte offsets inside a V tile, for j = 0
   const int tk = c16 >> 2, tm = c16 & 3;
-  uint32_t vrd[D / 16];
+  // D = 128: dim tile dt + 4 sits at chunk pair (dt ^ sw) ^ 4, byte offset
+  // ^ 128 of dt's (row offsets are multiples of 256), so 4 offsets are kept
+  constexpr int kVrd = D == 128 ? 4 : D / 16;
+  uint32_t vrd[kVrd];
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) {
+  for (int dt = 0; dt < kVrd; ++dt) {
     const int row = 4 * qd + tk;  // row + 32 j and row + 16 share its swizzle
     vrd[dt] = row * G::kRowBytes + ((((2 * dt + (tm >> 1)) ^ G::vswz(row)) << 4) | ((tm & 1) << 3));
   }
-  auto compute = [&](int k0, int stage) {
+  auto kfrag = [&](int stage) {
     const unsigned char* kt = pf_lds + stage * G::kStageBytes;
-    const uint32_t vt_addr = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((RLK_LDS const unsigned char*)(kt + G::kTileBytes)));
-    attend_tile<D, kQS, true>(
-        stt, k0, qb, qi, q_len, past, row0, wave_rows, qd,
-        [&](int t, int ks) {
-          const int row = 16 * t + c16;
-          return *reinterpret_cast<const f16x8*>(kt + row * G::kRowBytes +
-                                                 (((4 * ks + qd) ^ G::kswz(c16)) << 4));
-        },
-        [&](auto jc, int dt) {
-          // the transposing reads are issued as inline asm: the compiler's
-          // own form of them waits for every load-to-LDS in flight
-          constexpr int kOff = 32 * decltype(jc)::value * G::kRowBytes;
-          const uint32_t addr = vt_addr + vrd[dt];
-          u32x2 lo, hi;
-          asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
-                       : "=v"(lo), "=v"(hi)
-                       : "v"(addr), "n"(kOff), "n"(kOff + 16 * G::kRowBytes));
-          return __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        },
-        [](f16x8(&va)[D / 16]) {
-          if constexpr (D == 128)
-            asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]), "+v"(va[4]),
-                           "+v"(va[5]), "+v"(va[6]), "+v"(va[7]));
-          else
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]));
-        });
+    return [kt, c16, qd](int t, int ks) {
+      const int row = 16 * t + c16;
+      return *reinterpret_cast<const f16x8*>(kt + row * G::kRowBytes + (((4 * ks + qd) ^ G::kswz(c16)) << 4));
+    };
+  };
+  auto vfrag = [&](int stage) {
+    const uint32_t vt_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+        (RLK_LDS const unsigned char*)(pf_lds + stage * G::kStageBytes + G::kTileBytes)));
+    return [vt_addr, &vrd](auto jc, int dt) {
+      // the transposing reads are issued as inline asm: the compiler's own
+      // form of them waits for every load-to-LDS in flight
+      constexpr int kOff = 32 * decltype(jc)::value * G::kRowBytes;
+      const uint32_t addr = vt_addr + (dt < kVrd ? vrd[dt] : vrd[dt - kVrd] ^ 128u);
+      u32x2 lo, hi;
+      asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                   : "=v"(lo), "=v"(hi)
+                   : "v"(addr), "n"(kOff), "n"(kOff + 16 * G::kRowBytes));
+      return __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+    };
+  };
+  auto vready = [](f16x8(&va)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]));
   };
 
+  // Software pipeline over the tiles: the scores of tile t + 1 (MFMA) are
+  // computed in the same straight-line code as the softmax of tile t (VALU),
+  // so the matrix cores and the vector ALU of a wave overlap.  Four LDS
+  // stages: tiles t and t + 1 resident, t + 2 and t + 3 in flight.
   const int ntiles = (kv_end + kBK - 1) / kBK;
+  const int wtiles = (wave_kv_end + kBK - 1) / kBK;  // tiles this wave attends
   issue(0, 0);
   if (ntiles > 1) issue(1, 1);
-  for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) wait_vmem<G::kOps>();
+  if (ntiles > 2) issue(2, 2);
+  if (ntiles > 2) wait_vmem<2 * G::kOps>();
+  else if (ntiles > 1) wait_vmem<G::kOps>();
+  else wait_vmem<0>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  f32x4 s_even[kQS][4], s_odd[kQS][4];
+  if (wtiles > 0) score_tile<D, kQS>(s_even, qb, kfrag(0));
+
+  auto body = [&](int t, f32x4(&sc)[kQS][4], f32x4(&sn)[kQS][4]) {
+    // tile t + 1 in LDS for every wave; tile t - 1 consumed (its stage takes
+    // tile t + 3).  A bare barrier: __syncthreads() would also drain the
+    // tiles still in flight.
+    if (t + 2 < ntiles) wait_vmem<G::kOps>();
     else wait_vmem<0>();
-    // tile t is in LDS for every wave; tile t - 1 is consumed (its LDS reads
-    // fed MFMAs before this point).  A bare barrier: __syncthreads() would
-    // also drain the tiles still in flight.
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (t + 2 < ntiles) issue(t + 2, (t + 2) % kDmaStages);
-    if (t * kBK < wave_kv_end) compute(t * kBK, t % kDmaStages);
+    if (t + 3 < ntiles) issue(t + 3, (t + 3) % kDmaStages);
+    if (t >= wtiles) return;
+    const int k0 = t * kBK;
+    const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < kWaveRows;
+    f16x8 pb[kQS][2];
+    float alpha[kQS];
+    bool grew;
+    if (t + 1 < wtiles) {
+      const auto kf = kfrag((t + 1) % kDmaStages);
+      grew = masked ? softmax_beside_scores<1>(stt, sc, pb, alpha, sn, qb, kf, k0, qi, q_len, past, qd)
+                    : softmax_beside_scores<0>(stt, sc, pb, alpha, sn, qb, kf, k0, qi, q_len, past, qd);
+    } else {
+      grew = masked ? softmax_core<1>(stt, sc, pb, alpha, k0, qi, q_len, past, qd)
+                    : softmax_core<0>(stt, sc, pb, alpha, k0, qi, q_len, past, qd);
+    }
+    if (grew) rescale_output(stt, alpha);
+    value_tile<D, kQS>(stt, pb, vfrag(t % kDmaStages), vready);
+  };
+  int t = 0;
+  for (; t + 1 < ntiles; t += 2) {
+    body(t, s_even, s_odd);
+    body(t + 1, s_odd, s_even);
   }
+  if (t < ntiles) body(t, s_even, s_odd);
 
   stt.store(p, q0, qi, q_len, h, qd);
 }
