@@ -166,8 +166,9 @@ struct PfState {
                         int qd) const {
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
+      const float l = rows_sum<true>(rows_sum<false>(l_run[qs]));  // the 4 lanes of the row
       if (qi[qs] >= q_len) continue;
-      const float inv = l_run[qs] > 0.f ? 1.f / l_run[qs] : 0.f;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
       uint16_t* out = p.out + static_cast<size_t>(q0 + qi[qs]) * p.num_heads * D + h * D + 4 * qd;
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
@@ -230,7 +231,7 @@ __device__ __forceinline__ void softmax_exp(PfState<D, QS>& st, f32x4 (&s)[QS][4
       s[qs][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qs][t][e], c, -mc));  // masked: 2^-huge = 0
       ts += s[qs][t][e];
     }
-  ts = rows_sum<true>(rows_sum<false>(ts));
+  // the sum stays per lane (its keys of the row); store() adds the 4 lanes
   st.l_run[qs] = st.l_run[qs] * alpha + ts;
 #pragma unroll
   for (int j = 0; j < 2; ++j)
@@ -379,7 +380,10 @@ prefill_attention_kernel(PrefillArgs a) {
   const rlk_attention_params& p = a.p;
   const rlk_prefill_attention_work& w = a.w;
   const int h = blockIdx.y;
-  const int seq = w.seq_ids[blockIdx.z];
+  // sequences in reverse dispatch order: in a chunked-prefill batch the later
+  // chunks usually sit deeper in their sequences (more keys), so the longest
+  // workgroups start first
+  const int seq = w.seq_ids[gridDim.z - 1 - blockIdx.z];
   const int q_len = w.q_len[seq];
   // query tiles in reverse dispatch order: the last rows have the most keys,
   // so the longest workgroups start first and the causal tail is short
@@ -571,7 +575,10 @@ prefill_dma_kernel(PrefillArgs a) {
   const rlk_attention_params& p = a.p;
   const rlk_prefill_attention_work& w = a.w;
   const int h = blockIdx.y;
-  const int seq = w.seq_ids[blockIdx.z];
+  // sequences in reverse dispatch order: in a chunked-prefill batch the later
+  // chunks usually sit deeper in their sequences (more keys), so the longest
+  // workgroups start first
+  const int seq = w.seq_ids[gridDim.z - 1 - blockIdx.z];
   const int q_len = w.q_len[seq];
   const int qt = (q_len + kBQ - 1) / kBQ - 1 - static_cast<int>(blockIdx.x);
   if (qt < 0) return;  // workgroup-uniform
@@ -611,18 +618,14 @@ prefill_dma_kernel(PrefillArgs a) {
     for (int ks = 0; ks < kSteps; ++ks) asm volatile("" : "+v"(qb[qs][ks]));
   __syncthreads();
 
-  // Piece u of a tile for this lane: key row and 16-byte chunk of the LDS
-  // image (recomputed at each use: cheaper than holding registers).
+  // Piece u of a tile for this lane: key row r0 + 32 u (each wave
+  // instruction covers 1 KiB, the waves together 32 rows) and 16-byte chunk
+  // c of the LDS image; the swizzles of r0 + 32 u equal those of r0.
   constexpr int kHalf = G::kOps / 2;
-  auto piece = [&](int u, int& r, int& c) {
-    // the lane index passes through an empty asm so that the compiler
-    // recomputes these few values per tile instead of keeping them live
-    int l16 = lane * 16;
-    asm volatile("" : "+v"(l16));
-    const int byte = (wave + G::kWaves * u) * 1024 + l16;
-    r = byte / G::kRowBytes;
-    c = (byte % G::kRowBytes) / 16;
-  };
+  static_assert(G::kWaves * 1024 == 32 * G::kRowBytes, "32 rows per round of pieces");
+  const int r0 = (wave * 1024 + lane * 16) / G::kRowBytes;
+  const int cx = ((wave * 1024 + lane * 16) % G::kRowBytes) / 16;
+  const int kx0 = (cx ^ G::kswz(r0)) << 4, vx0 = (cx ^ G::vswz(r0)) << 4;
   const unsigned char* kbase = static_cast<const unsigned char*>(p.kv.k);
   const unsigned char* vbase = static_cast<const unsigned char*>(p.kv.v);
   auto dma = [&](unsigned char* sb, int u, bool isv, const unsigned char* src) {
@@ -641,29 +644,30 @@ prefill_dma_kernel(PrefillArgs a) {
   auto issue = [&](int tile, int stage) {
     const int k0 = tile * kBK;
     unsigned char* sb = pf_lds + stage * G::kStageBytes;
+    // the lane constants pass through an empty asm so that the compiler
+    // derives the addresses per tile instead of keeping them all live
+    int r = r0, kx = kx0, vx = vx0;
+    asm volatile("" : "+v"(r), "+v"(kx), "+v"(vx));
     if (pow2 && k0 + kBK <= kv_end) {
       const int blk0 = k0 >> lbs;
       const uint32_t koff = head_bytes + static_cast<uint32_t>(k0 & (bs - 1)) * G::kRowBytes;
 #pragma unroll
       for (int u = 0; u < kHalf; ++u) {
-        int r, c;
-        piece(u, r, c);
-        const uint64_t bb = static_cast<uint64_t>(static_cast<uint32_t>(tab_lds[blk0 + (r >> lbs)])) * block_bytes;
-        const uint32_t row_off = koff + static_cast<uint32_t>(r & (bs - 1)) * G::kRowBytes;
-        dma(sb, u, false, kbase + bb + (row_off + ((c ^ G::kswz(r)) << 4)));
-        dma(sb, u, true, vbase + bb + (row_off + ((c ^ G::vswz(r)) << 4)));
+        const int ru = r + 32 * u;
+        const uint64_t bb = static_cast<uint64_t>(static_cast<uint32_t>(tab_lds[blk0 + (ru >> lbs)])) * block_bytes;
+        const uint32_t row_off = koff + static_cast<uint32_t>(ru & (bs - 1)) * G::kRowBytes;
+        dma(sb, u, false, kbase + bb + (row_off + kx));
+        dma(sb, u, true, vbase + bb + (row_off + vx));
       }
       return;
     }
 #pragma unroll
     for (int u = 0; u < kHalf; ++u) {
-      int r, c;
-      piece(u, r, c);
-      const int pos = min(k0 + r, kv_end - 1);
+      const int pos = min(k0 + r + 32 * u, kv_end - 1);
       const int blk = pos / bs, off = pos - blk * bs;
       const size_t cell = (static_cast<size_t>(tab_lds[blk]) * hkv + kvh) * bs + off;
-      dma(sb, u, false, kbase + cell * G::kRowBytes + ((c ^ G::kswz(r)) << 4));
-      dma(sb, u, true, vbase + cell * G::kRowBytes + ((c ^ G::vswz(r)) << 4));
+      dma(sb, u, false, kbase + cell * G::kRowBytes + kx);
+      dma(sb, u, true, vbase + cell * G::kRowBytes + vx);
     }
   };
 
