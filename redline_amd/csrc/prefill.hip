@@ -519,40 +519,56 @@ prefill_attention_kernel(PrefillArgs a) {
   stt.store(p, q0, qi, q_len, h, qd);
 }
 
-// FP16 cache: tiles go from HBM to LDS by the load-to-LDS path (no register
-// staging, no VGPRs held by loads in flight), three stages with two tiles in
-// flight while the third is consumed.  Each wave instruction writes 1 KiB of
-// LDS contiguously, 16 bytes per lane, so the layouts are swizzled on the
-// source side: LDS chunk c (16 bytes) of key row r holds K chunk c ^ kswz(r)
-// and V chunk c ^ vswz(r).  The swizzles make every LDS read conflict-free
-// with 64 banks of 4 bytes: a 16-byte K read covers 16 key rows at 16
-// distinct 16-byte slots of 256 bytes, and a transposing V read
-// (ds_read_tr16_b64, 8 bytes a lane) covers 8 key rows at 8 distinct 32-byte
-// slots.  The block table of the sequence is copied to LDS first so that
-// the loop issues no other global load (whose wait would also drain the
-// tiles in flight).
+// Caches read by the load-to-LDS path (no register staging, no VGPRs held by
+// loads in flight): four raw LDS stages, tiles t + 2 and t + 3 in flight while
+// t and t + 1 are used.  Each wave instruction writes 1 KiB of LDS
+// contiguously, 16 bytes per lane.
+//   FP16: the raw stage is the MFMA operand image.  Its layouts are swizzled
+//     on the source side: LDS chunk c (16 bytes) of key row r holds K chunk
+//     c ^ kswz(r) and V chunk c ^ vswz(r).  The swizzles make every LDS read
+//     conflict-free with 64 banks of 4 bytes: a 16-byte K read covers 16 key
+//     rows at 16 distinct 16-byte slots of 256 bytes, and a transposing V
+//     read (ds_read_tr16_b64, 8 bytes a lane) covers 8 key rows at 8 distinct
+//     32-byte slots.
+//   INT8: the raw stage holds the codes row-major and the 64 K and 64 V
+//     scales (one dword per key, loaded by 4-byte load-to-LDS; fp16 scales
+//     take the dword that holds them).  The workgroup dequantises tile t + 1
+//     into one of two fp16 images of the FP16 layout, fp16(float(code) *
+//     scale) as attention.cu:266-274, before the scores of t + 1 need it.
+// The block table of the sequence is copied to LDS first so that the loop
+// issues no other global load (whose wait would also drain the tiles in
+// flight).
 constexpr int kDmaStages = 4;
 constexpr int kDmaTableCap = 4096;  // block-table entries staged in LDS
 
 #define RLK_LDS __attribute__((address_space(3)))
 
-template <int D>
+template <int D, bool kInt8>
 struct PfDma {
   static constexpr int kBQ = PfShape<D, false>::kBQ;
-  static constexpr int kRowBytes = 2 * D;
-  static constexpr int kTileBytes = kBK * kRowBytes;  // one K or V tile
-  static constexpr int kStageBytes = 2 * kTileBytes;
   static constexpr int kThreads = PfShape<D, false>::kThreads;
   static constexpr int kWaves = kThreads / 64;
-  static constexpr int kOpsPerTile = kTileBytes / 1024;
-  static constexpr int kOps = 2 * kOpsPerTile / kWaves;  // instructions per wave per stage
-  static_assert(kOpsPerTile % kWaves == 0, "whole instructions per wave");
+  static constexpr int kRowBytes = 2 * D;             // fp16 image
+  static constexpr int kTileBytes = kBK * kRowBytes;  // one fp16 K or V tile
+  static constexpr int kRawRow = kInt8 ? D : 2 * D;   // cache row
+  static constexpr int kRawTile = kBK * kRawRow;
+  static constexpr int kScaleOff = 2 * kRawTile;      // INT8: K scales, then V scales
+  static constexpr int kStageBytes = 2 * kRawTile + (kInt8 ? 2 * 4 * kBK : 0);
+  static constexpr int kImageOff = kDmaStages * kStageBytes;  // INT8: two fp16 images
+  static constexpr int kImages = kInt8 ? 2 : 0;
+  static constexpr int kTableOff = kImageOff + kImages * 2 * kTileBytes;
+  static constexpr int kPieces = kRawTile / 1024 / kWaves;  // 1 KiB pieces per wave per tile (K or V)
+  static_assert(kRawTile % (1024 * kWaves) == 0, "whole instructions per wave");
+  static_assert(kPieces == 1 || kWaves * 1024 == 32 * kRawRow, "32 rows per round of pieces");
+  // instructions a wave issues per tile (INT8: waves 0 and 1 also load the scales)
+  static constexpr int kOps = 2 * kPieces;
+  static constexpr int kOpsScales = kOps + (kInt8 ? 1 : 0);
   // row pitch 256 bytes (D = 128): 16 slots a row; 128 bytes (D = 64): a
   // 256-byte span holds rows r and r ^ 1
   __device__ static int kswz(int r) { return D == 128 ? r & 15 : (r >> 1) & 7; }
   __device__ static int vswz(int r) { return D == 128 ? (r & 7) << 1 : ((r >> 1) & 3) << 1; }
   static size_t lds_bytes(int table_entries) {
-    return static_cast<size_t>(kDmaStages) * kStageBytes + 4 * ((table_entries + 3) & ~3);
+    return static_cast<size_t>(kTableOff) + 4 * ((table_entries + 3) & ~3);
   }
 };
 
@@ -563,14 +579,14 @@ __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int D>
+template <int D, bool kInt8>
 __global__ __launch_bounds__((PfShape<D, false>::kThreads), (PfShape<D, false>::kWavesPerSimd)) void
 prefill_dma_kernel(PrefillArgs a) {
-  using G = PfDma<D>;
+  using G = PfDma<D, kInt8>;
   constexpr int kQS = PfShape<D, false>::kQS, kBQ = PfShape<D, false>::kBQ;
   constexpr int kSteps = D / 32, kWaveRows = 16 * kQS;
   extern __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[];
-  int32_t* tab_lds = reinterpret_cast<int32_t*>(pf_lds + kDmaStages * G::kStageBytes);
+  int32_t* tab_lds = reinterpret_cast<int32_t*>(pf_lds + G::kTableOff);
 
   const rlk_attention_params& p = a.p;
   const rlk_prefill_attention_work& w = a.w;
@@ -621,16 +637,14 @@ prefill_dma_kernel(PrefillArgs a) {
   // Piece u of a tile for this lane: key row r0 + 32 u (each wave
   // instruction covers 1 KiB, the waves together 32 rows) and 16-byte chunk
   // c of the LDS image; the swizzles of r0 + 32 u equal those of r0.
-  constexpr int kHalf = G::kOps / 2;
-  static_assert(G::kWaves * 1024 == 32 * G::kRowBytes, "32 rows per round of pieces");
-  const int r0 = (wave * 1024 + lane * 16) / G::kRowBytes;
-  const int cx = ((wave * 1024 + lane * 16) % G::kRowBytes) / 16;
-  const int kx0 = (cx ^ G::kswz(r0)) << 4, vx0 = (cx ^ G::vswz(r0)) << 4;
+  const int r0 = (wave * 1024 + lane * 16) / G::kRawRow;
+  const int cx = ((wave * 1024 + lane * 16) % G::kRawRow) / 16;
+  const int kx0 = (kInt8 ? cx : cx ^ G::kswz(r0)) << 4, vx0 = (kInt8 ? cx : cx ^ G::vswz(r0)) << 4;
   const unsigned char* kbase = static_cast<const unsigned char*>(p.kv.k);
   const unsigned char* vbase = static_cast<const unsigned char*>(p.kv.v);
   auto dma = [&](unsigned char* sb, int u, bool isv, const unsigned char* src) {
     __builtin_amdgcn_global_load_lds(
-        src, (RLK_LDS void*)(sb + (isv ? G::kTileBytes : 0) + (wave + G::kWaves * u) * 1024), 16, 0, 0);
+        src, (RLK_LDS void*)(sb + (isv ? G::kRawTile : 0) + (wave + G::kWaves * u) * 1024), 16, 0, 0);
   };
   // Block sizes that are powers of two: a whole tile inside the context takes
   // the block of each piece from its row (row >> log2 bs) plus the tile's
@@ -638,36 +652,96 @@ prefill_dma_kernel(PrefillArgs a) {
   // tile's offset into its block (non-zero for bs > 64).
   const bool pow2 = (bs & (bs - 1)) == 0;
   const int lbs = __builtin_ctz(bs);
-  const uint32_t block_bytes = static_cast<uint32_t>(hkv) * bs * G::kRowBytes;
-  const uint32_t head_bytes = static_cast<uint32_t>(kvh) * bs * G::kRowBytes;
+  const uint32_t block_bytes = static_cast<uint32_t>(hkv) * bs * G::kRawRow;
+  const uint32_t head_bytes = static_cast<uint32_t>(kvh) * bs * G::kRawRow;
   // keys past kv_end read the last key again: finite, and masked out of every row
   auto issue = [&](int tile, int stage) {
     const int k0 = tile * kBK;
     unsigned char* sb = pf_lds + stage * G::kStageBytes;
+    if constexpr (kInt8) {
+      // waves 0 and 1: the K and V scales of the tile's 64 keys, one per lane
+      if (wave < 2) {
+        const int pos = min(k0 + lane, kv_end - 1);
+        const int blk = pos / bs, off = pos - blk * bs;
+        const size_t cell = (static_cast<size_t>(tab_lds[blk]) * hkv + kvh) * bs + off;
+        const unsigned char* sbase = reinterpret_cast<const unsigned char*>(wave == 0 ? p.kv.k_scale : p.kv.v_scale);
+        const unsigned char* src = a.scale16 ? sbase + ((cell * 2) & ~size_t{3}) : sbase + cell * 4;
+        __builtin_amdgcn_global_load_lds(src, (RLK_LDS void*)(sb + G::kScaleOff + wave * 4 * kBK), 4, 0, 0);
+      }
+    }
     // the lane constants pass through an empty asm so that the compiler
     // derives the addresses per tile instead of keeping them all live
     int r = r0, kx = kx0, vx = vx0;
     asm volatile("" : "+v"(r), "+v"(kx), "+v"(vx));
     if (pow2 && k0 + kBK <= kv_end) {
       const int blk0 = k0 >> lbs;
-      const uint32_t koff = head_bytes + static_cast<uint32_t>(k0 & (bs - 1)) * G::kRowBytes;
+      const uint32_t koff = head_bytes + static_cast<uint32_t>(k0 & (bs - 1)) * G::kRawRow;
 #pragma unroll
-      for (int u = 0; u < kHalf; ++u) {
+      for (int u = 0; u < G::kPieces; ++u) {
         const int ru = r + 32 * u;
         const uint64_t bb = static_cast<uint64_t>(static_cast<uint32_t>(tab_lds[blk0 + (ru >> lbs)])) * block_bytes;
-        const uint32_t row_off = koff + static_cast<uint32_t>(ru & (bs - 1)) * G::kRowBytes;
+        const uint32_t row_off = koff + static_cast<uint32_t>(ru & (bs - 1)) * G::kRawRow;
         dma(sb, u, false, kbase + bb + (row_off + kx));
         dma(sb, u, true, vbase + bb + (row_off + vx));
       }
       return;
     }
 #pragma unroll
-    for (int u = 0; u < kHalf; ++u) {
+    for (int u = 0; u < G::kPieces; ++u) {
       const int pos = min(k0 + r + 32 * u, kv_end - 1);
       const int blk = pos / bs, off = pos - blk * bs;
       const size_t cell = (static_cast<size_t>(tab_lds[blk]) * hkv + kvh) * bs + off;
-      dma(sb, u, false, kbase + cell * G::kRowBytes + kx);
-      dma(sb, u, true, vbase + cell * G::kRowBytes + vx);
+      dma(sb, u, false, kbase + cell * G::kRawRow + kx);
+      dma(sb, u, true, vbase + cell * G::kRawRow + vx);
+    }
+  };
+  // wait until the tile issued `later` tiles before the newest has landed
+  auto wait_tiles = [&](int later) {
+    if (later >= 2) {
+      if (kInt8 && wave < 2) wait_vmem<2 * G::kOpsScales>();
+      else wait_vmem<2 * G::kOps>();
+    } else if (later == 1) {
+      if (kInt8 && wave < 2) wait_vmem<G::kOpsScales>();
+      else wait_vmem<G::kOps>();
+    } else {
+      wait_vmem<0>();
+    }
+  };
+  // the fp16 operand image of tile t: the raw stage (FP16) or one of two
+  // dequantised images (INT8)
+  auto image = [&](int t) -> unsigned char* {
+    if constexpr (kInt8) return pf_lds + G::kImageOff + (t & 1) * 2 * G::kTileBytes;
+    else return pf_lds + (t % kDmaStages) * G::kStageBytes;
+  };
+  // INT8: dequantise raw stage t into image(t); each thread takes 16-byte
+  // chunks of 8 codes, fp16 writes in the FP16 layout (swizzled)
+  auto dequant = [&](int t) {
+    if constexpr (kInt8) {
+      const unsigned char* sb = pf_lds + (t % kDmaStages) * G::kStageBytes;
+      unsigned char* img = image(t);
+      const float* sc = reinterpret_cast<const float*>(sb + G::kScaleOff);
+      constexpr int kChunks = kBK * D / 8;  // of K, and of V
+      static_assert(kChunks % G::kThreads == 0, "whole chunks per thread");
+      int me = tid;  // through an empty asm: addresses derived per tile, not kept live
+      asm volatile("" : "+v"(me));
+#pragma unroll
+      for (int u = 0; u < 2 * kChunks / G::kThreads; ++u) {
+        const bool isv = u >= kChunks / G::kThreads;
+        const int j = me + G::kThreads * u - (isv ? kChunks : 0);
+        const int r = j / (D / 8), c = j % (D / 8);
+        const u32x2 codes = *reinterpret_cast<const u32x2*>(sb + (isv ? G::kRawTile : 0) + r * D + c * 8);
+        float s = sc[(isv ? kBK : 0) + r];
+        if (a.scale16) {
+          // the dword holds the cells 2i and 2i + 1; the key's cell parity is
+          // its position's (even block size)
+          const uint32_t bits = __builtin_bit_cast(uint32_t, s);
+          const int pos = min(t * kBK + r, kv_end - 1);
+          s = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits >> (16 * (pos & 1)))));
+        }
+        const int sw = isv ? G::vswz(r) : G::kswz(r);
+        *reinterpret_cast<f16x8*>(img + (isv ? G::kTileBytes : 0) + r * G::kRowBytes + ((c ^ sw) << 4)) =
+            dequant8<true>(codes, s);
+      }
     }
   };
 
@@ -684,21 +758,29 @@ prefill_dma_kernel(PrefillArgs a) {
     const int row = 4 * qd + tk;  // row + 32 j and row + 16 share its swizzle
     vrd[dt] = row * G::kRowBytes + ((((2 * dt + (tm >> 1)) ^ G::vswz(row)) << 4) | ((tm & 1) << 3));
   }
-  auto kfrag = [&](int stage) {
-    const unsigned char* kt = pf_lds + stage * G::kStageBytes;
+  auto kfrag = [&](int t) {
+    const unsigned char* kt = image(t);
     return [kt, c16, qd](int t, int ks) {
       const int row = 16 * t + c16;
       return *reinterpret_cast<const f16x8*>(kt + row * G::kRowBytes + (((4 * ks + qd) ^ G::kswz(c16)) << 4));
     };
   };
-  auto vfrag = [&](int stage) {
-    const uint32_t vt_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-        (RLK_LDS const unsigned char*)(pf_lds + stage * G::kStageBytes + G::kTileBytes)));
-    return [vt_addr, &vrd](auto jc, int dt) {
+  auto vfrag = [&](int t) {
+    const uint32_t vt_addr = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((RLK_LDS const unsigned char*)(image(t) + G::kTileBytes)));
+    // the offsets pass through an empty asm so that the compiler adds them
+    // to this tile's base here instead of keeping every sum live
+    uint32_t vo[kVrd];
+#pragma unroll
+    for (int i = 0; i < kVrd; ++i) {
+      vo[i] = vrd[i];
+      asm volatile("" : "+v"(vo[i]));
+    }
+    return [vt_addr, vo](auto jc, int dt) {
       // the transposing reads are issued as inline asm: the compiler's own
       // form of them waits for every load-to-LDS in flight
       constexpr int kOff = 32 * decltype(jc)::value * G::kRowBytes;
-      const uint32_t addr = vt_addr + (dt < kVrd ? vrd[dt] : vrd[dt - kVrd] ^ 128u);
+      const uint32_t addr = vt_addr + (dt < kVrd ? vo[dt] : vo[dt - kVrd] ^ 128u);
       u32x2 lo, hi;
       asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
                    : "=v"(lo), "=v"(hi)
@@ -709,33 +791,43 @@ prefill_dma_kernel(PrefillArgs a) {
   auto vready = [](f16x8(&va)[4]) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]));
   };
+  // the image's LDS writes are complete (a bare barrier does not wait)
+  auto lds_written = []() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+  // a bare barrier: __syncthreads() would also drain the tiles in flight
+  auto barrier = []() {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
 
   // Software pipeline over the tiles: the scores of tile t + 1 (MFMA) are
   // computed in the same straight-line code as the softmax of tile t (VALU),
-  // so the matrix cores and the vector ALU of a wave overlap.  Four LDS
-  // stages: tiles t and t + 1 resident, t + 2 and t + 3 in flight.
+  // so the matrix cores and the vector ALU of a wave overlap.
   const int ntiles = (kv_end + kBK - 1) / kBK;
   const int wtiles = (wave_kv_end + kBK - 1) / kBK;  // tiles this wave attends
   issue(0, 0);
   if (ntiles > 1) issue(1, 1);
   if (ntiles > 2) issue(2, 2);
-  if (ntiles > 2) wait_vmem<2 * G::kOps>();
-  else if (ntiles > 1) wait_vmem<G::kOps>();
-  else wait_vmem<0>();
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  wait_tiles(min(ntiles, 3) - 1);
+  barrier();
+  if constexpr (kInt8) {
+    dequant(0);
+    lds_written();
+    barrier();
+  }
   f32x4 s_even[kQS][4], s_odd[kQS][4];
   if (wtiles > 0) score_tile<D, kQS>(s_even, qb, kfrag(0));
 
   auto body = [&](int t, f32x4(&sc)[kQS][4], f32x4(&sn)[kQS][4]) {
-    // tile t + 1 in LDS for every wave; tile t - 1 consumed (its stage takes
-    // tile t + 3).  A bare barrier: __syncthreads() would also drain the
-    // tiles still in flight.
-    if (t + 2 < ntiles) wait_vmem<G::kOps>();
-    else wait_vmem<0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    // raw tile t + 1 in LDS for every wave; tile t - 1 consumed (its raw
+    // stage takes tile t + 3, INT8: its image takes tile t + 1)
+    wait_tiles(t + 2 < ntiles ? 1 : 0);
+    barrier();
     if (t + 3 < ntiles) issue(t + 3, (t + 3) % kDmaStages);
+    if constexpr (kInt8) {
+      if (t + 1 < ntiles) dequant(t + 1);
+      lds_written();
+      barrier();
+    }
     if (t >= wtiles) return;
     const int k0 = t * kBK;
     const bool masked = k0 + kBK - 1 > past + row0 || wave_rows < kWaveRows;
@@ -743,7 +835,7 @@ prefill_dma_kernel(PrefillArgs a) {
     float alpha[kQS];
     bool grew;
     if (t + 1 < wtiles) {
-      const auto kf = kfrag((t + 1) % kDmaStages);
+      const auto kf = kfrag(t + 1);
       grew = masked ? softmax_beside_scores<1>(stt, sc, pb, alpha, sn, qb, kf, k0, qi, q_len, past, qd)
                     : softmax_beside_scores<0>(stt, sc, pb, alpha, sn, qb, kf, k0, qi, q_len, past, qd);
     } else {
@@ -751,7 +843,7 @@ prefill_dma_kernel(PrefillArgs a) {
                     : softmax_core<0>(stt, sc, pb, alpha, k0, qi, q_len, past, qd);
     }
     if (grew) rescale_output(stt, alpha);
-    value_tile<D, kQS>(stt, pb, vfrag(t % kDmaStages), vready);
+    value_tile<D, kQS>(stt, pb, vfrag(t), vready);
   };
   int t = 0;
   for (; t + 1 < ntiles; t += 2) {
@@ -791,13 +883,16 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
     const dim3 grid((rows + S::kBQ - 1) / S::kBQ, p.num_heads, w.num_seqs);
     kernel<<<grid, S::kThreads, 0, stream>>>(a);
   };
-  // FP16 caches take the load-to-LDS kernel when the block table fits its LDS
-  // copy; RLK_TUNE_PREFILL_DMA=0 forces the register-staged kernel
+  // The load-to-LDS kernel runs when the block table fits its LDS copy;
+  // RLK_TUNE_PREFILL_DMA=0 forces the register-staged kernel
   // (the kernel keeps byte offsets inside a cache block in 32 bits)
   const bool dma_fits = p.max_blocks_per_seq <= kDmaTableCap &&
                         static_cast<uint64_t>(p.kv.num_kv_heads) * p.kv.block_size * p.kv.head_dim * 2 <
                             (uint64_t{1} << 32);
-  if (!int8 && dma_fits && tune_knob("RLK_TUNE_PREFILL_DMA", 1) != 0) {
+  // (INT8 with fp16 scales reads the dword that holds a scale and picks the
+  // half by the key position's parity: even block sizes only)
+  const bool dma_ok = dma_fits && (!int8 || !scale16 || p.kv.block_size % 2 == 0);
+  if (dma_ok && tune_knob("RLK_TUNE_PREFILL_DMA", 1) != 0) {
     auto dma = [&](auto kernel, auto geo) -> int {
       using G = decltype(geo);
       const size_t lds = G::lds_bytes(p.max_blocks_per_seq);
@@ -817,8 +912,11 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
       kernel<<<grid, G::kThreads, lds, stream>>>(a);
       return launch_status(what);
     };
-    return p.kv.head_dim == 64 ? dma(prefill_dma_kernel<64>, PfDma<64>{})
-                               : dma(prefill_dma_kernel<128>, PfDma<128>{});
+    if (int8)
+      return p.kv.head_dim == 64 ? dma(prefill_dma_kernel<64, true>, PfDma<64, true>{})
+                                 : dma(prefill_dma_kernel<128, true>, PfDma<128, true>{});
+    return p.kv.head_dim == 64 ? dma(prefill_dma_kernel<64, false>, PfDma<64, false>{})
+                               : dma(prefill_dma_kernel<128, false>, PfDma<128, false>{});
   }
   if (p.kv.head_dim == 64) {
     if (int8) go(prefill_attention_kernel<64, true>, PfShape<64, true>{});
