@@ -288,26 +288,28 @@ __device__ __forceinline__ void score_tile(f32x4 (&s)[QS][4], const f16x8 (&qb)[
 }
 
 // The softmax of one tile (scores sc) interleaved with the scores of the
-// next (into sn): four sections, each one subtile of MFMAs beside one phase
-// of the softmax (max of set 0, exponentials of set 0, then set 1); the
+// next (into sn): 2 QS sections, each 4 / (2 QS) subtiles of MFMAs beside one
+// phase of the softmax (max of set 0, exponentials of set 0, then set 1); the
 // scheduling barriers keep each section's registers bounded.
-template <int kMask, int D, class KFrag>
-__device__ __forceinline__ bool softmax_beside_scores(PfState<D, 2>& st, f32x4 (&sc)[2][4], f16x8 (&pb)[2][2],
-                                                      float (&alpha)[2], f32x4 (&sn)[2][4],
-                                                      const f16x8 (&qb)[2][D / 32], KFrag kf, int k0,
-                                                      const int (&qi)[2], int q_len, int past, int qd) {
+template <int kMask, int D, int QS, class KFrag>
+__device__ __forceinline__ bool softmax_beside_scores(PfState<D, QS>& st, f32x4 (&sc)[QS][4],
+                                                      f16x8 (&pb)[QS][2], float (&alpha)[QS],
+                                                      f32x4 (&sn)[QS][4], const f16x8 (&qb)[QS][D / 32],
+                                                      KFrag kf, int k0, const int (&qi)[QS], int q_len,
+                                                      int past, int qd) {
+  static_assert(QS == 1 || QS == 2, "one or two query sets");
   bool grew = false;
-  score_sub<D, 2>(sn, qb, kf, 0);
-  grew |= softmax_max<kMask>(st, sc, 0, alpha[0], k0, qi, q_len, past, qd, true);
-  __builtin_amdgcn_sched_barrier(0);
-  score_sub<D, 2>(sn, qb, kf, 1);
-  softmax_exp(st, sc, pb, 0, alpha[0]);
-  __builtin_amdgcn_sched_barrier(0);
-  score_sub<D, 2>(sn, qb, kf, 2);
-  grew |= softmax_max<kMask>(st, sc, 1, alpha[1], k0, qi, q_len, past, qd, true);
-  __builtin_amdgcn_sched_barrier(0);
-  score_sub<D, 2>(sn, qb, kf, 3);
-  softmax_exp(st, sc, pb, 1, alpha[1]);
+  // QS phases of max and exponentials, spread over the 4 subtiles
+  constexpr int kSubPerPhase = 4 / (2 * QS);
+#pragma unroll
+  for (int ph = 0; ph < 2 * QS; ++ph) {
+#pragma unroll
+    for (int i = 0; i < kSubPerPhase; ++i) score_sub<D, QS>(sn, qb, kf, ph * kSubPerPhase + i);
+    const int qs = ph / 2;
+    if (ph % 2 == 0) grew |= softmax_max<kMask>(st, sc, qs, alpha[qs], k0, qi, q_len, past, qd, true);
+    else softmax_exp(st, sc, pb, qs, alpha[qs]);
+    if (ph + 1 < 2 * QS) __builtin_amdgcn_sched_barrier(0);
+  }
   return __any(grew);
 }
 
@@ -543,11 +545,14 @@ constexpr int kDmaTableCap = 4096;  // block-table entries staged in LDS
 
 #define RLK_LDS __attribute__((address_space(3)))
 
-template <int D, bool kInt8>
+// QS query sets of 16 rows per wave: 2 normally; 1 at D = 128 for grids too
+// small to give every CU two workgroups (half the rows per workgroup).
+template <int D, bool kInt8, int QS = 2>
 struct PfDma {
-  static constexpr int kBQ = PfShape<D, false>::kBQ;
+  static constexpr int kQS = QS;
   static constexpr int kThreads = PfShape<D, false>::kThreads;
   static constexpr int kWaves = kThreads / 64;
+  static constexpr int kBQ = kWaves * 16 * QS;
   static constexpr int kRowBytes = 2 * D;             // fp16 image
   static constexpr int kTileBytes = kBK * kRowBytes;  // one fp16 K or V tile
   static constexpr int kRawRow = kInt8 ? D : 2 * D;   // cache row
@@ -579,11 +584,11 @@ __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int D, bool kInt8>
+template <int D, bool kInt8, int QS>
 __global__ __launch_bounds__((PfShape<D, false>::kThreads), (PfShape<D, false>::kWavesPerSimd)) void
 prefill_dma_kernel(PrefillArgs a) {
-  using G = PfDma<D, kInt8>;
-  constexpr int kQS = PfShape<D, false>::kQS, kBQ = PfShape<D, false>::kBQ;
+  using G = PfDma<D, kInt8, QS>;
+  constexpr int kQS = G::kQS, kBQ = G::kBQ;
   constexpr int kSteps = D / 32, kWaveRows = 16 * kQS;
   extern __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[];
   int32_t* tab_lds = reinterpret_cast<int32_t*>(pf_lds + G::kTableOff);
@@ -855,6 +860,19 @@ prefill_dma_kernel(PrefillArgs a) {
   stt.store(p, q0, qi, q_len, h, qd);
 }
 
+// compute units of the current device (cached per device)
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work* work,
             int scale16, hipStream_t stream) {
   const char* what = "paged_attention_prefill";
@@ -912,11 +930,18 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
       kernel<<<grid, G::kThreads, lds, stream>>>(a);
       return launch_status(what);
     };
-    if (int8)
-      return p.kv.head_dim == 64 ? dma(prefill_dma_kernel<64, true>, PfDma<64, true>{})
-                                 : dma(prefill_dma_kernel<128, true>, PfDma<128, true>{});
-    return p.kv.head_dim == 64 ? dma(prefill_dma_kernel<64, false>, PfDma<64, false>{})
-                               : dma(prefill_dma_kernel<128, false>, PfDma<128, false>{});
+    if (p.kv.head_dim == 64)
+      return int8 ? dma(prefill_dma_kernel<64, true, 2>, PfDma<64, true, 2>{})
+                  : dma(prefill_dma_kernel<64, false, 2>, PfDma<64, false, 2>{});
+    // D = 128: 16 query rows per wave when 32 would not give every CU two
+    // workgroups (RLK_TUNE_PREFILL_QS=1 or 2 forces one form)
+    const int grid2 = (rows + PfDma<128, false, 2>::kBQ - 1) / PfDma<128, false, 2>::kBQ * p.num_heads *
+                      w.num_seqs;
+    if (tune_knob("RLK_TUNE_PREFILL_QS", grid2 < 2 * device_cus() ? 1 : 2) == 1)
+      return int8 ? dma(prefill_dma_kernel<128, true, 1>, PfDma<128, true, 1>{})
+                  : dma(prefill_dma_kernel<128, false, 1>, PfDma<128, false, 1>{});
+    return int8 ? dma(prefill_dma_kernel<128, true, 2>, PfDma<128, true, 2>{})
+                : dma(prefill_dma_kernel<128, false, 2>, PfDma<128, false, 2>{});
   }
   if (p.kv.head_dim == 64) {
     if (int8) go(prefill_attention_kernel<64, true>, PfShape<64, true>{});

@@ -16,10 +16,11 @@ rows gathered into a compact buffer.  Larger cases cover several 64-row query
 tiles and 64-key tiles, contexts that are not multiples of either, fp16-stored
 INT8 scales, and the Llama-3.1-8B C3 chunks at full size (sampled rows).
 
-FP16 caches have two kernels: one that copies tiles to LDS with load-to-LDS
+Prefill attention has two kernels: one that copies tiles to LDS with load-to-LDS
 instructions (the default when the block table fits its LDS copy) and one that
-stages them through registers (RLK_TUNE_PREFILL_DMA=0, and every INT8 cache);
-each test runs under both settings."""
+stages them through registers (RLK_TUNE_PREFILL_DMA=0).  At D = 128 the first
+gives each wave 32 query rows, or 16 for small grids (RLK_TUNE_PREFILL_QS=1).
+Each test runs under the three settings."""
 import numpy as np
 import pytest
 
@@ -34,9 +35,10 @@ REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
              (8, 2, 128, True, [33, 280]), (4, 2, 64, True, [520])]
 
 
-@pytest.fixture(autouse=True, params=["dma", "reg"])
+@pytest.fixture(autouse=True, params=["dma", "dma16", "reg"])
 def kernel_path(request, monkeypatch):
-    monkeypatch.setenv("RLK_TUNE_PREFILL_DMA", "1" if request.param == "dma" else "0")
+    monkeypatch.setenv("RLK_TUNE_PREFILL_DMA", "0" if request.param == "reg" else "1")
+    monkeypatch.setenv("RLK_TUNE_PREFILL_QS", "1" if request.param == "dma16" else "2")
     return request.param
 
 
