@@ -577,8 +577,10 @@ struct PfDma {
   }
 };
 
-// s_waitcnt vmcnt(N): the compiler does not count load-to-LDS instructions
-// against the LDS reads that follow them, so the wait is explicit
+// s_waitcnt vmcnt(N): the compiler's own waits do not follow this kernel's
+// ring (it puts none before the 16-byte LDS reads and drains every load in
+// flight before the transposing reads), so the loop waits explicitly for the
+// tile it needs and reads the transposed V through inline asm
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
