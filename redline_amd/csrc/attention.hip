@@ -316,7 +316,14 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const floa
   float v[kN];
 #pragma unroll
   for (int h = 0; h < kP / 2; ++h) {
-    const f16x8 va = Row<kInt8>::halves(vb.r[2 * h]), vb2 = Row<kInt8>::halves(vb.r[2 * h + 1]);
+    f16x2 vv[8];  // element x of the pass pair's two keys
+    if constexpr (kInt8) {
+      int8x8_pairs_to_f16x2(vb.r[2 * h], vb.r[2 * h + 1], vv);
+    } else {
+      const f16x8 va = Row<kInt8>::halves(vb.r[2 * h]), vb2 = Row<kInt8>::halves(vb.r[2 * h + 1]);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) vv[x] = f16x2{va[x], vb2[x]};
+    }
     f16x2 ph[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) ph[g] = pp[h][g];
@@ -328,10 +335,9 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const floa
     }
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
-      const f16x2 vv = {va[x], vb2[x]};
 #pragma unroll
       for (int g = 0; g < G; ++g)  // the first pair starts from 0 (no zeroed accumulator)
-        v[g * 8 + x] = __builtin_amdgcn_fdot2(ph[g], vv, h == 0 ? 0.f : v[g * 8 + x], false);
+        v[g * 8 + x] = __builtin_amdgcn_fdot2(ph[g], vv[x], h == 0 ? 0.f : v[g * 8 + x], false);
     }
   }
   if constexpr (Geo<D>::kLPK == 8) {

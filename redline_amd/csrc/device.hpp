@@ -139,6 +139,29 @@ __device__ __forceinline__ f16x8 int8x8_to_f16(u32x2 r) {
   return __builtin_bit_cast(f16x8, w) - static_cast<_Float16>(1152);
 }
 
+// The codes of two rows, paired by element: out[x] = {a[x], b[x]} as exact
+// fp16 values, ready for v_dot2 over the two rows.  The bytes are first
+// interleaved (a0 b0 a1 b1 ...) by one permute per 4 codes, then each pair
+// gets the 0x64 high bytes as in int8x8_to_f16: 4 XORs + 4 + 8 byte permutes
+// + 8 packed subtracts for 16 codes, with no repacking of converted halves.
+__device__ __forceinline__ void int8x8_pairs_to_f16x2(u32x2 a, u32x2 b, f16x2 (&out)[8]) {
+  const uint32_t w[4] = {a.x ^ 0x80808080u, b.x ^ 0x80808080u, a.y ^ 0x80808080u,
+                         b.y ^ 0x80808080u};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    // selectors 0-3 pick from the second source (a), 4-7 from the first (b)
+    const uint32_t lo = __builtin_amdgcn_perm(w[2 * d + 1], w[2 * d], 0x05010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(w[2 * d + 1], w[2 * d], 0x07030602u);
+    const uint32_t t[4] = {__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      out[4 * d + i] = __builtin_bit_cast(f16x2, t[i]) - static_cast<_Float16>(1152);
+  }
+}
+
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
