@@ -224,21 +224,22 @@ SWEEP_KNOBS = {
 
 def sweep(torch, data, reps, only=None):
     """Times each kernel under every combination of its launch-policy knobs
-    (the RLK_TUNE_* environment overrides the launchers read per call)."""
+    (the RLK_TUNE_* overrides, set through rlk_set_tune_knob)."""
     import itertools
+    from redline_amd._lib import set_tune_knob
     for kern, knobs in SWEEP_KNOBS.items():
         if only and kern != only:
             continue
         names = list(knobs)
         for vals in itertools.product(*knobs.values()):
             for n, v in zip(names, vals):
-                os.environ[n] = str(v)
+                set_tune_knob(n, v)
             r = per_kernel(torch, data, reps, kern)[kern]
             print(json.dumps({"workload": data.w.key, "kernel": kern, "knobs": dict(zip(names, vals)),
                               "us_per_call": r["us_per_call"], "gb_per_s": r["gb_per_s"]}),
                   flush=True)
         for n in names:
-            del os.environ[n]
+            set_tune_knob(n, None)
 
 
 def attention_bench(torch, K, w, int8, reps, rotations=3, seed=0, eager_calls=0):
@@ -546,7 +547,8 @@ def main():
         for m in (1, 8, 16, 32):
             for cfg in (range(8) if args.sweep else [None]):
                 if cfg is not None:
-                    os.environ["RLK_TUNE_W4_CFG"] = str(cfg)
+                    from redline_amd._lib import set_tune_knob
+                    set_tune_knob("RLK_TUNE_W4_CFG", cfg)
                 r = gemv_bench(torch, K, m, args.reps, unfused=not args.sweep)
                 r["cfg"] = cfg
                 print(json.dumps(r), flush=True)

@@ -78,7 +78,9 @@ struct DecodeAttentionWork {
   const int32_t* item_token = nullptr;  // [num_items]
   const int32_t* item_seq = nullptr;    // [num_items]
   int num_items = 0;
-  int max_partitions = 1;   // grid size; partitions beyond the context exit early
+  int max_partitions = 1;   // grid size; partitions beyond the context exit early.
+                            // Must be >= ceil(context / 256) for every item: keys
+                            // past max_partitions * 256 are not read (no error)
   float* ws_out = nullptr;  // [num_items, num_heads, max_partitions, head_dim]
   float* ws_max = nullptr;  // [num_items, num_heads, max_partitions]
   float* ws_sum = nullptr;

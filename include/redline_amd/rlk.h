@@ -59,6 +59,14 @@ const char* rlk_last_error(void);
 /* Library version string. */
 const char* rlk_version(void);
 
+/* Tuning hook (no counterpart in the reference): sets (set != 0) or clears
+ * the launch-policy override `name` (one of RLK_TUNE_GATHER_BS, _GATHER_NT,
+ * _NORM_TPR, _NORM_NT, _SWIGLU_BS, _SWIGLU_NT, _ROPE_WPT, _ATTN_PERSIST,
+ * _W4_CFG, _W8_CFG, _PREFILL_DMA, _PREFILL_QS).  The environment variables of
+ * the same names are read once, at the first launch of the process; later
+ * changes go through this call only.  Unknown name: RLK_EINVAL. */
+int rlk_set_tune_knob(const char* name, int value, int set);
+
 /* ------------------------------------------------------------ elementwise */
 
 /* out[t, :] = table[ids[t], :]   (table [V, hidden], out [n, hidden]).
@@ -218,7 +226,10 @@ typedef struct rlk_decode_attention_work {
  * through the caller's workspace.  Replaces kernels::paged_attention_decode,
  * src/cuda/kernels/attention.cu:70-210,362-398.
  * num_items <= 0: no-op.  head_dim not in {64, 128} or G > 8: RLK_EUNSUPPORTED.
- * max_partitions > 1 needs ws_out / ws_max / ws_sum. */
+ * max_partitions > 1 needs ws_out / ws_max / ws_sum.
+ * Contract: max_partitions >= ceil((positions[t] + 1) / 256) for every item.
+ * Keys past max_partitions * 256 are not read, and no error is reported (the
+ * launcher cannot see device-side positions without synchronising). */
 int rlk_paged_attention_decode(const rlk_attention_params* params,
                                const rlk_decode_attention_work* work, hipStream_t stream);
 

@@ -106,6 +106,7 @@ _I = C.c_int
 _SIGNATURES = {
     "rlk_last_error": (C.c_char_p, []),
     "rlk_version": (C.c_char_p, []),
+    "rlk_set_tune_knob": (_I, [C.c_char_p, _I, _I]),
     "rlk_embedding_lookup": (_I, [_P, _P, _I, _I, _P, _P]),
     "rlk_fused_add_rmsnorm": (_I, [_P, _P, _P, _I, _I, C.c_float, _P, _P]),
     "rlk_silu_and_mul": (_I, [_P, _I, _I, _P, _P]),
@@ -163,6 +164,29 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def set_tune_knob(name: str, value: int | None) -> None:
+    """Sets (or, with None, clears) a launch-policy override RLK_TUNE_*.
+    The library reads the environment once per process; tuning runs and the
+    tests that cover every launch policy change the knobs through this."""
+    check(lib().rlk_set_tune_knob(name.encode(), 0 if value is None else int(value),
+                                  0 if value is None else 1))
+
+
+class tune_knob:
+    """Context manager: the knob set to `value` inside the block, cleared after."""
+
+    def __init__(self, name: str, value: int | None):
+        self.name, self.value = name, value
+
+    def __enter__(self):
+        set_tune_knob(self.name, self.value)
+        return self
+
+    def __exit__(self, *exc):
+        set_tune_knob(self.name, None)
+        return False
 
 
 def exported_symbols() -> list[str]:

@@ -46,10 +46,23 @@ def _compile(src: str) -> Path:
     return out
 
 
-def build_library(verbose: bool = True) -> Path:
+def _stale(src: str) -> bool:
+    """True when the object is older than its source or than any header."""
+    out = OBJ / (src + ".o")
+    if not out.exists():
+        return True
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), *(ROOT / "include").rglob("*.h")]
+    return max(p.stat().st_mtime for p in deps) > out.stat().st_mtime
+
+
+def build_library(verbose: bool = True, only_changed: bool = False) -> Path:
+    """Compiles every source (or, with only_changed, those whose object is
+    stale) and links librlk.so."""
     OBJ.mkdir(exist_ok=True)
+    todo = [s for s in SOURCES if not only_changed or _stale(s)]
     with ThreadPoolExecutor(max_workers=4) as pool:
-        objs = list(pool.map(_compile, SOURCES))
+        list(pool.map(_compile, todo))
+    objs = [OBJ / (s + ".o") for s in SOURCES]
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(LIB), *map(str, objs)]
     subprocess.run(cmd, check=True)
     if verbose:
@@ -58,4 +71,4 @@ def build_library(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build_library()
+    build_library(only_changed="--changed" in sys.argv)

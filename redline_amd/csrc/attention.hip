@@ -723,7 +723,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
 // overrides: workgroups per CU for the persistent form, or 0 for the grid form.
 template <int D, int G>
 void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
-  const int mode = tune_knob("RLK_TUNE_ATTN_PERSIST", 2);
+  const int mode = tune_knob(kAttnPersist, 2);
   if (mode > 0 && a.w.num_items <= kMaxItemsLds) {
     const int64_t units = static_cast<int64_t>(a.w.num_items) * a.w.max_partitions * a.p.kv.num_kv_heads;
     const int blocks = static_cast<int>(std::min<int64_t>(units, static_cast<int64_t>(compute_units()) * mode));

@@ -31,9 +31,9 @@ struct FlatPolicy {
 // Launch policy of the flat streaming kernels (measured on MI355X with cold,
 // rotating buffers at decode b32 and 4k-16k-row prefill shapes): non-temporal
 // accesses were faster at every size, by 8-20%; the best block width depends
-// weakly on the launch size.  RLK_TUNE_<NAME>_BS / _NT override the policy for
-// tuning runs.
-FlatPolicy pick_flat(int bs, const char* bs_knob, const char* nt_knob) {
+// weakly on the launch size.  The RLK_TUNE_<NAME>_BS / _NT knobs (status.hpp)
+// override it for tuning runs.
+FlatPolicy pick_flat(int bs, Knob bs_knob, Knob nt_knob) {
   FlatPolicy p;
   p.bs = tune_knob(bs_knob, bs);
   p.nt = tune_knob(nt_knob, 1) != 0;
@@ -77,8 +77,7 @@ int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* ds
   if (total > 0x7fffffffull)
     return fail(RLK_EINVAL, "%s: %d rows x %d vectors exceed one launch; split the call", what, n,
                 vecs);
-  const FlatPolicy p = pick_flat(total >= (1u << 20) ? 256 : 128, "RLK_TUNE_GATHER_BS",
-                                 "RLK_TUNE_GATHER_NT");
+  const FlatPolicy p = pick_flat(total >= (1u << 20) ? 256 : 128, kGatherBs, kGatherNt);
   const uint64_t blocks = (total + p.bs - 1) / p.bs;
   const auto* s = static_cast<const u32x4*>(src);
   auto* d = static_cast<u32x4*>(dst);
@@ -302,7 +301,7 @@ void launch_swiglu_bs(bool interleaved, uint64_t blocks, const u32x4* gu, uint32
 
 void launch_swiglu(bool interleaved, const u32x4* gu, uint32_t vecs, uint32_t total, u32x4* o,
                    hipStream_t stream) {
-  const FlatPolicy p = pick_flat(64, "RLK_TUNE_SWIGLU_BS", "RLK_TUNE_SWIGLU_NT");
+  const FlatPolicy p = pick_flat(64, kSwigluBs, kSwigluNt);
   const uint64_t blocks = (total + p.bs - 1) / p.bs;
 #define RLK_SWIGLU_BS(B)                                                               \
   p.nt ? launch_swiglu_bs<B, true>(interleaved, blocks, gu, vecs, total, o, stream)    \
@@ -372,8 +371,8 @@ extern "C" int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta,
   // Non-temporal accesses measured faster at every batch size.
   int tpr = 64;
   while (tpr < 512 && tpr < a.vecs) tpr *= 2;
-  tpr = tune_knob("RLK_TUNE_NORM_TPR", tpr);
-  const bool nt = tune_knob("RLK_TUNE_NORM_NT", 1) != 0;
+  tpr = tune_knob(kNormTpr, tpr);
+  const bool nt = tune_knob(kNormNt, 1) != 0;
   bool launched = nt ? launch_norm_nt<true>(tpr, a, stream) : launch_norm_nt<false>(tpr, a, stream);
   if (!launched) launched = launch_norm_nt<false>(512, a, stream);
   if (!launched) {

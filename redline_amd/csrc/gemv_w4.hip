@@ -763,17 +763,10 @@ int launch_pairs(W4Args a, hipStream_t stream) {
   const int xper = (a.m * (std::min(cpp * kKP, a.k) / 8) + threads - 1) / threads;
   auto go = [&](auto kernel) -> int {
     if (lds > 64 * 1024) {
-      static size_t granted[64] = {0};  // per device, see launch()
-      int dev = 0;
-      if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || granted[dev] < lds) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(kLdsBudget));
-        if (e != hipSuccess)
-          return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
-                      hipGetErrorString(e));
-        if (dev >= 0 && dev < 64) granted[dev] = kLdsBudget;
-      }
+      const hipError_t e = grant_dynamic_lds(reinterpret_cast<const void*>(kernel), kLdsBudget);
+      if (e != hipSuccess)
+        return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
+                    hipGetErrorString(e));
     }
     kernel<<<(tiles + nw - 1) / nw, threads, lds, stream>>>(a);
     return RLK_OK;
@@ -833,7 +826,7 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
 template <int MODE>
 int dispatch(const W4Args& a, hipStream_t s) {
   const bool wide = a.group_size % 128 == 0;
-  const int cfg = tune_knob("RLK_TUNE_W4_CFG", 0);
+  const int cfg = tune_knob(kW4Cfg, 0);
   if (a.m <= 16)
     return wide ? launch_cfg<128, 1, MODE>(a, cfg, s) : launch_cfg<32, 1, MODE>(a, cfg, s);
   return wide ? launch_cfg<128, 2, MODE>(a, cfg, s) : launch_cfg<32, 2, MODE>(a, cfg, s);
@@ -886,7 +879,7 @@ int gemv_w4(const char* what, const uint16_t* x, int m, const uint8_t* w, const 
 // selects P = 2, 4, 8 for sweeps.
 template <int MT, int MODE>
 int dispatch_w8(const W4Args& a, hipStream_t s) {
-  switch (tune_knob("RLK_TUNE_W8_CFG", 0)) {
+  switch (tune_knob(kW8Cfg, 0)) {
     case 1: return launch_pairs<2, MT, MODE, true>(a, s);
     case 2: return launch_pairs<4, MT, MODE, true>(a, s);
     case 3: return launch_pairs<8, MT, MODE, true>(a, s);

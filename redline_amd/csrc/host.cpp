@@ -273,6 +273,7 @@ extern "C" int rlk_batch_builder_add(rlk_batch_builder* b, const int32_t* tokens
   if (b->num_seqs() + 1 > b->max_seqs)
     return fail(RLK_EINVAL, "batch exceeds max sequences (%d)", b->max_seqs);
   if (num_blocks < 0 || num_blocks > b->max_blocks) return fail(RLK_EINVAL, "block table too long");
+  if (blocks == nullptr && num_blocks > 0) return fail(RLK_EINVAL, "null block table");
   if (static_cast<int64_t>(num_blocks) * b->block_size < static_cast<int64_t>(start_pos) + n)
     return fail(RLK_EINVAL, "sequence has too few KV blocks for position %d", start_pos + n - 1);
   for (int i = 0; i < n; ++i) {

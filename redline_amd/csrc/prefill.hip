@@ -887,6 +887,11 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
   if (p.kv.head_dim != 64 && p.kv.head_dim != 128)
     return fail(RLK_EUNSUPPORTED, "%s: unsupported head_dim %d", what, p.kv.head_dim);
   if (p.kv.block_size <= 0) return fail(RLK_EINVAL, "%s: bad block_size %d", what, p.kv.block_size);
+  if (p.kv.dtype != RLK_KV_FP16 && p.kv.dtype != RLK_KV_INT8)
+    return fail(RLK_EINVAL, "%s: unknown KV dtype %d", what, p.kv.dtype);
+  if (w.num_seqs > 65535 || p.num_heads > 65535)
+    return fail(RLK_EINVAL, "%s: %d sequences x %d heads exceed one launch grid; split the call",
+                what, w.num_seqs, p.num_heads);
   const bool int8 = p.kv.dtype == RLK_KV_INT8;
   if (p.q == nullptr || p.out == nullptr || p.kv.k == nullptr || p.kv.v == nullptr ||
       p.block_tables == nullptr || w.seq_ids == nullptr || w.q_start == nullptr ||
@@ -912,22 +917,15 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
   // (INT8 with fp16 scales reads the dword that holds a scale and picks the
   // half by the key position's parity: even block sizes only)
   const bool dma_ok = dma_fits && (!int8 || !scale16 || p.kv.block_size % 2 == 0);
-  if (dma_ok && tune_knob("RLK_TUNE_PREFILL_DMA", 1) != 0) {
+  if (dma_ok && tune_knob(kPrefillDma, 1) != 0) {
     auto dma = [&](auto kernel, auto geo) -> int {
       using G = decltype(geo);
       const size_t lds = G::lds_bytes(p.max_blocks_per_seq);
-      static size_t granted[64] = {0};
-      int dev = 0;
-      if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || granted[dev] < lds) {
-        const size_t want = G::lds_bytes(kDmaTableCap);
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(want));
-        if (e != hipSuccess)
-          return fail(RLK_EUNSUPPORTED, "%s: %zu bytes of LDS refused (%s)", what, want,
-                      hipGetErrorString(e));
-        if (dev >= 0 && dev < 64) granted[dev] = want;
-      }
+      const size_t want = G::lds_bytes(kDmaTableCap);
+      const hipError_t e = grant_dynamic_lds(reinterpret_cast<const void*>(kernel), want);
+      if (e != hipSuccess)
+        return fail(RLK_EUNSUPPORTED, "%s: %zu bytes of LDS refused (%s)", what, want,
+                    hipGetErrorString(e));
       const dim3 grid((rows + G::kBQ - 1) / G::kBQ, p.num_heads, w.num_seqs);
       kernel<<<grid, G::kThreads, lds, stream>>>(a);
       return launch_status(what);
@@ -939,7 +937,7 @@ int prefill(const rlk_attention_params* params, const rlk_prefill_attention_work
     // workgroups (RLK_TUNE_PREFILL_QS=1 or 2 forces one form)
     const int grid2 = (rows + PfDma<128, false, 2>::kBQ - 1) / PfDma<128, false, 2>::kBQ * p.num_heads *
                       w.num_seqs;
-    if (tune_knob("RLK_TUNE_PREFILL_QS", grid2 < 2 * device_cus() ? 1 : 2) == 1)
+    if (tune_knob(kPrefillQs, grid2 < 2 * device_cus() ? 1 : 2) == 1)
       return int8 ? dma(prefill_dma_kernel<128, true, 1>, PfDma<128, true, 1>{})
                   : dma(prefill_dma_kernel<128, false, 1>, PfDma<128, false, 1>{});
     return int8 ? dma(prefill_dma_kernel<128, true, 2>, PfDma<128, true, 2>{})
@@ -970,6 +968,8 @@ extern "C" int rlk_paged_attention_prefill_ex(const rlk_attention_params* params
                                               const rlk_prefill_attention_work* work,
                                               const rlk_attention_options* options,
                                               hipStream_t stream) {
-  const int s16 = options != nullptr && options->scale_dtype == RLK_SCALE_F16;
-  return prefill(params, work, s16, stream);
+  const int scale_dtype = options != nullptr ? options->scale_dtype : RLK_SCALE_F32;
+  if (scale_dtype != RLK_SCALE_F32 && scale_dtype != RLK_SCALE_F16)
+    return fail(RLK_EINVAL, "paged_attention_prefill_ex: unknown scale dtype %d", scale_dtype);
+  return prefill(params, work, scale_dtype == RLK_SCALE_F16, stream);
 }

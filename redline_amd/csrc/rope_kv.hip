@@ -212,7 +212,7 @@ int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_map
   const int heads = num_heads + 2 * kv->num_kv_heads;
   const int heads_per_wave = kWave / (kv->head_dim / 16);
   int wpt = (heads + heads_per_wave - 1) / heads_per_wave;
-  wpt = tune_knob("RLK_TUNE_ROPE_WPT", wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
+  wpt = tune_knob(kRopeWpt, wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
   const bool int8 = kv->dtype == RLK_KV_INT8;
   if (kv->head_dim == 128) {
     launch_dt<128>(a, int8, wpt, stream);

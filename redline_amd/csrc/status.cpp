@@ -5,6 +5,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
+#include <climits>
+#include <mutex>
 
 #include "redline_amd/rlk.h"
 
@@ -40,14 +43,83 @@ int compute_units() {
   return cus[dev];
 }
 
-int tune_knob(const char* name, int fallback) {
-  const char* v = std::getenv(name);
-  if (v == nullptr || *v == '\0') return fallback;
-  return std::atoi(v);
+namespace {
+struct LdsGrant {
+  int dev;
+  const void* kernel;
+  size_t bytes;
+};
+std::mutex g_grant_mu;
+LdsGrant g_grants[256];
+int g_num_grants = 0;
+}  // namespace
+
+hipError_t grant_dynamic_lds(const void* kernel, size_t bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_grant_mu);
+  for (int i = 0; i < g_num_grants; ++i) {
+    if (g_grants[i].dev == dev && g_grants[i].kernel == kernel && g_grants[i].bytes >= bytes)
+      return hipSuccess;
+  }
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(bytes));
+  if (e != hipSuccess) return e;
+  for (int i = 0; i < g_num_grants; ++i) {
+    if (g_grants[i].dev == dev && g_grants[i].kernel == kernel) {
+      g_grants[i].bytes = bytes;
+      return hipSuccess;
+    }
+  }
+  if (g_num_grants < 256) g_grants[g_num_grants++] = LdsGrant{dev, kernel, bytes};
+  return hipSuccess;  // a full table only means the attribute is set again next time
+}
+
+namespace {
+// Launch-policy overrides, indexed by Knob.  They are read from the
+// environment once per process (the first launch) and can be changed only
+// through rlk_set_tune_knob; a production launch therefore pays one atomic
+// load per knob, and a variable inherited after start-up changes nothing.
+constexpr const char* kKnobNames[kNumKnobs] = {
+    "RLK_TUNE_GATHER_BS", "RLK_TUNE_GATHER_NT", "RLK_TUNE_NORM_TPR",   "RLK_TUNE_NORM_NT",
+    "RLK_TUNE_SWIGLU_BS", "RLK_TUNE_SWIGLU_NT", "RLK_TUNE_ROPE_WPT",   "RLK_TUNE_ATTN_PERSIST",
+    "RLK_TUNE_W4_CFG",    "RLK_TUNE_W8_CFG",    "RLK_TUNE_PREFILL_DMA", "RLK_TUNE_PREFILL_QS",
+};
+constexpr int kUnset = INT_MIN;
+std::atomic<int> g_knobs[kNumKnobs];
+std::once_flag g_knobs_once;
+
+void read_knobs_from_env() {
+  for (int k = 0; k < kNumKnobs; ++k) {
+    const char* v = std::getenv(kKnobNames[k]);
+    g_knobs[k].store(v != nullptr && *v != '\0' ? std::atoi(v) : kUnset,
+                     std::memory_order_relaxed);
+  }
+}
+}  // namespace
+
+int tune_knob(Knob knob, int fallback) {
+  std::call_once(g_knobs_once, read_knobs_from_env);
+  const int v = g_knobs[knob].load(std::memory_order_relaxed);
+  return v == kUnset ? fallback : v;
 }
 
 }  // namespace rlk
 
 extern "C" const char* rlk_last_error(void) { return rlk::g_message; }
+
+extern "C" int rlk_set_tune_knob(const char* name, int value, int set) {
+  std::call_once(rlk::g_knobs_once, rlk::read_knobs_from_env);
+  if (name != nullptr) {
+    for (int k = 0; k < rlk::kNumKnobs; ++k) {
+      if (std::strcmp(name, rlk::kKnobNames[k]) == 0) {
+        rlk::g_knobs[k].store(set ? value : rlk::kUnset, std::memory_order_relaxed);
+        return RLK_OK;
+      }
+    }
+  }
+  return rlk::fail(RLK_EINVAL, "rlk_set_tune_knob: unknown knob '%s'", name ? name : "(null)");
+}
 
 extern "C" const char* rlk_version(void) { return "redline_amd 0.1.0 (gfx950)"; }

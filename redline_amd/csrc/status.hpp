@@ -20,8 +20,20 @@ int launch_status(const char* what);
 // fails).
 int compute_units();
 
-// Environment override of a launch-policy knob (tuning experiments only);
-// returns `fallback` when the variable is unset.
-int tune_knob(const char* name, int fallback);
+// Raises the dynamic-LDS limit of `kernel` on the current device to at least
+// `bytes` (hipFuncSetAttribute), once per (device, kernel) and size: later
+// calls are a lookup.
+hipError_t grant_dynamic_lds(const void* kernel, size_t bytes);
+
+// Launch-policy knobs: overrides for tuning experiments, read from the
+// RLK_TUNE_* environment variables once per process and settable through
+// rlk_set_tune_knob.
+enum Knob {
+  kGatherBs, kGatherNt, kNormTpr, kNormNt, kSwigluBs, kSwigluNt, kRopeWpt, kAttnPersist,
+  kW4Cfg, kW8Cfg, kPrefillDma, kPrefillQs, kNumKnobs
+};
+
+// The override of `knob`, or `fallback` when none is set.
+int tune_knob(Knob knob, int fallback);
 
 }  // namespace rlk

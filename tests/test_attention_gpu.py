@@ -47,12 +47,9 @@ def attention_form(request):
     """The launcher's two kernel forms: one workgroup per (partition, kv head,
     item), or persistent workgroups over the in-context units only
     (RLK_TUNE_ATTN_PERSIST = 0 or workgroups per CU)."""
-    import os
-    env = {"grid": "0", "persistent": "2"}.get(request.param)
-    if env is not None:
-        os.environ["RLK_TUNE_ATTN_PERSIST"] = env
-    yield request.param
-    os.environ.pop("RLK_TUNE_ATTN_PERSIST", None)
+    from redline_amd._lib import tune_knob
+    with tune_knob("RLK_TUNE_ATTN_PERSIST", {"grid": 0, "persistent": 2}.get(request.param)):
+        yield request.param
 
 
 REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),

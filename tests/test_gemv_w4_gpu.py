@@ -11,13 +11,13 @@ and the SwiGLU output additionally with the reference's 6e-3 bound
 g = 64, m in 1, 3, 8, 13, 16; inter = 192, k = 256, g = 64), the 128-K chunk
 path (g a multiple of 128), m up to 32 (two activation tiles) and the
 Llama-3.1-8B gate_up projection (n = 2 x 14336, k = 4096, g = 128)."""
-import os
 
 import numpy as np
 import pytest
 
 import oracle
 import redline_amd as ra
+from redline_amd._lib import tune_knob
 from tests._util import (assert_close_f16, int4_linear, interleave_rows, randn_f16, rel_max_err,
                          say)
 
@@ -124,11 +124,8 @@ def test_gemv_w4_launch_policies_agree(torch_cuda, cfg):
     packed, s, o, _ = int4_linear(rng, n, k, g)
     x = randn_f16(rng, (m, k))
     want = oracle.gemv_w4a16(x, packed, s, o, g)
-    os.environ["RLK_TUNE_W4_CFG"] = str(cfg)
-    try:
+    with tune_knob("RLK_TUNE_W4_CFG", cfg):
         got = run_gemv(torch, x, packed, s, o, g, f32=True)
-    finally:
-        del os.environ["RLK_TUNE_W4_CFG"]
     assert rel_max_err(got, want) <= 1e-4
 
 

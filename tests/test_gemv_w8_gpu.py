@@ -10,13 +10,13 @@ bias), K that is not a multiple of the 128-K chunk pair (16 .. 1040), m up to 32
 (two activation tiles), Llama-3.1-8B projections (gate: n = 14336, k = 4096;
 down: n = 4096, k = 14336, where x is staged in several passes) and every
 launch policy."""
-import os
 
 import numpy as np
 import pytest
 
 import oracle
 import redline_amd as ra
+from redline_amd._lib import tune_knob
 from tests._util import assert_close_f16, int8_linear, randn_f16, rel_max_err, say
 
 pytestmark = pytest.mark.gpu
@@ -101,11 +101,8 @@ def test_gemv_w8_launch_policies_agree(torch_cuda, cfg):
     for m in (1, 9, 24):
         x = randn_f16(rng, (m, k))
         want = oracle.gemv_w8a16(x, q, s)
-        os.environ["RLK_TUNE_W8_CFG"] = str(cfg)
-        try:
+        with tune_knob("RLK_TUNE_W8_CFG", cfg):
             got = run_w8(torch_cuda, x, q, s, None, True)
-        finally:
-            del os.environ["RLK_TUNE_W8_CFG"]
         assert rel_max_err(got, want) <= 1e-4, m
 
 

@@ -259,3 +259,47 @@ def test_batch_builder_limits():
     b.add([1], 0, 1, None, [1], mode=ra.LogitsMode.kLast)
     with pytest.raises(ra.Error, match="max sequences"):
         b.add([1], 0, 1, None, [1])
+
+
+def test_batch_builder_null_block_table():
+    L = ra.lib()
+    b = L.rlk_batch_builder_create(4, 2, 2, 2, 16, 1)
+    try:
+        toks = (C.c_int32 * 1)(5)
+        st = L.rlk_batch_builder_add(b, toks, 0, 1, None, None, 1, 1.0, 0, 1.0, 0, 0, None)
+        assert st == _lib.RLK_EINVAL
+        assert b"null block table" in L.rlk_last_error()
+    finally:
+        L.rlk_batch_builder_destroy(b)
+
+
+def test_prefill_argument_errors():
+    """The prefill launcher validates the KV dtype, the options' scale dtype and
+    the grid limits before launching, as the decode launcher does."""
+    L = ra.lib()
+    d = C.c_void_p(16)  # non-null stand-in: nothing is launched
+    kv = _lib.KVLayerView(d, d, d, d, 16, 2, 128, 5)
+    prm = _lib.AttentionParams(d, 1024, d, 4, 0.1, kv, d, 4, d)
+    wk = _lib.PrefillAttentionWork(d, d, d, d, 2, 1)
+    assert L.rlk_paged_attention_prefill(C.byref(prm), C.byref(wk), None) == _lib.RLK_EINVAL
+    assert b"unknown KV dtype" in L.rlk_last_error()
+    prm.kv.dtype = 0
+    opt = _lib.AttentionOptions(7)
+    assert L.rlk_paged_attention_prefill_ex(C.byref(prm), C.byref(wk), C.byref(opt), None) == \
+        _lib.RLK_EINVAL
+    assert b"unknown scale dtype" in L.rlk_last_error()
+    wk.num_seqs = 70000
+    assert L.rlk_paged_attention_prefill(C.byref(prm), C.byref(wk), None) == _lib.RLK_EINVAL
+    assert b"split the call" in L.rlk_last_error()
+
+
+def test_tune_knobs_set_and_clear():
+    """Launch-policy overrides change only through rlk_set_tune_knob once the
+    library has started; unknown names are rejected."""
+    L = ra.lib()
+    assert L.rlk_set_tune_knob(b"RLK_TUNE_ROPE_WPT", 3, 1) == 0
+    assert L.rlk_set_tune_knob(b"RLK_TUNE_ROPE_WPT", 0, 0) == 0
+    assert L.rlk_set_tune_knob(b"RLK_TUNE_NOPE", 1, 1) == _lib.RLK_EINVAL
+    assert b"unknown knob" in L.rlk_last_error()
+    with _lib.tune_knob("RLK_TUNE_W4_CFG", 2):
+        pass

@@ -36,10 +36,11 @@ REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
 
 
 @pytest.fixture(autouse=True, params=["dma", "dma16", "reg"])
-def kernel_path(request, monkeypatch):
-    monkeypatch.setenv("RLK_TUNE_PREFILL_DMA", "0" if request.param == "reg" else "1")
-    monkeypatch.setenv("RLK_TUNE_PREFILL_QS", "1" if request.param == "dma16" else "2")
-    return request.param
+def kernel_path(request):
+    from redline_amd._lib import tune_knob
+    with tune_knob("RLK_TUNE_PREFILL_DMA", 0 if request.param == "reg" else 1), \
+            tune_knob("RLK_TUNE_PREFILL_QS", 1 if request.param == "dma16" else 2):
+        yield request.param
 
 
 @pytest.fixture(scope="module")
