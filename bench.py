@@ -448,12 +448,14 @@ def w8_bench(torch, K, m, reps, n=2 * 14336, k=4096, eager_calls=0):
             "rotating_input_sets": R}
 
 
-def cpu_baseline(torch, data, seconds=10.0):
-    """The CPU oracle (oracle/oracle.c, single thread) on the same step:
-    a bounded number of full steps over one input set, copied to host."""
-    import ctypes as C
+def cpu_baseline(torch, data, seconds=8.0, max_threads=16):
+    """The CPU port of the layer step (oracle/cpu_step.cpp: F16C conversions,
+    rows split over a persistent std::thread pool pinned to the affinity
+    mask's cores) on the same step, timed on this box's host cores: once on
+    one thread and once on min(affinity cores, max_threads) threads, each for
+    a bounded `seconds` of full steps over one input set copied to host."""
     import oracle
-    L = oracle.lib()
+    L = oracle.cpu_step_lib()
     w, m, T = data.w, data.w.model, data.T
     s = data.sets[0]
     h = lambda t: np.ascontiguousarray(t.cpu().numpy())  # noqa: E731
@@ -471,23 +473,43 @@ def cpu_baseline(torch, data, seconds=10.0):
     vs = np.zeros(shape[:3], np.float32) if w.kv_int8 else None
     gu, act = h(s["gu"]).view(np.uint16), np.empty((T, m.inter), np.uint16)
     p = oracle.p
+    import ctypes as C
     args = (p(ids), p(table), T, m.hidden, p(emb), p(res), p(delta), p(wgt), C.c_float(m.eps),
             p(normed), p(qkv), p(pos), p(slot), m.hq, m.hkv, m.head_dim, p(cos), p(sin), p(kc),
             p(vc), p(ks), p(vs), w.block_size, int(w.kv_int8), p(gu), m.inter, p(act))
-    L.orc_layer_step(*args)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        L.orc_layer_step(*args)
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= seconds:
-            break
     nb = data.bytes()
     step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
-    return {"value": round(step_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port", "ms_per_step": round(dt / n * 1e3, 3),
-            "sample": f"{n} full {w.key} steps (embedding, 2x add+RMSNorm, RoPE+KV, SwiGLU) "
-                      f"in {dt:.1f} s, single thread, oracle/oracle.c"}
+    affinity = L.cps_affinity_cores()
+
+    def run(threads):
+        pool = L.cps_create(threads)
+        if not pool:
+            raise RuntimeError("CPU baseline needs AVX2 and F16C")
+        try:
+            for _ in range(3):
+                L.cps_layer_step(pool, *args)  # warm: page in the table rows and the cache
+            n, t0 = 0, time.perf_counter()
+            while True:
+                L.cps_layer_step(pool, *args)
+                n += 1
+                dt = time.perf_counter() - t0
+                if dt >= seconds:
+                    break
+        finally:
+            L.cps_destroy(pool)
+        return n, dt
+
+    n1, dt1 = run(1)
+    threads = max(1, min(affinity, max_threads))
+    nm, dtm = run(threads)
+    gbs = lambda n, dt: round(step_bytes * n / dt / 1e9, 3)  # noqa: E731
+    return {"value": gbs(nm, dtm), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(dtm / nm * 1e3, 4),
+            "single_thread": {"value": gbs(n1, dt1), "ms_per_step": round(dt1 / n1 * 1e3, 4)},
+            "affinity_cores": affinity,
+            "sample": f"{w.key} layer steps (embedding, 2x add+RMSNorm, RoPE+KV, SwiGLU) on one "
+                      f"input set: {nm} steps in {dtm:.1f} s on {threads} threads, {n1} steps in "
+                      f"{dt1:.1f} s on 1 thread; oracle/cpu_step.cpp (F16C, std::thread rows)"}
 
 
 def main():
@@ -502,7 +524,8 @@ def main():
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention figures")
     ap.add_argument("--no-gemv", action="store_true", help="skip the INT4 GEMV + SwiGLU figures")
     ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="seconds of CPU steps per thread count (single and multi)")
     ap.add_argument("--rotations", type=int, default=None,
                     help="rotating input sets (default: enough to exceed 2x the Infinity Cache)")
     ap.add_argument("--sweep", action="store_true",
@@ -674,11 +697,12 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log("CPU baseline (oracle) ...")
+        log("CPU baseline (oracle/cpu_step.cpp, 1 and N threads) ...")
         dcpu = LayerData(torch, K, w, rotations=1)
         cpu = cpu_baseline(torch, dcpu, args.cpu_seconds)
         del dcpu
-        log(f"CPU: {cpu['value']} GB/s, {cpu['ms_per_step']} ms/step")
+        log(f"CPU: {cpu['value']} GB/s, {cpu['ms_per_step']} ms/step on {cpu['cores']} threads; "
+            f"1 thread {cpu['single_thread']['value']} GB/s")
 
     line = {
         "metric": "achieved HBM GB/s (% of peak) and us/call per fused layer kernel, 8B decode b32",

@@ -62,6 +62,28 @@ def lib() -> C.CDLL:
     return _o
 
 
+CPUSTEP_LIB = HERE / "libcpustep.so"
+_c = None
+
+
+def cpu_step_lib() -> C.CDLL:
+    """The multi-threaded CPU port of the layer step (cpu_step.cpp), used as
+    bench.py's CPU baseline; same step arguments as orc_layer_step after the
+    pool handle."""
+    global _c
+    if _c is None:
+        if not CPUSTEP_LIB.exists():
+            build()
+        L = C.CDLL(str(CPUSTEP_LIB))
+        L.cps_affinity_cores.restype, L.cps_affinity_cores.argtypes = _I, []
+        L.cps_create.restype, L.cps_create.argtypes = _P, [_I]
+        L.cps_destroy.restype, L.cps_destroy.argtypes = None, [_P]
+        L.cps_layer_step.restype = None
+        L.cps_layer_step.argtypes = [_P] + list(lib().orc_layer_step.argtypes)
+        _c = L
+    return _c
+
+
 def has_ref() -> bool:
     return REF_LIB.exists()
 

@@ -70,5 +70,23 @@ def build_library(verbose: bool = True, only_changed: bool = False) -> Path:
     return LIB
 
 
+TEST_PROGRAMS = {"kernels_gpu": ROOT / "tests" / "cpp" / "kernels_gpu_main.cpp"}
+TEST_BIN = ROOT / "tests" / "cpp" / "bin"
+
+
+def build_test_programs(verbose: bool = True) -> None:
+    """Compiles the C++ test programs that link librlk.so through the C++
+    header (tests/cpp/*_main.cpp) into tests/cpp/bin/, with an rpath relative
+    to the program so the tree can move (it runs on the GPU box)."""
+    TEST_BIN.mkdir(parents=True, exist_ok=True)
+    for name, src in TEST_PROGRAMS.items():
+        out = TEST_BIN / name
+        subprocess.run([HIPCC, "-O2", "-std=c++17", f"-I{ROOT / 'include'}", str(src), "-o", str(out),
+                        f"-L{PKG}", "-lrlk", "-Wl,-rpath,$ORIGIN/../../../redline_amd"], check=True)
+        if verbose:
+            print(f"built {out}", file=sys.stderr)
+
+
 if __name__ == "__main__":
     build_library(only_changed="--changed" in sys.argv)
+    build_test_programs()
