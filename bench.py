@@ -109,9 +109,33 @@ class LayerData:
         s, m = self.sets[r], self.w.model
         self.K.silu_and_mul(s["gu"], self.T, m.inter, s["act"])
 
-    def step(self, r):
+    def norm_first(self, r):
+        """The layer's first norm: fused_add_rmsnorm(delta=None) on the
+        residual the embedding gather just wrote (llama.cpp:79-80)."""
+        s, m = self.sets[r], self.w.model
+        self.K.fused_add_rmsnorm(s["emb"], None, self.weight, self.T, m.hidden, m.eps, s["normed"])
+
+    def embedding_norm(self, r):
+        """Extension: the gather and the first norm in one launch."""
+        s, m = self.sets[r], self.w.model
+        self.K.embedding_rmsnorm(s["ids"], self.table, self.T, m.hidden, self.weight, m.eps,
+                                 s["emb"], s["normed"])
+
+    def step_plain(self, r):
+        """The reference's launches in its forward-pass order (llama.cpp:79-80,
+        122, 131, 139 with silu_and_mul for the gated projection's epilogue):
+        embedding_lookup, fused_add_rmsnorm(delta=None), rope_and_write_kv,
+        fused_add_rmsnorm(delta), silu_and_mul."""
         self.embedding(r)
+        self.norm_first(r)
+        self.rope(r)
         self.norm(r)
+        self.swiglu(r)
+
+    def step(self, r):
+        """The same layer step with the first two launches fused
+        (embedding_rmsnorm): four launches."""
+        self.embedding_norm(r)
         self.rope(r)
         self.norm(r)
         self.swiglu(r)
@@ -121,6 +145,8 @@ class LayerData:
         m, T = self.w.model, self.T
         return {
             "embedding_lookup": C.bytes_embedding(T, m.hidden),
+            "embedding_rmsnorm": C.bytes_embedding_rmsnorm(T, m.hidden),
+            "fused_add_rmsnorm_nodelta": C.bytes_add_rmsnorm(T, m.hidden, delta=False),
             "fused_add_rmsnorm": C.bytes_add_rmsnorm(T, m.hidden),
             "rope_and_write_kv": C.bytes_rope_kv(T, m.hq, m.hkv, m.head_dim, self.w.kv_int8,
                                                  self.w.kv_scale_f16, self.w.qkv_bias),
@@ -191,14 +217,24 @@ def time_graph(torch, graph, reps):
 
 
 KERNELS = ("embedding_lookup", "fused_add_rmsnorm", "rope_and_write_kv", "silu_and_mul")
+# the launches of the decode step that are not in KERNELS
+STEP_EXTRA = ("embedding_rmsnorm", "fused_add_rmsnorm_nodelta")
 
 
-def per_kernel(torch, data, reps, only=None):
-    fns = {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
-           "rope_and_write_kv": data.rope, "silu_and_mul": data.swiglu}
+def kernel_fns(data):
+    return {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
+            "rope_and_write_kv": data.rope, "silu_and_mul": data.swiglu,
+            "embedding_rmsnorm": data.embedding_norm, "fused_add_rmsnorm_nodelta": data.norm_first}
+
+
+def per_kernel(torch, data, reps, only=None, names=KERNELS):
+    """Per-call time of each kernel: a graph of R back-to-back launches (one
+    per rotating input set), replayed `reps` times between HIP events on the
+    launch stream."""
+    fns = kernel_fns(data)
     nbytes = data.bytes()
     out = {}
-    for name in KERNELS:
+    for name in names:
         if only and name != only:
             continue
         f = fns[name]
@@ -478,7 +514,8 @@ def cpu_baseline(torch, data, seconds=8.0, max_threads=16):
             p(normed), p(qkv), p(pos), p(slot), m.hq, m.hkv, m.head_dim, p(cos), p(sin), p(kc),
             p(vc), p(ks), p(vs), w.block_size, int(w.kv_int8), p(gu), m.inter, p(act))
     nb = data.bytes()
-    step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
+    step_bytes = (nb["embedding_lookup"] + nb["fused_add_rmsnorm_nodelta"] + nb["rope_and_write_kv"] +
+                  nb["fused_add_rmsnorm"] + nb["silu_and_mul"])
     affinity = L.cps_affinity_cores()
 
     def run(threads):
@@ -507,7 +544,8 @@ def cpu_baseline(torch, data, seconds=8.0, max_threads=16):
             "ms_per_step": round(dtm / nm * 1e3, 4),
             "single_thread": {"value": gbs(n1, dt1), "ms_per_step": round(dt1 / n1 * 1e3, 4)},
             "affinity_cores": affinity,
-            "sample": f"{w.key} layer steps (embedding, 2x add+RMSNorm, RoPE+KV, SwiGLU) on one "
+            "sample": f"{w.key} layer steps (embedding, RMSNorm, RoPE+KV, add+RMSNorm, SwiGLU: the "
+                      f"reference's five launches) on one "
                       f"input set: {nm} steps in {dtm:.1f} s on {threads} threads, {n1} steps in "
                       f"{dt1:.1f} s on 1 thread; oracle/cpu_step.cpp (F16C, std::thread rows)"}
 
@@ -582,16 +620,17 @@ def main():
     log(f"setting up {w.key} ({w.model.name}, T={w.num_tokens})")
     data = LayerData(torch, K, w, rotations=args.rotations)
     nb = data.bytes()
-    step_bytes = nb["embedding_lookup"] + 2 * nb["fused_add_rmsnorm"] + nb["rope_and_write_kv"] + nb["silu_and_mul"]
+    step_bytes = nb["embedding_rmsnorm"] + nb["rope_and_write_kv"] + nb["fused_add_rmsnorm"] + nb["silu_and_mul"]
+    plain_bytes = (nb["embedding_lookup"] + nb["fused_add_rmsnorm_nodelta"] + nb["rope_and_write_kv"] +
+                   nb["fused_add_rmsnorm"] + nb["silu_and_mul"])
 
     if args.sweep:
         sweep(torch, data, args.reps, args.only)
         return
 
     if args.profile_calls:
-        fns = {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
-               "rope_and_write_kv": data.rope, "silu_and_mul": data.swiglu}
-        for name in KERNELS:
+        fns = kernel_fns(data)
+        for name in KERNELS + STEP_EXTRA:
             if args.only and name != args.only:
                 continue
             for i in range(args.profile_calls):
@@ -618,12 +657,12 @@ def main():
                           "rotating_input_sets": data.R}))
         return
 
-    result = {}
-    if args.only is None:
-        # K steps = (K // R) replays of a graph holding all R rotating steps,
-        # plus one graph of the remaining K % R steps; warmup (W steps) likewise.
-        full = capture(torch, lambda: [data.step(r) for r in range(data.R)])
-        part = lambda n: capture(torch, lambda: [data.step(r) for r in range(n)]) if n else None  # noqa: E731
+    def time_steps(step):
+        """K timed steps after W warmup steps: (K // R) replays of a graph
+        holding all R rotating steps plus one graph of the remaining K % R
+        steps (warmup likewise), between HIP events on the launch stream."""
+        full = capture(torch, lambda: [step(r) for r in range(data.R)])
+        part = lambda n: capture(torch, lambda: [step(r) for r in range(n)]) if n else None  # noqa: E731
         rem, wrem = part(args.steps % data.R), part(args.warmup % data.R)
         for _ in range(args.warmup // data.R):
             full.replay()
@@ -638,13 +677,27 @@ def main():
             rem.replay()
         end.record()
         torch.cuda.synchronize()
-        ms_step = start.elapsed_time(end) / args.steps
+        ms = start.elapsed_time(end) / args.steps
         del full, rem, wrem
-        value = step_bytes / (ms_step * 1e-3) / 1e9
-        log(f"{w.key} step: {ms_step * 1e3:.2f} us, {value:.1f} GB/s")
-        result.update(ms_per_step=round(ms_step, 5), value=round(value, 2))
+        return ms
 
-    kern = per_kernel(torch, data, args.reps, args.only)
+    result = {}
+    if args.only is None:
+        ms_step = time_steps(data.step)
+        value = step_bytes / (ms_step * 1e-3) / 1e9
+        log(f"{w.key} step (4 launches, embedding_rmsnorm): {ms_step * 1e3:.2f} us, {value:.1f} GB/s")
+        result.update(ms_per_step=round(ms_step, 5), value=round(value, 2))
+        ms_plain = time_steps(data.step_plain)
+        log(f"{w.key} step of the reference's 5 launches: {ms_plain * 1e3:.2f} us, "
+            f"{plain_bytes / (ms_plain * 1e-3) / 1e9:.1f} GB/s")
+        result["step_plain"] = {"us_per_step": round(ms_plain * 1e3, 3),
+                                "gb_per_s": round(plain_bytes / (ms_plain * 1e-3) / 1e9, 1),
+                                "bytes_per_step": plain_bytes,
+                                "launches": "embedding_lookup, fused_add_rmsnorm(delta=None), "
+                                            "rope_and_write_kv, fused_add_rmsnorm, silu_and_mul"}
+
+    kern = per_kernel(torch, data, args.reps, args.only,
+                      KERNELS + (STEP_EXTRA if args.only is None or args.only in STEP_EXTRA else ()))
     rot = data.R
     del data
     torch.cuda.empty_cache()
@@ -711,13 +764,15 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": f"{w.key}: {w.model.name}-shaped decode, batch {w.num_tokens}"
                                if w.key == "C2" else f"{w.key}: {w.model.name}, T={w.num_tokens}",
-                   "step": "embedding_lookup, fused_add_rmsnorm, rope_and_write_kv (FP16 KV), "
-                           "fused_add_rmsnorm, silu_and_mul",
+                   "step": "embedding_rmsnorm (embedding_lookup + fused_add_rmsnorm(delta=None) "
+                           "in one launch), rope_and_write_kv (FP16 KV), fused_add_rmsnorm, "
+                           "silu_and_mul",
                    "global_batch": w.num_tokens, "rotating_input_sets": rot,
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kern,
+        "step_plain": result.get("step_plain"),
         "prefill": extra,
         "decode_attention": attention,
         "prefill_attention": prefill,

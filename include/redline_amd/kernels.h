@@ -140,6 +140,16 @@ inline void fused_add_rmsnorm(half* residual, const half* delta, const half* wei
                                       stream));
 }
 
+// Extension: residual = table[ids]; out = rmsnorm(residual) * weight in one
+// launch (the reference's embedding_lookup + fused_add_rmsnorm(delta = nullptr)
+// pair at the start of the forward pass, llama.cpp:79-80).
+inline void embedding_rmsnorm(const int32_t* ids, const half* table, int n, int hidden,
+                              const half* weight, float eps, half* residual, half* out,
+                              hipStream_t stream) {
+  detail::check(rlk_embedding_rmsnorm(ids, detail::bits(table), n, hidden, detail::bits(weight),
+                                      eps, detail::bits(residual), detail::bits(out), stream));
+}
+
 // out[r, i] = silu(gate_up[r, i]) * gate_up[r, inter + i]
 inline void silu_and_mul(const half* gate_up, int rows, int inter, half* out, hipStream_t stream) {
   detail::check(rlk_silu_and_mul(detail::bits(gate_up), rows, inter, detail::bits(out), stream));

@@ -82,6 +82,17 @@ int rlk_embedding_lookup(const int32_t* ids, const uint16_t* table, int n, int h
 int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta, const uint16_t* weight,
                           int rows, int hidden, float eps, uint16_t* out, hipStream_t stream);
 
+/* Extension, no single counterpart in the reference: residual[t, :] =
+ * table[ids[t], :] and out = RMSNorm(residual) * weight in one launch -- the
+ * same results as the reference's back-to-back embedding_lookup(ids, table,
+ * n, hidden, residual) and fused_add_rmsnorm(residual, NULL, weight, n,
+ * hidden, eps, out) that start its forward pass (src/cuda/model/llama.cpp:79-80),
+ * with one launch and one pass over the rows instead of two.
+ * n <= 0: no-op.  hidden % 8 != 0: RLK_EINVAL.  ids are not bounds-checked. */
+int rlk_embedding_rmsnorm(const int32_t* ids, const uint16_t* table, int n, int hidden,
+                          const uint16_t* weight, float eps, uint16_t* residual, uint16_t* out,
+                          hipStream_t stream);
+
 /* out[r, i] = fp16(fp16(silu(gate_up[r, i])) * gate_up[r, inter + i]).
  * Replaces kernels::silu_and_mul, elementwise.cu:140-145.
  * rows <= 0: no-op.  inter % 8 != 0: RLK_EINVAL. */

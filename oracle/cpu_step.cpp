@@ -1,6 +1,7 @@
-// Multi-threaded CPU port of one layer step of the fused per-layer kernels:
-// embedding gather, residual-add + RMSNorm, RoPE + paged-KV write, residual-
-// add + RMSNorm, SwiGLU.  TEST INFRASTRUCTURE: it is the CPU baseline that
+// Multi-threaded CPU port of one layer step of the fused per-layer kernels, in
+// the reference's forward-pass order (src/cuda/model/llama.cpp:79-80,122,131,
+// 139): embedding gather into `emb`, RMSNorm of that row (no delta), RoPE +
+// paged-KV write, residual-add + RMSNorm, SwiGLU.  TEST INFRASTRUCTURE: it is the CPU baseline that
 // bench.py times next to the GPU (and that tests/test_cpu_step.py checks
 // against the oracle); nothing in the product path links or calls it.
 //
@@ -271,7 +272,7 @@ void cps_layer_step(void* pool_, const int32_t* ids, const uint16_t* table, int 
                     int I, uint16_t* act) {
   Pool& pool = *static_cast<Pool*>(pool_);
   embedding(pool, ids, table, T, H, emb);
-  add_rmsnorm(pool, residual, delta, w_norm, T, H, eps, normed);
+  add_rmsnorm(pool, emb, nullptr, w_norm, T, H, eps, normed);
   rope_kv(pool, qkv, positions, slots, T, Hq, Hkv, D, cos_t, sin_t, k_cache, v_cache, k_scale,
           v_scale, bs, int8);
   add_rmsnorm(pool, residual, delta, w_norm, T, H, eps, normed);

@@ -465,9 +465,10 @@ void orc_paged_attention_prefill(const uint16_t* q, int q_stride, uint16_t* out,
   }
 }
 
-/* One layer's hot path on one batch, as a single call for CPU timing:
- * embedding gather, residual add + RMSNorm (attention input), RoPE + KV write,
- * residual add + RMSNorm (FFN input), SwiGLU. */
+/* One layer's hot path on one batch, as a single call, in the reference's
+ * forward-pass order (src/cuda/model/llama.cpp:79-80,122,131,139): embedding
+ * gather into emb, RMSNorm of emb (no delta), RoPE + KV write, residual add +
+ * RMSNorm (FFN input), SwiGLU. */
 void orc_layer_step(const int32_t* ids, const uint16_t* table, int T, int H, uint16_t* emb,
                     uint16_t* residual, const uint16_t* delta, const uint16_t* w_norm, float eps,
                     uint16_t* normed, uint16_t* qkv, const int32_t* positions,
@@ -476,7 +477,7 @@ void orc_layer_step(const int32_t* ids, const uint16_t* table, int T, int H, uin
                     float* v_scale, int bs, int int8, const uint16_t* gate_up, int I,
                     uint16_t* act) {
   orc_embedding_lookup(ids, table, T, H, emb);
-  orc_fused_add_rmsnorm(residual, delta, w_norm, T, H, eps, normed);
+  orc_fused_add_rmsnorm(emb, NULL, w_norm, T, H, eps, normed);
   orc_rope_and_write_kv(qkv, positions, slots, T, Hq, Hkv, D, cos_t, sin_t, k_cache, v_cache,
                         k_scale, v_scale, bs, int8);
   orc_fused_add_rmsnorm(residual, delta, w_norm, T, H, eps, normed);

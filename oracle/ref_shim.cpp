@@ -10,6 +10,7 @@
 #include "core/batch_builder.h"
 #include "core/common.h"
 #include "core/model_config.h"
+#include "cpu/random_model.h"
 
 using namespace redline;
 
@@ -100,6 +101,27 @@ void ref_meta_layout(const int* shape7, int max_blocks, size_t* out19) {
                         m.param_row,   m.temperature, m.top_k,        m.top_p,
                         m.seed_lo,     m.seed_hi,     m.total_words};
   std::memcpy(out19, v, sizeof(v));
+}
+
+// The reference's weight quantisers (src/cpu/random_model.cpp:99-140): w is
+// fp32 [n, k]; outputs are sized by the caller.
+void ref_quantize_int8_rows(const float* w, int n, int k, int8_t* q, uint16_t* scales) {
+  std::vector<int8_t> qv;
+  std::vector<uint16_t> sv;
+  quantize_int8_rows(std::vector<float>(w, w + static_cast<size_t>(n) * k), n, k, &qv, &sv);
+  std::memcpy(q, qv.data(), qv.size());
+  std::memcpy(scales, sv.data(), sv.size() * 2);
+}
+
+void ref_quantize_int4_groups(const float* w, int n, int k, int group_size, uint8_t* packed,
+                              uint16_t* scales, uint16_t* offsets) {
+  std::vector<uint8_t> pv;
+  std::vector<uint16_t> sv, ov;
+  quantize_int4_groups(std::vector<float>(w, w + static_cast<size_t>(n) * k), n, k, group_size,
+                       &pv, &sv, &ov);
+  std::memcpy(packed, pv.data(), pv.size());
+  std::memcpy(scales, sv.data(), sv.size() * 2);
+  std::memcpy(offsets, ov.data(), ov.size() * 2);
 }
 
 }  // extern "C"

@@ -109,6 +109,7 @@ _SIGNATURES = {
     "rlk_set_tune_knob": (_I, [C.c_char_p, _I, _I]),
     "rlk_embedding_lookup": (_I, [_P, _P, _I, _I, _P, _P]),
     "rlk_fused_add_rmsnorm": (_I, [_P, _P, _P, _I, _I, C.c_float, _P, _P]),
+    "rlk_embedding_rmsnorm": (_I, [_P, _P, _I, _I, _P, C.c_float, _P, _P, _P]),
     "rlk_silu_and_mul": (_I, [_P, _I, _I, _P, _P]),
     "rlk_silu_and_mul_interleaved": (_I, [_P, _I, _I, _P, _P]),
     "rlk_gather_rows": (_I, [_P, _P, _I, _I, _P, _P]),

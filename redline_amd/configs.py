@@ -154,6 +154,11 @@ def bytes_add_rmsnorm(T, H, delta=True):
     return T * (8 * H if delta else 4 * H) + 2 * H
 
 
+def bytes_embedding_rmsnorm(T, H):
+    """ids and table rows read, residual and normed rows written, weight once."""
+    return T * (4 + 6 * H) + 2 * H
+
+
 def bytes_swiglu(T, I):
     return T * 6 * I
 

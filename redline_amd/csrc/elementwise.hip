@@ -98,24 +98,33 @@ int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* ds
 // re-read.  Rounding points follow elementwise.cu:45,52,61: the residual sum
 // is rounded to fp16, the sum of squares is fp32, x * inv is rounded to fp16
 // before the fp16 weight multiply.
-template <int TPR, int NV, bool kDelta, bool NT>
+// Where the row comes from: the residual in place (kNoDelta), the residual
+// plus delta written back (kDelta), or an embedding-table row table[ids[row]]
+// written to the residual (kGather: embedding_lookup followed by
+// fused_add_rmsnorm with delta == nullptr, in one pass).
+enum NormSrc { kNoDelta = 0, kDelta = 1, kGather = 2 };
+
+template <int TPR, int NV, int kSrc, bool NT>
 __global__ __launch_bounds__(TPR) void add_rmsnorm_kernel(
     u32x4* __restrict__ residual, const u32x4* __restrict__ delta,
     const u32x4* __restrict__ weight, int vecs, float hidden, float eps,
-    u32x4* __restrict__ out) {
+    u32x4* __restrict__ out, const int32_t* __restrict__ ids) {
   constexpr int kWaves = TPR / kWave;
   __shared__ float partial[kWaves];
   const int lt = threadIdx.x;
   const int64_t row = blockIdx.x;
   u32x4* res = residual + row * vecs;
+  // kGather: `delta` is the embedding table
+  const u32x4* src =
+      kSrc == kGather ? delta + static_cast<int64_t>(static_cast<uint32_t>(ids[row])) * vecs : res;
 
   u32x4 rv[NV], dv[NV], wv[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = lt + k * TPR;
     const bool ok = i < vecs;
-    rv[k] = ok ? ld16<NT>(res + i) : u32x4{0, 0, 0, 0};
-    if constexpr (kDelta) dv[k] = ok ? ld16<NT>(delta + row * vecs + i) : u32x4{0, 0, 0, 0};
+    rv[k] = ok ? ld16<NT>(src + i) : u32x4{0, 0, 0, 0};
+    if constexpr (kSrc == kDelta) dv[k] = ok ? ld16<NT>(delta + row * vecs + i) : u32x4{0, 0, 0, 0};
     wv[k] = ok ? weight[i] : u32x4{0, 0, 0, 0};  // shared by all rows: cached load, issued early
   }
   f32x8 x[NV];
@@ -123,10 +132,12 @@ __global__ __launch_bounds__(TPR) void add_rmsnorm_kernel(
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     x[k] = unpack8(rv[k]);
-    if constexpr (kDelta) {
+    const int i = lt + k * TPR;
+    if constexpr (kSrc == kDelta) {
       x[k] = round_f16(x[k] + unpack8(dv[k]));
-      const int i = lt + k * TPR;
       if (i < vecs) st16<NT>(res + i, pack8(x[k]));
+    } else if constexpr (kSrc == kGather) {
+      if (i < vecs) st16<NT>(res + i, rv[k]);  // the gathered row, bit for bit
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += x[k][j] * x[k][j];
@@ -150,20 +161,25 @@ __global__ __launch_bounds__(TPR) void add_rmsnorm_kernel(
 
 // Rows wider than the register-resident variants cover: one block per row,
 // two passes (the second re-reads the residual from cache).
-template <bool kDelta>
+template <int kSrc>
 __global__ __launch_bounds__(256) void add_rmsnorm_wide_kernel(
     u32x4* __restrict__ residual, const u32x4* __restrict__ delta,
     const u32x4* __restrict__ weight, int vecs, float hidden, float eps,
-    u32x4* __restrict__ out) {
+    u32x4* __restrict__ out, const int32_t* __restrict__ ids) {
   __shared__ float partial[256 / kWave];
   const int64_t row = blockIdx.x;
   u32x4* res = residual + row * vecs;
+  const u32x4* src =
+      kSrc == kGather ? delta + static_cast<int64_t>(static_cast<uint32_t>(ids[row])) * vecs : res;
   float ss = 0.f;
   for (int i = threadIdx.x; i < vecs; i += 256) {
-    f32x8 x = unpack8(res[i]);
-    if constexpr (kDelta) {
+    const u32x4 r = src[i];
+    f32x8 x = unpack8(r);
+    if constexpr (kSrc == kDelta) {
       x = round_f16(x + unpack8(delta[row * vecs + i]));
       res[i] = pack8(x);
+    } else if constexpr (kSrc == kGather) {
+      res[i] = r;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
@@ -182,22 +198,29 @@ __global__ __launch_bounds__(256) void add_rmsnorm_wide_kernel(
 
 struct NormArgs {
   u32x4* res;
-  const u32x4* del;
+  const u32x4* del;  // delta, or the embedding table (ids != nullptr)
   const u32x4* w;
   int rows, vecs;
   float hidden, eps;
   u32x4* out;
+  const int32_t* ids;  // non-null: gather the rows from the table
 };
+
+int norm_src(const NormArgs& a) {
+  return a.ids != nullptr ? kGather : (a.del != nullptr ? kDelta : kNoDelta);
+}
 
 template <int TPR, int NV, bool NT>
 void launch_norm_tn(const NormArgs& a, hipStream_t stream) {
-  if (a.del != nullptr) {
-    add_rmsnorm_kernel<TPR, NV, true, NT>
-        <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out);
-  } else {
-    add_rmsnorm_kernel<TPR, NV, false, NT>
-        <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out);
+#define RLK_NORM_LAUNCH(S)                                                                       \
+  add_rmsnorm_kernel<TPR, NV, S, NT>                                                             \
+      <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out, a.ids)
+  switch (norm_src(a)) {
+    case kDelta: RLK_NORM_LAUNCH(kDelta); break;
+    case kGather: RLK_NORM_LAUNCH(kGather); break;
+    default: RLK_NORM_LAUNCH(kNoDelta); break;
   }
+#undef RLK_NORM_LAUNCH
 }
 
 // Register-resident variants: NV vectors (8 halves each) per lane.
@@ -239,6 +262,29 @@ bool launch_norm_nt(int tpr, const NormArgs& a, hipStream_t stream) {
     case 512: return launch_norm_t<512, NT>(nv, a, stream);
     default: return launch_norm_t<256, NT>(nv, a, stream);
   }
+}
+
+// Lanes per row: enough for one 16-byte vector per lane up to 512 lanes
+// (eight waves); wider rows keep several vectors per lane in registers, and
+// rows past 512 x 16 vectors take the two-pass kernel.  Non-temporal accesses
+// measured faster at every batch size.
+void launch_norm(const NormArgs& a, hipStream_t stream) {
+  int tpr = 64;
+  while (tpr < 512 && tpr < a.vecs) tpr *= 2;
+  tpr = tune_knob(kNormTpr, tpr);
+  const bool nt = tune_knob(kNormNt, 1) != 0;
+  bool launched = nt ? launch_norm_nt<true>(tpr, a, stream) : launch_norm_nt<false>(tpr, a, stream);
+  if (!launched) launched = launch_norm_nt<false>(512, a, stream);
+  if (launched) return;
+#define RLK_NORM_WIDE(S)                                                                   \
+  add_rmsnorm_wide_kernel<S><<<a.rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, \
+                                                         a.eps, a.out, a.ids)
+  switch (norm_src(a)) {
+    case kDelta: RLK_NORM_WIDE(kDelta); break;
+    case kGather: RLK_NORM_WIDE(kGather); break;
+    default: RLK_NORM_WIDE(kNoDelta); break;
+  }
+#undef RLK_NORM_WIDE
 }
 
 // ------------------------------------------------------------------ SwiGLU
@@ -366,23 +412,33 @@ extern "C" int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta,
   a.hidden = static_cast<float>(hidden);
   a.eps = eps;
   a.out = reinterpret_cast<u32x4*>(out);
-  // Lanes per row: enough for one 16-byte vector per lane up to 512 lanes
-  // (eight waves); wider rows keep several vectors per lane in registers.
-  // Non-temporal accesses measured faster at every batch size.
-  int tpr = 64;
-  while (tpr < 512 && tpr < a.vecs) tpr *= 2;
-  tpr = tune_knob(kNormTpr, tpr);
-  const bool nt = tune_knob(kNormNt, 1) != 0;
-  bool launched = nt ? launch_norm_nt<true>(tpr, a, stream) : launch_norm_nt<false>(tpr, a, stream);
-  if (!launched) launched = launch_norm_nt<false>(512, a, stream);
-  if (!launched) {
-    if (a.del != nullptr) {
-      add_rmsnorm_wide_kernel<true><<<rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, eps, a.out);
-    } else {
-      add_rmsnorm_wide_kernel<false><<<rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, eps, a.out);
-    }
-  }
+  a.ids = nullptr;
+  launch_norm(a, stream);
   return launch_status("fused_add_rmsnorm");
+}
+
+extern "C" int rlk_embedding_rmsnorm(const int32_t* ids, const uint16_t* table, int n, int hidden,
+                                     const uint16_t* weight, float eps, uint16_t* residual,
+                                     uint16_t* out, hipStream_t stream) {
+  if (n <= 0) return RLK_OK;
+  if (hidden <= 0 || hidden % 8 != 0)
+    return fail(RLK_EINVAL, "embedding_rmsnorm: hidden size must be a multiple of 8 (got %d)",
+                hidden);
+  if (ids == nullptr || table == nullptr || weight == nullptr || residual == nullptr ||
+      out == nullptr)
+    return fail(RLK_EINVAL, "embedding_rmsnorm: null pointer argument");
+  NormArgs a;
+  a.res = reinterpret_cast<u32x4*>(residual);
+  a.del = reinterpret_cast<const u32x4*>(table);
+  a.w = reinterpret_cast<const u32x4*>(weight);
+  a.rows = n;
+  a.vecs = hidden / 8;
+  a.hidden = static_cast<float>(hidden);
+  a.eps = eps;
+  a.out = reinterpret_cast<u32x4*>(out);
+  a.ids = ids;
+  launch_norm(a, stream);
+  return launch_status("embedding_rmsnorm");
 }
 
 extern "C" int rlk_silu_and_mul(const uint16_t* gate_up, int rows, int inter, uint16_t* out,

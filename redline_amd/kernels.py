@@ -17,7 +17,7 @@ from . import _lib
 from ._lib import KVLayerView, check, lib
 
 __all__ = [
-    "embedding_lookup", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
+    "embedding_lookup", "embedding_rmsnorm", "fused_add_rmsnorm", "silu_and_mul", "silu_and_mul_interleaved",
     "gather_rows", "resolve_input_ids", "rope_and_write_kv", "rope_and_write_kv_ex", "KVDType",
     "KVCache", "SCALE_F32", "SCALE_F16", "paged_attention_decode", "paged_attention_decode_ex",
     "attention_params",
@@ -84,6 +84,19 @@ def fused_add_rmsnorm(residual, delta, weight, rows, hidden, eps, out, stream=No
     check(lib().rlk_fused_add_rmsnorm(
         _ptr(residual, torch.float16, "residual"), _ptr(delta, torch.float16, "delta", True),
         _ptr(weight, torch.float16, "weight"), rows, hidden, float(eps),
+        _ptr(out, torch.float16, "out"), _stream(stream)))
+
+
+def embedding_rmsnorm(ids, table, n, hidden, weight, eps, residual, out, stream=None):
+    """Extension: residual[t, :] = table[ids[t], :]; out = rmsnorm(residual) *
+    weight, in one launch -- the reference's embedding_lookup followed by
+    fused_add_rmsnorm(delta=None) (llama.cpp:79-80), same results."""
+    if n > 0:
+        _need(ids, n, "ids"); _need(residual, n * hidden, "residual"); _need(out, n * hidden, "out")
+        _need(weight, hidden, "weight")
+    check(lib().rlk_embedding_rmsnorm(
+        _ptr(ids, torch.int32, "ids"), _ptr(table, torch.float16, "table"), n, hidden,
+        _ptr(weight, torch.float16, "weight"), float(eps), _ptr(residual, torch.float16, "residual"),
         _ptr(out, torch.float16, "out"), _stream(stream)))
 
 

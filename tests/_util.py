@@ -59,10 +59,35 @@ def int8_linear(rng: np.random.Generator, n: int, k: int, std: float = 0.05):
     fp16(amax / 127), codes = clamp(rint(w / scale), -127, 127) against the stored
     scale.  Returns (codes int8 [n, k], scales fp16 [n], float64 W = codes * scale)."""
     w = (rng.standard_normal((n, k)) * std).astype(np.float32)
+    q, s = int8_quantize_rows(w)
+    return q, s, q.astype(np.float64) * s.astype(np.float64)[:, None]
+
+
+def int8_quantize_rows(w: np.ndarray):
+    """quantize_int8_rows (src/cpu/random_model.cpp:99-115) in numpy: fp32 w
+    [n, k] -> (codes int8 [n, k], scales fp16 [n])."""
+    w = np.asarray(w, np.float32)
     amax = np.abs(w).max(axis=1)
     s = np.where(amax > 0, amax / np.float32(127), np.float32(1)).astype(np.float16)
     q = np.clip(np.rint(w / s.astype(np.float32)[:, None]), -127, 127).astype(np.int8)
-    return q, s, q.astype(np.float64) * s.astype(np.float64)[:, None]
+    return q, s
+
+
+def int4_quantize_groups(w: np.ndarray, group_size: int):
+    """quantize_int4_groups (src/cpu/random_model.cpp:118-140) in numpy: per
+    group scale = fp16((hi - lo) / 15) (1 when hi == lo), offset = fp16(lo),
+    code = clamp(rint((x - offset) / scale), 0, 15) against the stored fp16
+    values, two codes per byte with the even column in the low nibble.
+    Returns (packed uint8 [n, k/2], scales fp16 [n, k/g], offsets fp16 [n, k/g])."""
+    w = np.asarray(w, np.float32)
+    n, k = w.shape
+    x = w.reshape(n, k // group_size, group_size)
+    lo, hi = x.min(axis=2), x.max(axis=2)
+    s = np.where(hi > lo, (hi - lo) / np.float32(15), np.float32(1)).astype(np.float16)
+    o = lo.astype(np.float16)
+    q = np.clip(np.rint((x - o.astype(np.float32)[..., None]) / s.astype(np.float32)[..., None]),
+                0, 15).astype(np.uint8).reshape(n, k)
+    return (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8), s, o
 
 
 def int4_linear(rng: np.random.Generator, n: int, k: int, group_size: int, dense: bool = True):

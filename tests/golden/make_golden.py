@@ -7,6 +7,8 @@ Fixtures (inputs and the reference's outputs only):
   half_f2h.npz       float32 inputs -> reference float_to_half_bits
   rope_tables.npz    inv_freq and cos/sin rows at selected positions for the
                      theta / head_dim / scaling cases of the workloads
+  quantize.npz       weights -> reference quantize_int8_rows / quantize_int4_groups
+                     (src/cpu/random_model.cpp:99-140)
   batch_meta.npz     BatchBuilder metadata for the KAT case of
                      tests/cpp/test_core.cpp:334-386, the graph-padding case
                      (:388-404), and the C2 / C3 workload batches (per-token
@@ -146,12 +148,43 @@ def batch_fixture(R):
     np.savez_compressed(OUT / "batch_meta.npz", **arrays)
 
 
+def quantize_fixture(R):
+    """The reference's weight quantisers on seeded weights, including rows and
+    groups that are constant (amax 0 / hi == lo) and values on exact .5 code
+    ties, for the GEMV tests' weight builders."""
+    rng = np.random.default_rng(99)
+    arrays = {}
+    w8 = (rng.standard_normal((37, 200)) * 0.05).astype(np.float32)
+    w8[3] = 0.0
+    w8[4, :] = 0.25
+    w8[5, :8] = np.float32(127.0) * np.array([1, -1, 0.5, -0.5, 1.5, -2.5, 0, 126.5], np.float32) / 127
+    q8 = np.empty(w8.shape, np.int8)
+    s8 = np.empty(w8.shape[0], np.uint16)
+    R.ref_quantize_int8_rows(p(w8), *w8.shape, p(q8), p(s8))
+    arrays.update(w8=w8, q8=q8, s8=s8)
+    for g in (32, 64, 128):
+        w4 = (rng.standard_normal((20, 256)) * 0.05).astype(np.float32)
+        w4[2, :g] = 0.125  # hi == lo
+        w4[3, :g] = np.linspace(0, 15, g).astype(np.float32)  # ties at x.5 codes
+        n, k = w4.shape
+        packed = np.empty((n, k // 2), np.uint8)
+        s4 = np.empty((n, k // g), np.uint16)
+        o4 = np.empty_like(s4)
+        R.ref_quantize_int4_groups(p(w4), n, k, g, p(packed), p(s4), p(o4))
+        arrays.update({f"w4_{g}": w4, f"packed_{g}": packed, f"s4_{g}": s4, f"o4_{g}": o4})
+    np.savez_compressed(OUT / "quantize.npz", **arrays)
+
+
 def main():
     oracle.build(ref=True)
     R = oracle.ref()
+    if sys.argv[1:] == ["quantize"]:  # only the quantiser fixture
+        quantize_fixture(R)
+        return
     half_fixture(R)
     rope_fixture(R)
     batch_fixture(R)
+    quantize_fixture(R)
     for f in sorted(OUT.glob("*.npz")):
         print(f.name, f.stat().st_size)
 

@@ -62,6 +62,38 @@ def test_embedding_full_vocab_zipf(torch_cuda):
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
 
 
+@pytest.mark.parametrize("vocab,hidden,n,eps", [(50, 64, 4, 1e-5), (4096, 4096, 32, 1e-5),
+                                                (997, 3584, 300, 1e-6), (64, 8, 5, 1e-5),
+                                                (300, 4104, 33, 1e-5), (40, 73728, 3, 1e-5)])
+def test_embedding_rmsnorm_matches_two_calls(torch_cuda, vocab, hidden, n, eps):
+    """The fused extension equals embedding_lookup + fused_add_rmsnorm(delta =
+    None) bit for bit (the same kernel arithmetic), and the oracle's composition
+    of the two: residual bit-exact, out within fp16 tolerance.  Covers H = 4096
+    (C2's shape and table), the Qwen2 width, H = 8, a ragged 513-vector row and
+    the two-pass width (73728)."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    say(f"embedding_rmsnorm vocab={vocab} hidden={hidden} n={n}")
+    rng = np.random.default_rng(vocab + hidden + n)
+    table = randn_f16(rng, (vocab, hidden), 0.02)
+    w = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float16)
+    ids = rng.integers(0, vocab, n, dtype=np.int32)
+    ids[0], ids[-1] = vocab - 1, 0
+    d_ids, d_table, d_w = dev(torch, ids), dev(torch, table), dev(torch, w)
+    res = torch.empty((n, hidden), dtype=torch.float16, device="cuda")
+    out = torch.empty_like(res)
+    K.embedding_rmsnorm(d_ids, d_table, n, hidden, d_w, eps, res, out)
+    res2, out2 = torch.empty_like(res), torch.empty_like(res)
+    K.embedding_lookup(d_ids, d_table, n, hidden, res2)
+    K.fused_add_rmsnorm(res2, None, d_w, n, hidden, eps, out2)
+    assert torch.equal(res.view(torch.int16), res2.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    want_res = oracle.embedding_lookup(ids, table, hidden)
+    _, want = oracle.fused_add_rmsnorm(want_res, None, w, eps)
+    assert_bits_equal(host(res), want_res, "residual")
+    assert_close_f16(host(out), want, what="out")
+
+
 def test_gather_rows_and_resolve(torch_cuda):
     torch = torch_cuda
     from redline_amd import kernels as K

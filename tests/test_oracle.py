@@ -677,3 +677,41 @@ def test_gemv_w4_swiglu_is_interleaved_silu_of_fp16_outputs():
     ok = safe(y[:, 0::2]) & safe(y[:, 1::2])
     assert ok.mean() > 0.99
     np.testing.assert_array_equal(fused.view(np.uint16)[ok], unfused.view(np.uint16)[ok])
+
+
+# ------------------------------------------------- GEMV weight quantisers
+
+def test_weight_quantisers_match_reference(golden):
+    """The GEMV tests' weight builders (tests/_util.py) quantise exactly as the
+    reference's quantize_int8_rows / quantize_int4_groups
+    (src/cpu/random_model.cpp:99-140): codes, packing and fp16 scales/offsets
+    bit for bit, on the reference's own output (tests/golden/quantize.npz)."""
+    from tests._util import int4_quantize_groups, int8_quantize_rows
+    z = golden("quantize.npz")
+    q, s = int8_quantize_rows(z["w8"])
+    assert np.array_equal(q, z["q8"])
+    assert np.array_equal(s.view(np.uint16), z["s8"])
+    for g in (32, 64, 128):
+        packed, s4, o4 = int4_quantize_groups(z[f"w4_{g}"], g)
+        assert np.array_equal(packed, z[f"packed_{g}"]), g
+        assert np.array_equal(s4.view(np.uint16), z[f"s4_{g}"]), g
+        assert np.array_equal(o4.view(np.uint16), z[f"o4_{g}"]), g
+
+
+@pytest.mark.skipif(not oracle.has_ref(), reason="compiled reference core not present")
+def test_weight_quantisers_match_compiled_reference_random():
+    from tests._util import int4_quantize_groups, int8_quantize_rows
+    R = oracle.ref()
+    rng = np.random.default_rng(5)
+    for n, k, g in ((64, 512, 128), (9, 96, 32), (33, 1024, 256)):
+        w = (rng.standard_normal((n, k)) * rng.uniform(0.01, 1.0)).astype(np.float32)
+        q8, s8 = np.empty((n, k), np.int8), np.empty(n, np.uint16)
+        R.ref_quantize_int8_rows(oracle.p(w), n, k, oracle.p(q8), oracle.p(s8))
+        q, s = int8_quantize_rows(w)
+        assert np.array_equal(q, q8) and np.array_equal(s.view(np.uint16), s8)
+        pk, s4, o4 = (np.empty((n, k // 2), np.uint8), np.empty((n, k // g), np.uint16),
+                      np.empty((n, k // g), np.uint16))
+        R.ref_quantize_int4_groups(oracle.p(w), n, k, g, oracle.p(pk), oracle.p(s4), oracle.p(o4))
+        a, b, c = int4_quantize_groups(w, g)
+        assert np.array_equal(a, pk) and np.array_equal(b.view(np.uint16), s4)
+        assert np.array_equal(c.view(np.uint16), o4)
