@@ -254,7 +254,8 @@ SWEEP_KNOBS = {
     "embedding_lookup": {"RLK_TUNE_GATHER_BS": [64, 128, 256], "RLK_TUNE_GATHER_NT": [0, 1]},
     "fused_add_rmsnorm": {"RLK_TUNE_NORM_TPR": [64, 128, 256, 512], "RLK_TUNE_NORM_NT": [0, 1]},
     "silu_and_mul": {"RLK_TUNE_SWIGLU_BS": [64, 128, 256], "RLK_TUNE_SWIGLU_NT": [0, 1]},
-    "rope_and_write_kv": {"RLK_TUNE_ROPE_WPT": [1, 2, 4, 5, 6, 8]},
+    "rope_and_write_kv": {"RLK_TUNE_ROPE_UNROLL": [1, 2], "RLK_TUNE_ROPE_WPT": [1, 2, 3, 4, 5, 6, 8]},
+    "embedding_lookup_vpl": {"RLK_TUNE_GATHER_VPL": [1, 2, 4, 8], "RLK_TUNE_GATHER_BS": [64, 128, 256]},
 }
 
 
@@ -263,14 +264,15 @@ def sweep(torch, data, reps, only=None):
     (the RLK_TUNE_* overrides, set through rlk_set_tune_knob)."""
     import itertools
     from redline_amd._lib import set_tune_knob
-    for kern, knobs in SWEEP_KNOBS.items():
+    for key, knobs in SWEEP_KNOBS.items():
+        kern = key.removesuffix("_vpl")
         if only and kern != only:
             continue
         names = list(knobs)
         for vals in itertools.product(*knobs.values()):
             for n, v in zip(names, vals):
                 set_tune_knob(n, v)
-            r = per_kernel(torch, data, reps, kern)[kern]
+            r = per_kernel(torch, data, reps, kern, names=(kern,))[kern]
             print(json.dumps({"workload": data.w.key, "kernel": kern, "knobs": dict(zip(names, vals)),
                               "us_per_call": r["us_per_call"], "gb_per_s": r["gb_per_s"]}),
                   flush=True)

@@ -61,14 +61,61 @@ __global__ __launch_bounds__(BS) void gather_rows_kernel(const int32_t* __restri
   st16<NT>(dst + g, ld16<NT>(src + srow * vecs + col));
 }
 
-template <int BS>
-void launch_gather_bs(bool nt, uint64_t blocks, const int32_t* idx, const u32x4* s, uint32_t vecs,
-                      uint32_t total, u32x4* d, hipStream_t stream) {
-  if (nt) {
-    gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, total, d);
-  } else {
-    gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, total, d);
+// V vectors per lane: a workgroup covers BS * V consecutive vectors, lane l
+// the vectors l, l + BS, ... (each step one coalesced 16-byte access per
+// lane); all V loads are issued before the first store, so each wave keeps V
+// KiB in flight.
+template <int BS, int V, bool NT>
+__global__ __launch_bounds__(BS) void gather_rows_v_kernel(const int32_t* __restrict__ idx,
+                                                           const u32x4* __restrict__ src,
+                                                           uint32_t vecs, uint32_t total,
+                                                           u32x4* __restrict__ dst) {
+  const uint32_t base = blockIdx.x * (BS * V) + threadIdx.x;
+  u32x4 v[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const uint32_t g = base + k * BS;
+    if (g < total) {
+      const uint32_t row = g / vecs;
+      const uint32_t col = g - row * vecs;
+      const uint64_t srow = idx != nullptr ? static_cast<uint32_t>(idx[row]) : row;
+      v[k] = ld16<NT>(src + srow * vecs + col);
+    }
   }
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const uint32_t g = base + k * BS;
+    if (g < total) st16<NT>(dst + g, v[k]);
+  }
+}
+
+template <int BS>
+void launch_gather_bs(bool nt, int vpl, uint64_t total, const int32_t* idx, const u32x4* s,
+                      uint32_t vecs, u32x4* d, hipStream_t stream) {
+  const uint32_t t32 = static_cast<uint32_t>(total);
+#define RLK_GATHER_V(V)                                                                       \
+  {                                                                                           \
+    const uint64_t blocks = (total + BS * V - 1) / (BS * V);                                  \
+    if (nt) {                                                                                 \
+      gather_rows_v_kernel<BS, V, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);     \
+    } else {                                                                                  \
+      gather_rows_v_kernel<BS, V, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);    \
+    }                                                                                         \
+  }
+  switch (vpl) {
+    case 2: RLK_GATHER_V(2) break;
+    case 4: RLK_GATHER_V(4) break;
+    case 8: RLK_GATHER_V(8) break;
+    default: {
+      const uint64_t blocks = (total + BS - 1) / BS;
+      if (nt) {
+        gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
+      } else {
+        gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
+      }
+    }
+  }
+#undef RLK_GATHER_V
 }
 
 int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* dst,
@@ -78,14 +125,13 @@ int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* ds
     return fail(RLK_EINVAL, "%s: %d rows x %d vectors exceed one launch; split the call", what, n,
                 vecs);
   const FlatPolicy p = pick_flat(total >= (1u << 20) ? 256 : 128, kGatherBs, kGatherNt);
-  const uint64_t blocks = (total + p.bs - 1) / p.bs;
+  const int vpl = tune_knob(kGatherVpl, 1);
   const auto* s = static_cast<const u32x4*>(src);
   auto* d = static_cast<u32x4*>(dst);
-  const uint32_t t32 = static_cast<uint32_t>(total);
   switch (p.bs) {
-    case 128: launch_gather_bs<128>(p.nt, blocks, idx, s, vecs, t32, d, stream); break;
-    case 256: launch_gather_bs<256>(p.nt, blocks, idx, s, vecs, t32, d, stream); break;
-    default: launch_gather_bs<64>(p.nt, blocks, idx, s, vecs, t32, d, stream); break;
+    case 128: launch_gather_bs<128>(p.nt, vpl, total, idx, s, vecs, d, stream); break;
+    case 256: launch_gather_bs<256>(p.nt, vpl, total, idx, s, vecs, d, stream); break;
+    default: launch_gather_bs<64>(p.nt, vpl, total, idx, s, vecs, d, stream); break;
   }
   return launch_status(what);
 }

@@ -45,6 +45,26 @@ def test_embedding_bit_exact(torch_cuda, vocab, hidden, n):
     assert_bits_equal(host(out), oracle.embedding_lookup(ids, table, hidden), "embedding")
 
 
+@pytest.mark.parametrize("vpl", [2, 4, 8])
+@pytest.mark.parametrize("bs", [64, 256])
+def test_embedding_vectors_per_lane(torch_cuda, vpl, bs):
+    """The gather with several 16-byte vectors per lane (launch-policy knob)
+    is bit-exact, including a ragged final workgroup and rows narrower than a
+    workgroup's span."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    from redline_amd._lib import tune_knob
+    say(f"embedding vpl={vpl} bs={bs}")
+    rng = np.random.default_rng(vpl * 7 + bs)
+    for vocab, hidden, n in ((1000, 4096, 37), (64, 8, 5), (300, 4104, 129)):
+        table = randn_f16(rng, (vocab, hidden), 0.02)
+        ids = rng.integers(0, vocab, n, dtype=np.int32)
+        out = torch.empty((n, hidden), dtype=torch.float16, device="cuda")
+        with tune_knob("RLK_TUNE_GATHER_VPL", vpl), tune_knob("RLK_TUNE_GATHER_BS", bs):
+            K.embedding_lookup(dev(torch, ids), dev(torch, table), n, hidden, out)
+        assert_bits_equal(host(out), oracle.embedding_lookup(ids, table, hidden), "embedding")
+
+
 def test_embedding_full_vocab_zipf(torch_cuda):
     """Qwen2-7B-shaped gather (152064 x 3584) with Zipf(1.1) ids: every row
     equals the table row it names (size-independent check on the device)."""
