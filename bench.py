@@ -250,12 +250,33 @@ def per_kernel(torch, data, reps, only=None, names=KERNELS):
     return out
 
 
+def launch_durations(torch, fn, R, n=400):
+    """Average duration (us) of one launch of fn(r) on its own: each launch is
+    bracketed by a pair of HIP events on the launch stream (torch's current
+    stream), with eager launches, so the GPU runs it in isolation -- the
+    quantity a profiler's kernel trace records per dispatch.  Also returns the
+    median."""
+    for r in range(min(R, 8)):
+        fn(r)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    for i, (a, b) in enumerate(ev):
+        a.record()
+        fn(i % R)
+        b.record()
+    torch.cuda.synchronize()
+    us = np.array([a.elapsed_time(b) * 1e3 for a, b in ev])
+    return float(us.mean()), float(np.median(us))
+
+
 SWEEP_KNOBS = {
     "embedding_lookup": {"RLK_TUNE_GATHER_BS": [64, 128, 256], "RLK_TUNE_GATHER_NT": [0, 1]},
     "fused_add_rmsnorm": {"RLK_TUNE_NORM_TPR": [64, 128, 256, 512], "RLK_TUNE_NORM_NT": [0, 1]},
     "silu_and_mul": {"RLK_TUNE_SWIGLU_BS": [64, 128, 256], "RLK_TUNE_SWIGLU_NT": [0, 1]},
-    "rope_and_write_kv": {"RLK_TUNE_ROPE_UNROLL": [1, 2], "RLK_TUNE_ROPE_WPT": [1, 2, 3, 4, 5, 6, 8]},
-    "embedding_lookup_vpl": {"RLK_TUNE_GATHER_VPL": [1, 2, 4, 8], "RLK_TUNE_GATHER_BS": [64, 128, 256]},
+    "rope_and_write_kv": {"RLK_TUNE_ROPE_WPT": [1, 2, 3, 4, 5, 6, 8]},
+    "embedding_lookup_sp": {"RLK_TUNE_STORE_POL": [0, 1, 2, 3], "RLK_TUNE_GATHER_BS": [128, 256]},
+    "silu_and_mul_sp": {"RLK_TUNE_STORE_POL": [0, 1, 2, 3]},
 }
 
 
@@ -265,7 +286,7 @@ def sweep(torch, data, reps, only=None):
     import itertools
     from redline_amd._lib import set_tune_knob
     for key, knobs in SWEEP_KNOBS.items():
-        kern = key.removesuffix("_vpl")
+        kern = key.removesuffix("_sp")
         if only and kern != only:
             continue
         names = list(knobs)
@@ -563,7 +584,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the C3-C5 per-kernel figures")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention figures")
     ap.add_argument("--no-gemv", action="store_true", help="skip the INT4 GEMV + SwiGLU figures")
-    ap.add_argument("--only", default=None, help="time only this kernel (profiling runs)")
+    ap.add_argument("--only", default=None,
+                    help="time only this kernel (profiling runs); with --profile-calls, "
+                         "'elementwise' selects the layer kernels only")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="seconds of CPU steps per thread count (single and multi)")
     ap.add_argument("--rotations", type=int, default=None,
@@ -633,7 +656,7 @@ def main():
     if args.profile_calls:
         fns = kernel_fns(data)
         for name in KERNELS + STEP_EXTRA:
-            if args.only and name != args.only:
+            if args.only and args.only not in (name, "elementwise"):
                 continue
             for i in range(args.profile_calls):
                 fns[name](i % data.R)
@@ -700,6 +723,12 @@ def main():
 
     kern = per_kernel(torch, data, args.reps, args.only,
                       KERNELS + (STEP_EXTRA if args.only is None or args.only in STEP_EXTRA else ()))
+    fns = kernel_fns(data)
+    for name, r in kern.items():  # each launch on its own, between HIP events
+        mean, med = launch_durations(torch, fns[name], data.R)
+        r["us_per_launch_isolated"] = round(mean, 3)
+        r["us_per_launch_isolated_median"] = round(med, 3)
+        log(f"  {w.key} {name:26s} isolated launch {mean:7.3f} us (median {med:7.3f})")
     rot = data.R
     del data
     torch.cuda.empty_cache()
@@ -707,10 +736,18 @@ def main():
         print(json.dumps({"only": args.only, "workload": w.key, "kernels": kern}))
         return
 
+    # The dominant kernel (most bytes per launch) at its average launch
+    # duration: each launch bracketed by HIP events, as a kernel trace times a
+    # dispatch.  Its back-to-back per-call time in a graph (us_per_call) is
+    # reported beside it.
     dominant = max(KERNELS, key=lambda k: nb[k])
     dk = kern[dominant]
-    roofline = {"bound": "hbm", "kernel": dominant, "achieved": dk["gb_per_s"],
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_of_hbm_peak"],
+    achieved = nb[dominant] / (dk["us_per_launch_isolated"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "us_per_launch": dk["us_per_launch_isolated"],
+                "graph_us_per_call": dk["us_per_call"],
+                "graph_frac": dk["frac_of_hbm_peak"],
                 "traffic": measured_traffic(w.key, KERNEL_SYMBOL[dominant]),
                 "traffic_source": "profiles/hbm_traffic_C2_C5.md (rocprofv3 FETCH_SIZE and "
                                   "WRITE_SIZE, each scaled by its reading for a 256 MiB copy)",

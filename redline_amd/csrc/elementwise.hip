@@ -61,61 +61,37 @@ __global__ __launch_bounds__(BS) void gather_rows_kernel(const int32_t* __restri
   st16<NT>(dst + g, ld16<NT>(src + srow * vecs + col));
 }
 
-// V vectors per lane: a workgroup covers BS * V consecutive vectors, lane l
-// the vectors l, l + BS, ... (each step one coalesced 16-byte access per
-// lane); all V loads are issued before the first store, so each wave keeps V
-// KiB in flight.
-template <int BS, int V, bool NT>
-__global__ __launch_bounds__(BS) void gather_rows_v_kernel(const int32_t* __restrict__ idx,
-                                                           const u32x4* __restrict__ src,
-                                                           uint32_t vecs, uint32_t total,
-                                                           u32x4* __restrict__ dst) {
-  const uint32_t base = blockIdx.x * (BS * V) + threadIdx.x;
-  u32x4 v[V];
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const uint32_t g = base + k * BS;
-    if (g < total) {
-      const uint32_t row = g / vecs;
-      const uint32_t col = g - row * vecs;
-      const uint64_t srow = idx != nullptr ? static_cast<uint32_t>(idx[row]) : row;
-      v[k] = ld16<NT>(src + srow * vecs + col);
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const uint32_t g = base + k * BS;
-    if (g < total) st16<NT>(dst + g, v[k]);
-  }
+// The same gather with an explicit store cache policy SP (st16p); a
+// launch-policy experiment selected by RLK_TUNE_STORE_POL.
+template <int BS, int SP>
+__global__ __launch_bounds__(BS) void gather_rows_sp_kernel(const int32_t* __restrict__ idx,
+                                                            const u32x4* __restrict__ src,
+                                                            uint32_t vecs, uint32_t total,
+                                                            u32x4* __restrict__ dst) {
+  const uint32_t g = blockIdx.x * BS + threadIdx.x;
+  if (g >= total) return;
+  const uint32_t row = g / vecs;
+  const uint32_t col = g - row * vecs;
+  const uint64_t srow = idx != nullptr ? static_cast<uint32_t>(idx[row]) : row;
+  st16p<SP>(dst + g, ld16<true>(src + srow * vecs + col));
 }
 
 template <int BS>
-void launch_gather_bs(bool nt, int vpl, uint64_t total, const int32_t* idx, const u32x4* s,
+void launch_gather_bs(bool nt, int sp, uint64_t total, const int32_t* idx, const u32x4* s,
                       uint32_t vecs, u32x4* d, hipStream_t stream) {
   const uint32_t t32 = static_cast<uint32_t>(total);
-#define RLK_GATHER_V(V)                                                                       \
-  {                                                                                           \
-    const uint64_t blocks = (total + BS * V - 1) / (BS * V);                                  \
-    if (nt) {                                                                                 \
-      gather_rows_v_kernel<BS, V, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);     \
-    } else {                                                                                  \
-      gather_rows_v_kernel<BS, V, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);    \
-    }                                                                                         \
+  const uint64_t blocks = (total + BS - 1) / BS;
+  switch (sp) {
+    case 1: gather_rows_sp_kernel<BS, 1><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d); return;
+    case 2: gather_rows_sp_kernel<BS, 2><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d); return;
+    case 3: gather_rows_sp_kernel<BS, 3><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d); return;
+    default: break;
   }
-  switch (vpl) {
-    case 2: RLK_GATHER_V(2) break;
-    case 4: RLK_GATHER_V(4) break;
-    case 8: RLK_GATHER_V(8) break;
-    default: {
-      const uint64_t blocks = (total + BS - 1) / BS;
-      if (nt) {
-        gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
-      } else {
-        gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
-      }
-    }
+  if (nt) {
+    gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
+  } else {
+    gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
   }
-#undef RLK_GATHER_V
 }
 
 int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* dst,
@@ -125,13 +101,13 @@ int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* ds
     return fail(RLK_EINVAL, "%s: %d rows x %d vectors exceed one launch; split the call", what, n,
                 vecs);
   const FlatPolicy p = pick_flat(total >= (1u << 20) ? 256 : 128, kGatherBs, kGatherNt);
-  const int vpl = tune_knob(kGatherVpl, 1);
+  const int sp = tune_knob(kStorePol, 0);
   const auto* s = static_cast<const u32x4*>(src);
   auto* d = static_cast<u32x4*>(dst);
   switch (p.bs) {
-    case 128: launch_gather_bs<128>(p.nt, vpl, total, idx, s, vecs, d, stream); break;
-    case 256: launch_gather_bs<256>(p.nt, vpl, total, idx, s, vecs, d, stream); break;
-    default: launch_gather_bs<64>(p.nt, vpl, total, idx, s, vecs, d, stream); break;
+    case 128: launch_gather_bs<128>(p.nt, sp, total, idx, s, vecs, d, stream); break;
+    case 256: launch_gather_bs<256>(p.nt, sp, total, idx, s, vecs, d, stream); break;
+    default: launch_gather_bs<64>(p.nt, sp, total, idx, s, vecs, d, stream); break;
   }
   return launch_status(what);
 }
@@ -337,7 +313,7 @@ void launch_norm(const NormArgs& a, hipStream_t stream) {
 
 // Split layout: gate in [r, 0:I], up in [r, I:2I]; flat over the [rows, vecs]
 // output vectors (vecs = I / 8).
-template <int BS, bool NT>
+template <int BS, bool NT, int SP = 0>
 __global__ __launch_bounds__(BS) void silu_and_mul_kernel(const u32x4* __restrict__ gate_up,
                                                           uint32_t vecs, uint32_t total,
                                                           u32x4* __restrict__ out) {
@@ -351,7 +327,11 @@ __global__ __launch_bounds__(BS) void silu_and_mul_kernel(const u32x4* __restric
   f32x8 s;
 #pragma unroll
   for (int j = 0; j < 8; ++j) s[j] = silu_f16(gf[j]);
-  st16<NT>(out + g, pack8(s * unpack8(uv)));
+  if constexpr (SP == 0) {
+    st16<NT>(out + g, pack8(s * unpack8(uv)));
+  } else {
+    st16p<SP>(out + g, pack8(s * unpack8(uv)));
+  }
 }
 
 // Interleaved layout (gate_i, up_i): output vector g (8 outputs) reads input
@@ -386,8 +366,13 @@ void launch_swiglu_bs(bool interleaved, uint64_t blocks, const u32x4* gu, uint32
                       uint32_t total, u32x4* o, hipStream_t stream) {
   if (interleaved) {
     silu_and_mul_interleaved_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, total, o);
-  } else {
-    silu_and_mul_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, vecs, total, o);
+    return;
+  }
+  switch (NT ? tune_knob(kStorePol, 0) : 0) {
+    case 1: silu_and_mul_kernel<BS, NT, 1><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
+    case 2: silu_and_mul_kernel<BS, NT, 2><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
+    case 3: silu_and_mul_kernel<BS, NT, 3><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
+    default: silu_and_mul_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
   }
 }
 

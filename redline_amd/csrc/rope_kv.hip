@@ -49,37 +49,28 @@ struct RopeArgs {
   int block_size;
 };
 
-template <int D, bool kInt8, int WPT, int U>
+template <int D, bool kInt8, int WPT>
 __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr bool NT = true;  // streaming accesses: measured faster at every batch size
   constexpr int kHalf = D / 2;
   constexpr int kLPH = kHalf / 8;            // lanes per head
   constexpr int kHeadsPerWave = kWave / kLPH;
-  constexpr int kGroups = kHeadsPerWave * WPT;  // heads of one token per sweep of the workgroup
+  constexpr int kGroups = kHeadsPerWave * WPT;  // heads of one token in flight
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t t = blockIdx.x;  // one token per workgroup of WPT waves
   const int hg = wave * kHeadsPerWave + lane / kLPH;
   const int p0 = (lane % kLPH) * 8;  // first pair index owned by this lane
   const int heads = a.hq + 2 * a.hkv;
   _Float16* row = a.qkv + t * heads * D;
-  // The activations do not depend on the metadata: issue the loads of the
-  // lane's first U heads before the positions -> cos/sin and slot -> cell
-  // chain, so the two latencies overlap instead of adding up.  U heads per
-  // lane are loaded together (heads hg, hg + kGroups, ...): U x 32 bytes in
-  // flight per lane.
-  u32x4 v0[U], v1[U];
-  auto load = [&](int h0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int h = h0 + u * kGroups;
-      if (h < heads) {
-        v0[u] = ld16<NT>(reinterpret_cast<const u32x4*>(row + h * D + p0));
-        v1[u] = ld16<NT>(reinterpret_cast<const u32x4*>(row + h * D + kHalf + p0));
-      }
-    }
-  };
-  load(hg);
+  // The activations do not depend on the metadata: issue their loads for the
+  // first head before the positions -> cos/sin and slot -> cell chain, so the
+  // two latencies overlap instead of adding up.
+  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+  if (hg < heads) {
+    v0 = ld16<NT>(reinterpret_cast<const u32x4*>(row + hg * D + p0));
+    v1 = ld16<NT>(reinterpret_cast<const u32x4*>(row + hg * D + kHalf + p0));
+  }
   const int pos = a.positions[t];
   const int slot = a.slots[t];
 
@@ -95,90 +86,83 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
     blk = slot / a.block_size;
     off = slot - blk * a.block_size;
   }
-  for (int h0 = hg; h0 < heads; h0 += kGroups * U) {  // all lanes of a head share h0
-    if (h0 != hg) load(h0);
+  for (int h = hg; h < heads; h += kGroups) {  // all lanes of a head share h
+    _Float16* hp = row + h * D;
+    if (h != hg) {
+      v0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
+      v1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
+    }
+    f32x8 x0 = unpack8(v0);
+    f32x8 x1 = unpack8(v1);
+    if (a.bias != nullptr) {  // extension: QKV bias, fp16-rounded sum
+      x0 = round_f16(x0 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + p0)));
+      x1 = round_f16(x1 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0)));
+    }
+    if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
+      const f32x8 y0 = x0 * c - x1 * s;
+      const f32x8 y1 = x1 * c + x0 * s;
+      x0 = round_f16(y0);
+      x1 = round_f16(y1);
+    }
+    if (h < a.hq) {  // query: back in place
+      st16<NT>(reinterpret_cast<u32x4*>(hp + p0), pack8(x0));
+      st16<NT>(reinterpret_cast<u32x4*>(hp + kHalf + p0), pack8(x1));
+      continue;
+    }
+    if (slot < 0) continue;
+    const bool is_v = h >= a.hq + a.hkv;
+    const int kvh = is_v ? h - a.hq - a.hkv : h - a.hq;
+    const int64_t cell = (static_cast<int64_t>(blk) * a.hkv + kvh) * a.block_size + off;
+    if constexpr (!kInt8) {
+      _Float16* dst = static_cast<_Float16*>(is_v ? a.v : a.k) + cell * D;
+      st16<NT>(reinterpret_cast<u32x4*>(dst + p0), pack8(x0));
+      st16<NT>(reinterpret_cast<u32x4*>(dst + kHalf + p0), pack8(x1));
+    } else {
+      float amax = 0.f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int h = h0 + u * kGroups;
-      if (h >= heads) break;
-      _Float16* hp = row + h * D;
-      f32x8 x0 = unpack8(v0[u]);
-      f32x8 x1 = unpack8(v1[u]);
-      if (a.bias != nullptr) {  // extension: QKV bias, fp16-rounded sum
-        x0 = round_f16(x0 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + p0)));
-        x1 = round_f16(x1 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0)));
-      }
-      if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
-        const f32x8 y0 = x0 * c - x1 * s;
-        const f32x8 y1 = x1 * c + x0 * s;
-        x0 = round_f16(y0);
-        x1 = round_f16(y1);
-      }
-      if (h < a.hq) {  // query: back in place
-        st16<NT>(reinterpret_cast<u32x4*>(hp + p0), pack8(x0));
-        st16<NT>(reinterpret_cast<u32x4*>(hp + kHalf + p0), pack8(x1));
-        continue;
-      }
-      if (slot < 0) continue;
-      const bool is_v = h >= a.hq + a.hkv;
-      const int kvh = is_v ? h - a.hq - a.hkv : h - a.hq;
-      const int64_t cell = (static_cast<int64_t>(blk) * a.hkv + kvh) * a.block_size + off;
-      if constexpr (!kInt8) {
-        _Float16* dst = static_cast<_Float16*>(is_v ? a.v : a.k) + cell * D;
-        st16<NT>(reinterpret_cast<u32x4*>(dst + p0), pack8(x0));
-        st16<NT>(reinterpret_cast<u32x4*>(dst + kHalf + p0), pack8(x1));
-      } else {
-        float amax = 0.f;
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fmaxf(__builtin_fabsf(x0[j]), __builtin_fabsf(x1[j])));
+      amax = group_max<kLPH>(amax);
+      float scale = amax > 0.f ? amax / 127.f : 1.f;
+      if (a.scale16) scale = round_f16(scale);  // extension: quantise against the stored fp16 scale
+      const float inv = 1.f / scale;
+      i8x8 q0, q1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          amax = fmaxf(amax, fmaxf(__builtin_fabsf(x0[j]), __builtin_fabsf(x1[j])));
-        amax = group_max<kLPH>(amax);
-        float scale = amax > 0.f ? amax / 127.f : 1.f;
-        if (a.scale16) scale = round_f16(scale);  // extension: quantise against the stored fp16 scale
-        const float inv = 1.f / scale;
-        i8x8 q0, q1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          q0[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x0[j] * inv, -127.f), 127.f)));
-          q1[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x1[j] * inv, -127.f), 127.f)));
-        }
-        int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
-        st8<NT>(reinterpret_cast<u32x2*>(dst + p0), __builtin_bit_cast(u32x2, q0));
-        st8<NT>(reinterpret_cast<u32x2*>(dst + kHalf + p0), __builtin_bit_cast(u32x2, q1));
-        if (p0 == 0) {
-          void* scp = is_v ? a.v_scale : a.k_scale;
-          if (a.scale16) {
-            static_cast<_Float16*>(scp)[cell] = static_cast<_Float16>(scale);
-          } else {
-            static_cast<float*>(scp)[cell] = scale;
-          }
+      for (int j = 0; j < 8; ++j) {
+        q0[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x0[j] * inv, -127.f), 127.f)));
+        q1[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x1[j] * inv, -127.f), 127.f)));
+      }
+      int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
+      st8<NT>(reinterpret_cast<u32x2*>(dst + p0), __builtin_bit_cast(u32x2, q0));
+      st8<NT>(reinterpret_cast<u32x2*>(dst + kHalf + p0), __builtin_bit_cast(u32x2, q1));
+      if (p0 == 0) {
+        void* sp = is_v ? a.v_scale : a.k_scale;
+        if (a.scale16) {
+          static_cast<_Float16*>(sp)[cell] = static_cast<_Float16>(scale);
+        } else {
+          static_cast<float*>(sp)[cell] = scale;
         }
       }
     }
   }
 }
 
-template <int D, bool kInt8, int U>
-void launch_du(const RopeArgs& a, int wpt, hipStream_t stream) {
+template <int D, bool kInt8>
+void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
   switch (wpt) {
-    case 1: rope_kv_kernel<D, kInt8, 1, U><<<a.num_tokens, kWave, 0, stream>>>(a); break;
-    case 2: rope_kv_kernel<D, kInt8, 2, U><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
-    case 3: rope_kv_kernel<D, kInt8, 3, U><<<a.num_tokens, 3 * kWave, 0, stream>>>(a); break;
-    case 4: rope_kv_kernel<D, kInt8, 4, U><<<a.num_tokens, 4 * kWave, 0, stream>>>(a); break;
-    case 5: rope_kv_kernel<D, kInt8, 5, U><<<a.num_tokens, 5 * kWave, 0, stream>>>(a); break;
-    case 6: rope_kv_kernel<D, kInt8, 6, U><<<a.num_tokens, 6 * kWave, 0, stream>>>(a); break;
-    case 7: rope_kv_kernel<D, kInt8, 7, U><<<a.num_tokens, 7 * kWave, 0, stream>>>(a); break;
-    default: rope_kv_kernel<D, kInt8, 8, U><<<a.num_tokens, 8 * kWave, 0, stream>>>(a); break;
+    case 1: rope_kv_kernel<D, kInt8, 1><<<a.num_tokens, kWave, 0, stream>>>(a); break;
+    case 2: rope_kv_kernel<D, kInt8, 2><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
+    case 3: rope_kv_kernel<D, kInt8, 3><<<a.num_tokens, 3 * kWave, 0, stream>>>(a); break;
+    case 4: rope_kv_kernel<D, kInt8, 4><<<a.num_tokens, 4 * kWave, 0, stream>>>(a); break;
+    case 5: rope_kv_kernel<D, kInt8, 5><<<a.num_tokens, 5 * kWave, 0, stream>>>(a); break;
+    case 6: rope_kv_kernel<D, kInt8, 6><<<a.num_tokens, 6 * kWave, 0, stream>>>(a); break;
+    case 7: rope_kv_kernel<D, kInt8, 7><<<a.num_tokens, 7 * kWave, 0, stream>>>(a); break;
+    default: rope_kv_kernel<D, kInt8, 8><<<a.num_tokens, 8 * kWave, 0, stream>>>(a); break;
   }
 }
 
 template <int D>
-void launch_dt(const RopeArgs& a, bool int8, int wpt, int unroll, hipStream_t stream) {
-  if (unroll == 2) {
-    int8 ? launch_du<D, true, 2>(a, wpt, stream) : launch_du<D, false, 2>(a, wpt, stream);
-  } else {
-    int8 ? launch_du<D, true, 1>(a, wpt, stream) : launch_du<D, false, 1>(a, wpt, stream);
-  }
+void launch_dt(const RopeArgs& a, bool int8, int wpt, hipStream_t stream) {
+  int8 ? launch_d<D, true>(a, wpt, stream) : launch_d<D, false>(a, wpt, stream);
 }
 
 }  // namespace
@@ -225,18 +209,15 @@ int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_map
   // heads of the token at once, so wpt = ceil(heads / heads_per_wave) (at most
   // 8) handles every head of the token in one pass: 6 waves for Llama-3.1-8B
   // (48 heads of 128), 5 for Qwen2-7B (36 heads).
-  // RLK_TUNE_ROPE_UNROLL = 2 gives each lane two heads in flight (and half
-  // the waves per token).
-  const int unroll = tune_knob(kRopeUnroll, 1) == 2 ? 2 : 1;
   const int heads = num_heads + 2 * kv->num_kv_heads;
-  const int heads_per_wave = kWave / (kv->head_dim / 16) * unroll;
+  const int heads_per_wave = kWave / (kv->head_dim / 16);
   int wpt = (heads + heads_per_wave - 1) / heads_per_wave;
   wpt = tune_knob(kRopeWpt, wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
   const bool int8 = kv->dtype == RLK_KV_INT8;
   if (kv->head_dim == 128) {
-    launch_dt<128>(a, int8, wpt, unroll, stream);
+    launch_dt<128>(a, int8, wpt, stream);
   } else {
-    launch_dt<64>(a, int8, wpt, unroll, stream);
+    launch_dt<64>(a, int8, wpt, stream);
   }
   return launch_status(what);
 }

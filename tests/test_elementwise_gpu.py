@@ -45,22 +45,22 @@ def test_embedding_bit_exact(torch_cuda, vocab, hidden, n):
     assert_bits_equal(host(out), oracle.embedding_lookup(ids, table, hidden), "embedding")
 
 
-@pytest.mark.parametrize("vpl", [2, 4, 8])
+@pytest.mark.parametrize("sp", [1, 2, 3])
 @pytest.mark.parametrize("bs", [64, 256])
-def test_embedding_vectors_per_lane(torch_cuda, vpl, bs):
-    """The gather with several 16-byte vectors per lane (launch-policy knob)
+def test_embedding_store_policies(torch_cuda, sp, bs):
+    """The gather under each explicit store cache policy (launch-policy knob)
     is bit-exact, including a ragged final workgroup and rows narrower than a
-    workgroup's span."""
+    workgroup."""
     torch = torch_cuda
     from redline_amd import kernels as K
     from redline_amd._lib import tune_knob
-    say(f"embedding vpl={vpl} bs={bs}")
-    rng = np.random.default_rng(vpl * 7 + bs)
+    say(f"embedding store policy={sp} bs={bs}")
+    rng = np.random.default_rng(sp * 7 + bs)
     for vocab, hidden, n in ((1000, 4096, 37), (64, 8, 5), (300, 4104, 129)):
         table = randn_f16(rng, (vocab, hidden), 0.02)
         ids = rng.integers(0, vocab, n, dtype=np.int32)
         out = torch.empty((n, hidden), dtype=torch.float16, device="cuda")
-        with tune_knob("RLK_TUNE_GATHER_VPL", vpl), tune_knob("RLK_TUNE_GATHER_BS", bs):
+        with tune_knob("RLK_TUNE_STORE_POL", sp), tune_knob("RLK_TUNE_GATHER_BS", bs):
             K.embedding_lookup(dev(torch, ids), dev(torch, table), n, hidden, out)
         assert_bits_equal(host(out), oracle.embedding_lookup(ids, table, hidden), "embedding")
 
@@ -240,6 +240,20 @@ def test_swiglu(torch_cuda, rows, inter, interleaved):
         u = torch.from_numpy(gu[:, inter:].astype(np.float32))
         ref = torch.nn.functional.silu(g) * u
         assert rel_max_err(host(out), ref.numpy()) <= 3e-3
+
+
+@pytest.mark.parametrize("sp", [1, 2, 3])
+def test_swiglu_store_policies(torch_cuda, sp):
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    from redline_amd._lib import tune_knob
+    say(f"swiglu store policy={sp}")
+    rng = np.random.default_rng(sp)
+    gu = randn_f16(rng, (33, 2 * 1032))
+    out = torch.empty((33, 1032), dtype=torch.float16, device="cuda")
+    with tune_knob("RLK_TUNE_STORE_POL", sp):
+        K.silu_and_mul(dev(torch, gu), 33, 1032, out)
+    assert_close_f16(host(out), oracle.silu_and_mul(gu, 1032), what="swiglu")
 
 
 @pytest.mark.parametrize("inter", [1, 3, 100, 1001])

@@ -378,23 +378,23 @@ def test_rope_extension_null_options_is_plain(torch_cuda):
     assert_bits_equal(outs[0][1], outs[1][1], "k cache")
 
 
-@pytest.mark.parametrize("unroll,wpt", [(2, None), (2, 1), (2, 8), (1, 2)])
+@pytest.mark.parametrize("wpt", [1, 2, 3, 8])
 @pytest.mark.parametrize("hq,hkv,D,int8,lens", [REF_CASES[0], REF_CASES[1], REF_CASES[4],
                                                 (32, 8, 128, False, [200, 57]),
                                                 (32, 8, 128, True, [130]), (28, 4, 128, False, [90])])
-def test_rope_kv_launch_policies(torch_cuda, unroll, wpt, hq, hkv, D, int8, lens):
-    """Every launch policy (heads in flight per lane, waves per token) gives the
-    same bits: the Llama-3.1-8B and Qwen2-7B head counts leave partial head
-    sweeps at every setting."""
+def test_rope_kv_launch_policies(torch_cuda, wpt, hq, hkv, D, int8, lens):
+    """Every launch policy (waves per token) gives the same bits: the
+    Llama-3.1-8B and Qwen2-7B head counts leave partial head sweeps at every
+    setting."""
     from redline_amd._lib import tune_knob
-    say(f"rope policy unroll={unroll} wpt={wpt} hq={hq} hkv={hkv} D={D} int8={int8}")
+    say(f"rope policy wpt={wpt} hq={hq} hkv={hkv} D={D} int8={int8}")
     bs = 16
-    rng = np.random.default_rng(hq + hkv + D + unroll)
+    rng = np.random.default_rng(hq + hkv + D + wpt)
     T = sum(lens)
     nblocks = 2 + T // bs + len(lens)
     slots = rng.permutation(np.arange(bs, nblocks * bs, dtype=np.int32))[:T]
     slots[rng.integers(0, T)] = -1
     pos = rng.integers(0, 4096, T).astype(np.int32)
     qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
-    with tune_knob("RLK_TUNE_ROPE_UNROLL", unroll), tune_knob("RLK_TUNE_ROPE_WPT", wpt):
+    with tune_knob("RLK_TUNE_ROPE_WPT", wpt):
         run_case(torch_cuda, qkv, pos, slots, hq, hkv, D, nblocks, int8, theta=5e5)
