@@ -244,6 +244,20 @@ typedef struct rlk_decode_attention_work {
 int rlk_paged_attention_decode(const rlk_attention_params* params,
                                const rlk_decode_attention_work* work, hipStream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): rlk_paged_attention_decode with the split-K partials in a
+ * library-owned device array of RLK_DECODE_SCRATCH_BYTES per GPU (held until
+ * the process ends) instead of work->ws_out / ws_max / ws_sum, which are
+ * ignored.  Allocates nothing.  Needs num_items * num_heads * max_partitions *
+ * (head_dim + 2) * 4 bytes (each of the three regions rounded up to 256);
+ * more than RLK_DECODE_SCRATCH_BYTES: RLK_EINVAL.  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or
+ * threads) race and must be serialised by the caller. */
+#define RLK_DECODE_SCRATCH_BYTES (32u << 20)
+int rlk_paged_attention_decode_noalloc(const rlk_attention_params* params,
+                                       const rlk_decode_attention_work* work, hipStream_t stream);
+
 /* Extension, no counterpart in the reference (whose scales are fp32 only):
  * decode attention over an INT8 cache whose scales were stored as fp16 by
  * rlk_rope_and_write_kv_ex with RLK_SCALE_F16 (k_scale / v_scale then address

@@ -119,6 +119,8 @@ _SIGNATURES = {
                                       C.POINTER(RopeKVOptions), _P]),
     "rlk_paged_attention_decode": (_I, [C.POINTER(AttentionParams),
                                         C.POINTER(DecodeAttentionWork), _P]),
+    "rlk_paged_attention_decode_noalloc": (_I, [C.POINTER(AttentionParams),
+                                                C.POINTER(DecodeAttentionWork), _P]),
     "rlk_paged_attention_decode_ex": (_I, [C.POINTER(AttentionParams),
                                            C.POINTER(DecodeAttentionWork),
                                            C.POINTER(AttentionOptions), _P]),

@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <cstdint>
+#include <mutex>
 
 #include "device.hpp"
 #include "redline_amd/rlk.h"
@@ -813,6 +814,77 @@ int attention_launch(const rlk_attention_params* p, const rlk_decode_attention_w
 }
 
 }  // namespace
+
+// ---- the no-allocation form.  Its split-K partials live in a file-scope
+// device array, one copy per GPU, instead of a caller workspace.  In host
+// code `scratch` names a host-side stand-in, not device memory: the device
+// address of each GPU's copy comes from hipGetSymbolAddress, taken once per
+// device (with that device current) on the first call there, and only that
+// address is handed to kernels.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[RLK_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of the current device's scratch array, or null (message set).
+void* device_scratch() {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(RLK_EINVAL, "paged_attention_decode_noalloc: no usable current device (%s)",
+         hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t s = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (s != hipSuccess || ptr == nullptr) {
+      fail(static_cast<int>(s), "paged_attention_decode_noalloc: hipGetSymbolAddress failed (%s)",
+           hipGetErrorString(s));
+      return nullptr;
+    }
+    g_scratch[dev] = ptr;
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" int rlk_paged_attention_decode_noalloc(const rlk_attention_params* p,
+                                                  const rlk_decode_attention_work* w,
+                                                  hipStream_t stream) {
+  if (p == nullptr || w == nullptr)
+    return fail(RLK_EINVAL, "paged_attention_decode_noalloc: null params or work");
+  if (w->num_items <= 0) return RLK_OK;
+  if (w->max_partitions < 1 || p->num_heads <= 0 || p->kv.head_dim <= 0)
+    return fail(RLK_EINVAL, "paged_attention_decode_noalloc: bad max_partitions %d, num_heads %d "
+                            "or head_dim %d", w->max_partitions, p->num_heads, p->kv.head_dim);
+  // partials [items, heads, partitions, D] then max and sum [items, heads,
+  // partitions], each region 256-byte aligned; no zeroing is needed (every
+  // partition a merge reads is written first by the same call)
+  const uint64_t rows = static_cast<uint64_t>(w->num_items) * p->num_heads * w->max_partitions;
+  const uint64_t out_bytes = (rows * p->kv.head_dim * 4 + 255) / 256 * 256;
+  const uint64_t stat_bytes = (rows * 4 + 255) / 256 * 256;
+  const uint64_t need = out_bytes + 2 * stat_bytes;
+  if (need > RLK_DECODE_SCRATCH_BYTES)
+    return fail(RLK_EINVAL, "paged_attention_decode_noalloc: %d items x %d heads x %d partitions "
+                            "need %llu bytes of split-K scratch, more than the %llu available; "
+                            "split the call or pass a workspace to paged_attention_decode",
+                w->num_items, p->num_heads, w->max_partitions,
+                static_cast<unsigned long long>(need),
+                static_cast<unsigned long long>(RLK_DECODE_SCRATCH_BYTES));
+  char* base = static_cast<char*>(device_scratch());
+  if (base == nullptr) return RLK_EINVAL;
+  rlk_decode_attention_work ws = *w;
+  ws.ws_out = reinterpret_cast<float*>(base);
+  ws.ws_max = reinterpret_cast<float*>(base + out_bytes);
+  ws.ws_sum = reinterpret_cast<float*>(base + out_bytes + stat_bytes);
+  return attention_launch(p, &ws, 0, stream);
+}
 
 extern "C" int rlk_paged_attention_decode(const rlk_attention_params* p,
                                           const rlk_decode_attention_work* w,
