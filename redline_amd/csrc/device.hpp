@@ -184,23 +184,6 @@ __device__ __forceinline__ void st16(u32x4* p, u32x4 v) {
     *p = v;
   }
 }
-// 16-byte store with an explicit gfx950 cache policy: 0 = nt (what st16<true>
-// emits), 1 = sc0 sc1 nt (write-through to memory scope, streaming), 2 = sc1
-// nt, 3 = sc0 sc1.  A launch-policy experiment on where the end-of-kernel
-// write-back of dirty L2 lines goes.
-template <int SP>
-__device__ __forceinline__ void st16p(u32x4* p, u32x4 v) {
-  if constexpr (SP == 0) {
-    __builtin_nontemporal_store(v, p);
-  } else if constexpr (SP == 1) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(p), "v"(v) : "memory");
-  } else if constexpr (SP == 2) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" ::"v"(p), "v"(v) : "memory");
-  } else {
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
-  }
-}
-
 template <bool kNT>
 __device__ __forceinline__ void st8(u32x2* p, u32x2 v) {
   if constexpr (kNT) {

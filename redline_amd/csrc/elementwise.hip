@@ -17,6 +17,7 @@
 #include <cstdint>
 
 #include "device.hpp"
+#include "launch.hpp"
 #include "redline_amd/rlk.h"
 #include "status.hpp"
 
@@ -61,37 +62,13 @@ __global__ __launch_bounds__(BS) void gather_rows_kernel(const int32_t* __restri
   st16<NT>(dst + g, ld16<NT>(src + srow * vecs + col));
 }
 
-// The same gather with an explicit store cache policy SP (st16p); a
-// launch-policy experiment selected by RLK_TUNE_STORE_POL.
-template <int BS, int SP>
-__global__ __launch_bounds__(BS) void gather_rows_sp_kernel(const int32_t* __restrict__ idx,
-                                                            const u32x4* __restrict__ src,
-                                                            uint32_t vecs, uint32_t total,
-                                                            u32x4* __restrict__ dst) {
-  const uint32_t g = blockIdx.x * BS + threadIdx.x;
-  if (g >= total) return;
-  const uint32_t row = g / vecs;
-  const uint32_t col = g - row * vecs;
-  const uint64_t srow = idx != nullptr ? static_cast<uint32_t>(idx[row]) : row;
-  st16p<SP>(dst + g, ld16<true>(src + srow * vecs + col));
-}
-
 template <int BS>
-void launch_gather_bs(bool nt, int sp, uint64_t total, const int32_t* idx, const u32x4* s,
+void launch_gather_bs(bool nt, uint64_t total, const int32_t* idx, const u32x4* s,
                       uint32_t vecs, u32x4* d, hipStream_t stream) {
   const uint32_t t32 = static_cast<uint32_t>(total);
   const uint64_t blocks = (total + BS - 1) / BS;
-  switch (sp) {
-    case 1: gather_rows_sp_kernel<BS, 1><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d); return;
-    case 2: gather_rows_sp_kernel<BS, 2><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d); return;
-    case 3: gather_rows_sp_kernel<BS, 3><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d); return;
-    default: break;
-  }
-  if (nt) {
-    gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
-  } else {
-    gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
-  }
+  launch(nt ? gather_rows_kernel<BS, true> : gather_rows_kernel<BS, false>, blocks, BS, 0, stream,
+         idx, s, vecs, t32, d);
 }
 
 int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* dst,
@@ -101,13 +78,12 @@ int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* ds
     return fail(RLK_EINVAL, "%s: %d rows x %d vectors exceed one launch; split the call", what, n,
                 vecs);
   const FlatPolicy p = pick_flat(total >= (1u << 20) ? 256 : 128, kGatherBs, kGatherNt);
-  const int sp = tune_knob(kStorePol, 0);
   const auto* s = static_cast<const u32x4*>(src);
   auto* d = static_cast<u32x4*>(dst);
   switch (p.bs) {
-    case 128: launch_gather_bs<128>(p.nt, sp, total, idx, s, vecs, d, stream); break;
-    case 256: launch_gather_bs<256>(p.nt, sp, total, idx, s, vecs, d, stream); break;
-    default: launch_gather_bs<64>(p.nt, sp, total, idx, s, vecs, d, stream); break;
+    case 128: launch_gather_bs<128>(p.nt, total, idx, s, vecs, d, stream); break;
+    case 256: launch_gather_bs<256>(p.nt, total, idx, s, vecs, d, stream); break;
+    default: launch_gather_bs<64>(p.nt, total, idx, s, vecs, d, stream); break;
   }
   return launch_status(what);
 }
@@ -234,9 +210,9 @@ int norm_src(const NormArgs& a) {
 
 template <int TPR, int NV, bool NT>
 void launch_norm_tn(const NormArgs& a, hipStream_t stream) {
-#define RLK_NORM_LAUNCH(S)                                                                       \
-  add_rmsnorm_kernel<TPR, NV, S, NT>                                                             \
-      <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out, a.ids)
+#define RLK_NORM_LAUNCH(S)                                                                 \
+  launch(add_rmsnorm_kernel<TPR, NV, S, NT>, a.rows, TPR, 0, stream, a.res, a.del, a.w, a.vecs, \
+         a.hidden, a.eps, a.out, a.ids)
   switch (norm_src(a)) {
     case kDelta: RLK_NORM_LAUNCH(kDelta); break;
     case kGather: RLK_NORM_LAUNCH(kGather); break;
@@ -298,9 +274,9 @@ void launch_norm(const NormArgs& a, hipStream_t stream) {
   bool launched = nt ? launch_norm_nt<true>(tpr, a, stream) : launch_norm_nt<false>(tpr, a, stream);
   if (!launched) launched = launch_norm_nt<false>(512, a, stream);
   if (launched) return;
-#define RLK_NORM_WIDE(S)                                                                   \
-  add_rmsnorm_wide_kernel<S><<<a.rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, \
-                                                         a.eps, a.out, a.ids)
+#define RLK_NORM_WIDE(S)                                                                  \
+  launch(add_rmsnorm_wide_kernel<S>, a.rows, 256, 0, stream, a.res, a.del, a.w, a.vecs, a.hidden, \
+         a.eps, a.out, a.ids)
   switch (norm_src(a)) {
     case kDelta: RLK_NORM_WIDE(kDelta); break;
     case kGather: RLK_NORM_WIDE(kGather); break;
@@ -313,7 +289,7 @@ void launch_norm(const NormArgs& a, hipStream_t stream) {
 
 // Split layout: gate in [r, 0:I], up in [r, I:2I]; flat over the [rows, vecs]
 // output vectors (vecs = I / 8).
-template <int BS, bool NT, int SP = 0>
+template <int BS, bool NT>
 __global__ __launch_bounds__(BS) void silu_and_mul_kernel(const u32x4* __restrict__ gate_up,
                                                           uint32_t vecs, uint32_t total,
                                                           u32x4* __restrict__ out) {
@@ -327,11 +303,7 @@ __global__ __launch_bounds__(BS) void silu_and_mul_kernel(const u32x4* __restric
   f32x8 s;
 #pragma unroll
   for (int j = 0; j < 8; ++j) s[j] = silu_f16(gf[j]);
-  if constexpr (SP == 0) {
-    st16<NT>(out + g, pack8(s * unpack8(uv)));
-  } else {
-    st16p<SP>(out + g, pack8(s * unpack8(uv)));
-  }
+  st16<NT>(out + g, pack8(s * unpack8(uv)));
 }
 
 // Interleaved layout (gate_i, up_i): output vector g (8 outputs) reads input
@@ -365,14 +337,9 @@ template <int BS, bool NT>
 void launch_swiglu_bs(bool interleaved, uint64_t blocks, const u32x4* gu, uint32_t vecs,
                       uint32_t total, u32x4* o, hipStream_t stream) {
   if (interleaved) {
-    silu_and_mul_interleaved_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, total, o);
-    return;
-  }
-  switch (NT ? tune_knob(kStorePol, 0) : 0) {
-    case 1: silu_and_mul_kernel<BS, NT, 1><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
-    case 2: silu_and_mul_kernel<BS, NT, 2><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
-    case 3: silu_and_mul_kernel<BS, NT, 3><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
-    default: silu_and_mul_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, vecs, total, o); break;
+    launch(silu_and_mul_interleaved_kernel<BS, NT>, blocks, BS, 0, stream, gu, total, o);
+  } else {
+    launch(silu_and_mul_kernel<BS, NT>, blocks, BS, 0, stream, gu, vecs, total, o);
   }
 }
 
@@ -503,9 +470,9 @@ extern "C" int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, i
                   static_cast<uint32_t>(pairs / 8), reinterpret_cast<u32x4*>(out), stream);
   } else {
     const uint64_t blocks = (pairs + 255) / 256;
-    silu_and_mul_interleaved_scalar_kernel<<<blocks, 256, 0, stream>>>(
-        reinterpret_cast<const f16x2*>(gate_up), static_cast<int64_t>(pairs),
-        reinterpret_cast<_Float16*>(out));
+    launch(silu_and_mul_interleaved_scalar_kernel, blocks, 256, 0, stream,
+           reinterpret_cast<const f16x2*>(gate_up), static_cast<int64_t>(pairs),
+           reinterpret_cast<_Float16*>(out));
   }
   return launch_status("silu_and_mul_interleaved");
 }

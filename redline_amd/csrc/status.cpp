@@ -14,6 +14,13 @@
 namespace rlk {
 namespace {
 thread_local char g_message[512] = "";
+thread_local LaunchEvents g_launch_events = {nullptr, nullptr};
+}  // namespace
+
+LaunchEvents take_launch_events() {
+  const LaunchEvents ev = g_launch_events;
+  g_launch_events = LaunchEvents{nullptr, nullptr};
+  return ev;
 }
 
 int fail(int code, const char* fmt, ...) {
@@ -85,7 +92,6 @@ constexpr const char* kKnobNames[kNumKnobs] = {
     "RLK_TUNE_GATHER_BS", "RLK_TUNE_GATHER_NT", "RLK_TUNE_NORM_TPR",   "RLK_TUNE_NORM_NT",
     "RLK_TUNE_SWIGLU_BS", "RLK_TUNE_SWIGLU_NT", "RLK_TUNE_ROPE_WPT",   "RLK_TUNE_ATTN_PERSIST",
     "RLK_TUNE_W4_CFG",    "RLK_TUNE_W8_CFG",    "RLK_TUNE_PREFILL_DMA", "RLK_TUNE_PREFILL_QS",
-    "RLK_TUNE_STORE_POL",
 };
 constexpr int kUnset = INT_MIN;
 std::atomic<int> g_knobs[kNumKnobs];
@@ -109,6 +115,13 @@ int tune_knob(Knob knob, int fallback) {
 }  // namespace rlk
 
 extern "C" const char* rlk_last_error(void) { return rlk::g_message; }
+
+extern "C" int rlk_time_next_launch(hipEvent_t start, hipEvent_t stop) {
+  if ((start == nullptr) != (stop == nullptr))
+    return rlk::fail(RLK_EINVAL, "rlk_time_next_launch: give both events or neither");
+  rlk::g_launch_events = rlk::LaunchEvents{start, stop};
+  return RLK_OK;
+}
 
 extern "C" int rlk_set_tune_knob(const char* name, int value, int set) {
   std::call_once(rlk::g_knobs_once, rlk::read_knobs_from_env);

@@ -20,6 +20,14 @@ int launch_status(const char* what);
 // fails).
 int compute_units();
 
+// Events armed by rlk_time_next_launch on the calling thread for its next
+// launch ({null, null} when none); the call disarms them.
+struct LaunchEvents {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+LaunchEvents take_launch_events();
+
 // Raises the dynamic-LDS limit of `kernel` on the current device to at least
 // `bytes` (hipFuncSetAttribute), once per (device, kernel) and size: later
 // calls are a lookup.
@@ -30,7 +38,7 @@ hipError_t grant_dynamic_lds(const void* kernel, size_t bytes);
 // rlk_set_tune_knob.
 enum Knob {
   kGatherBs, kGatherNt, kNormTpr, kNormNt, kSwigluBs, kSwigluNt, kRopeWpt, kAttnPersist,
-  kW4Cfg, kW8Cfg, kPrefillDma, kPrefillQs, kStorePol, kNumKnobs
+  kW4Cfg, kW8Cfg, kPrefillDma, kPrefillQs, kNumKnobs
 };
 
 // The override of `knob`, or `fallback` when none is set.

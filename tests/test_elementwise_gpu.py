@@ -45,22 +45,20 @@ def test_embedding_bit_exact(torch_cuda, vocab, hidden, n):
     assert_bits_equal(host(out), oracle.embedding_lookup(ids, table, hidden), "embedding")
 
 
-@pytest.mark.parametrize("sp", [1, 2, 3])
-@pytest.mark.parametrize("bs", [64, 256])
-def test_embedding_store_policies(torch_cuda, sp, bs):
-    """The gather under each explicit store cache policy (launch-policy knob)
-    is bit-exact, including a ragged final workgroup and rows narrower than a
-    workgroup."""
+@pytest.mark.parametrize("bs,nt", [(64, 1), (256, 1), (128, 0)])
+def test_embedding_launch_policies(torch_cuda, bs, nt):
+    """The gather under each block width and cache policy (launch-policy
+    knobs) is bit-exact, including a ragged final workgroup."""
     torch = torch_cuda
     from redline_amd import kernels as K
     from redline_amd._lib import tune_knob
-    say(f"embedding store policy={sp} bs={bs}")
-    rng = np.random.default_rng(sp * 7 + bs)
+    say(f"embedding policy bs={bs} nt={nt}")
+    rng = np.random.default_rng(bs + nt)
     for vocab, hidden, n in ((1000, 4096, 37), (64, 8, 5), (300, 4104, 129)):
         table = randn_f16(rng, (vocab, hidden), 0.02)
         ids = rng.integers(0, vocab, n, dtype=np.int32)
         out = torch.empty((n, hidden), dtype=torch.float16, device="cuda")
-        with tune_knob("RLK_TUNE_STORE_POL", sp), tune_knob("RLK_TUNE_GATHER_BS", bs):
+        with tune_knob("RLK_TUNE_GATHER_BS", bs), tune_knob("RLK_TUNE_GATHER_NT", nt):
             K.embedding_lookup(dev(torch, ids), dev(torch, table), n, hidden, out)
         assert_bits_equal(host(out), oracle.embedding_lookup(ids, table, hidden), "embedding")
 
@@ -242,20 +240,6 @@ def test_swiglu(torch_cuda, rows, inter, interleaved):
         assert rel_max_err(host(out), ref.numpy()) <= 3e-3
 
 
-@pytest.mark.parametrize("sp", [1, 2, 3])
-def test_swiglu_store_policies(torch_cuda, sp):
-    torch = torch_cuda
-    from redline_amd import kernels as K
-    from redline_amd._lib import tune_knob
-    say(f"swiglu store policy={sp}")
-    rng = np.random.default_rng(sp)
-    gu = randn_f16(rng, (33, 2 * 1032))
-    out = torch.empty((33, 1032), dtype=torch.float16, device="cuda")
-    with tune_knob("RLK_TUNE_STORE_POL", sp):
-        K.silu_and_mul(dev(torch, gu), 33, 1032, out)
-    assert_close_f16(host(out), oracle.silu_and_mul(gu, 1032), what="swiglu")
-
-
 @pytest.mark.parametrize("inter", [1, 3, 100, 1001])
 def test_swiglu_interleaved_any_width(torch_cuda, inter):
     torch = torch_cuda
@@ -297,3 +281,29 @@ def test_swiglu_qwen2_16k_sampled_rows(torch_cuda):
     sel = torch.arange(0, rows, 64, device="cuda")
     want = oracle.silu_and_mul(host(gu.index_select(0, sel)), inter)
     assert_close_f16(host(out.index_select(0, sel)), want, what="swiglu C5 rows")
+
+
+def test_timed_launch_records_dispatch(torch_cuda):
+    """A launch armed with rlk_time_next_launch runs the same kernel (same
+    output) and its events bound a positive duration."""
+    import ctypes as C
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    from redline_amd._lib import check, lib
+    say("timed launch")
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    a, b = C.c_void_p(), C.c_void_p()
+    assert hip.hipEventCreate(C.byref(a)) == 0 and hip.hipEventCreate(C.byref(b)) == 0
+    rng = np.random.default_rng(4)
+    gu = randn_f16(rng, (32, 2 * 14336))
+    out = torch.empty((32, 14336), dtype=torch.float16, device="cuda")
+    check(lib().rlk_time_next_launch(a, b))
+    K.silu_and_mul(dev(torch, gu), 32, 14336, out)
+    assert hip.hipEventSynchronize(b) == 0
+    ms = C.c_float()
+    assert hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
+    assert 0 < ms.value < 1.0
+    assert_close_f16(host(out), oracle.silu_and_mul(gu, 14336), what="swiglu (timed)")
+    hip.hipEventDestroy(a)
+    hip.hipEventDestroy(b)
