@@ -250,36 +250,83 @@ def per_kernel(torch, data, reps, only=None, names=KERNELS):
     return out
 
 
-def dispatch_durations(torch, fn, R, n=300):
-    """Average and median duration (us) of one dispatch of fn(r): each launch
-    is made with rlk_time_next_launch, so the library launches it through
-    hipExtLaunchKernel with a pair of HIP events that take the dispatch's own
-    begin and end timestamps on the launch stream -- the duration a
-    profiler's kernel trace records.  Launches are eager and synchronised one
-    by one, so each dispatch runs alone."""
-    import ctypes as C
+class _HipEvents:
+    """A pool of HIP events (libamdhip64 through ctypes) for timing single
+    dispatches with rlk_time_next_launch."""
+
+    def __init__(self, n):
+        import ctypes as C
+        self.C = C
+        self.hip = C.CDLL("libamdhip64.so")
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.ev = []
+        for _ in range(n):
+            e = C.c_void_p()
+            assert self.hip.hipEventCreate(C.byref(e)) == 0
+            self.ev.append(e)
+
+    def elapsed_us(self, a, b):
+        ms = self.C.c_float()
+        assert self.hip.hipEventSynchronize(self.ev[b]) == 0
+        assert self.hip.hipEventElapsedTime(self.C.byref(ms), self.ev[a], self.ev[b]) == 0
+        return ms.value * 1e3
+
+    def close(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+
+
+_SLEEP_CYCLES = None
+
+
+def _sleep_cycles(torch, ms=3.0):
+    """Argument of torch.cuda._sleep that holds the stream for about `ms`
+    (calibrated once with HIP events)."""
+    global _SLEEP_CYCLES
+    if _SLEEP_CYCLES is None:
+        probe = 1_000_000
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(probe)  # warm
+        a.record()
+        torch.cuda._sleep(probe)
+        b.record()
+        torch.cuda.synchronize()
+        per_ms = probe / max(a.elapsed_time(b), 1e-3)
+        _SLEEP_CYCLES = max(10_000, int(per_ms * ms))
+    return _SLEEP_CYCLES
+
+
+def dispatch_durations(torch, fn, R, batches=12, per_batch=None, isolated=False):
+    """Durations (us) of single dispatches of fn(r), each timed by a pair of
+    HIP events that rlk_time_next_launch binds to the dispatch itself
+    (hipExtLaunchKernel takes the dispatch's own begin and end timestamps on
+    the launch stream -- the per-dispatch duration a profiler's kernel trace
+    records).
+
+    Back to back (the default): each batch parks the stream behind a short
+    sleep kernel, enqueues `per_batch` timed launches meanwhile, and lets them
+    run back to back as in a graph replay.  isolated=True synchronises after
+    every launch instead, so each dispatch starts on an idle GPU.
+    Returns (mean, median)."""
     from redline_amd._lib import check, lib
-    hip = C.CDLL("libamdhip64.so")
-    hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-    evs = []
-    for _ in range(2):
-        e = C.c_void_p()
-        assert hip.hipEventCreate(C.byref(e)) == 0
-        evs.append(e)
+    per_batch = per_batch or min(R, 32)
+    ev = _HipEvents(2 * per_batch)
     us = []
     try:
-        for i in range(n + 5):
-            check(lib().rlk_time_next_launch(evs[0], evs[1]))
-            fn(i % R)
-            assert hip.hipEventSynchronize(evs[1]) == 0
-            ms = C.c_float()
-            assert hip.hipEventElapsedTime(C.byref(ms), evs[0], evs[1]) == 0
-            if i >= 5:  # the first launches warm the code object and caches
-                us.append(ms.value * 1e3)
+        for b in range(batches + 1):
+            if not isolated:
+                torch.cuda._sleep(_sleep_cycles(torch))  # holds the stream while the batch is enqueued
+            for i in range(per_batch):
+                check(lib().rlk_time_next_launch(ev.ev[2 * i], ev.ev[2 * i + 1]))
+                fn((b * per_batch + i) % R)
+                if isolated:
+                    torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            if b > 0:  # the first batch warms the code objects and caches
+                us += [ev.elapsed_us(2 * i, 2 * i + 1) for i in range(per_batch)]
     finally:
         check(lib().rlk_time_next_launch(None, None))
-        for e in evs:
-            hip.hipEventDestroy(e)
+        ev.close()
     us = np.array(us)
     return float(us.mean()), float(np.median(us))
 
@@ -736,11 +783,14 @@ def main():
     kern = per_kernel(torch, data, args.reps, args.only,
                       KERNELS + (STEP_EXTRA if args.only is None or args.only in STEP_EXTRA else ()))
     fns = kernel_fns(data)
-    for name, r in kern.items():  # each dispatch on its own, timed by its own events
+    for name, r in kern.items():  # dispatches timed by their own events
         mean, med = dispatch_durations(torch, fns[name], data.R)
+        iso, _ = dispatch_durations(torch, fns[name], data.R, batches=4, isolated=True)
         r["us_per_dispatch"] = round(mean, 3)
         r["us_per_dispatch_median"] = round(med, 3)
-        log(f"  {w.key} {name:26s} dispatch {mean:7.3f} us (median {med:7.3f})")
+        r["us_per_dispatch_isolated"] = round(iso, 3)
+        log(f"  {w.key} {name:26s} dispatch {mean:7.3f} us back to back (median {med:7.3f}), "
+            f"{iso:7.3f} us alone")
     rot = data.R
     del data
     torch.cuda.empty_cache()

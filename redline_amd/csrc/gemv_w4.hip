@@ -714,17 +714,10 @@ int launch(W4Args a, int wr_max, hipStream_t stream) {
   if (lds > 64 * 1024) {
     // dynamic LDS above 64 KiB must be granted per kernel and device; the
     // grant is remembered so that steady-state launches make no extra call
-    static size_t granted[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || granted[dev] < lds) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(kLdsBudget));
-      if (e != hipSuccess)
-        return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
-                    hipGetErrorString(e));
-      if (dev >= 0 && dev < 64) granted[dev] = kLdsBudget;
-    }
+    const hipError_t e = grant_dynamic_lds(reinterpret_cast<const void*>(kernel), kLdsBudget);
+    if (e != hipSuccess)
+      return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
+                  hipGetErrorString(e));
   }
   const int blocks = (tiles + wr - 1) / wr;
   kernel<<<blocks, 64 * wr * S, lds, stream>>>(a);
