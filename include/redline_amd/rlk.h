@@ -59,14 +59,6 @@ const char* rlk_last_error(void);
 /* Library version string. */
 const char* rlk_version(void);
 
-/* Measurement hook (no counterpart in the reference): the next launch of an
- * elementwise or RoPE kernel of this library on the calling thread records its
- * dispatch's own begin and end timestamps into `start` and `stop` (through
- * hipExtLaunchKernel), so hipEventElapsedTime(start, stop) is that kernel's
- * duration on the GPU.  The call after it is untimed again; both NULL
- * disarms.  Not for use under graph capture. */
-int rlk_time_next_launch(hipEvent_t start, hipEvent_t stop);
-
 /* Tuning hook (no counterpart in the reference): sets (set != 0) or clears
  * the launch-policy override `name` (one of RLK_TUNE_GATHER_BS, _GATHER_NT,
  * _NORM_TPR, _NORM_NT, _SWIGLU_BS, _SWIGLU_NT, _ROPE_WPT, _ATTN_PERSIST,

@@ -107,7 +107,6 @@ _SIGNATURES = {
     "rlk_last_error": (C.c_char_p, []),
     "rlk_version": (C.c_char_p, []),
     "rlk_set_tune_knob": (_I, [C.c_char_p, _I, _I]),
-    "rlk_time_next_launch": (_I, [_P, _P]),
     "rlk_embedding_lookup": (_I, [_P, _P, _I, _I, _P, _P]),
     "rlk_fused_add_rmsnorm": (_I, [_P, _P, _P, _I, _I, C.c_float, _P, _P]),
     "rlk_embedding_rmsnorm": (_I, [_P, _P, _I, _I, _P, C.c_float, _P, _P, _P]),

@@ -17,7 +17,6 @@
 #include <cstdint>
 
 #include "device.hpp"
-#include "launch.hpp"
 #include "redline_amd/rlk.h"
 #include "status.hpp"
 
@@ -67,8 +66,11 @@ void launch_gather_bs(bool nt, uint64_t total, const int32_t* idx, const u32x4* 
                       uint32_t vecs, u32x4* d, hipStream_t stream) {
   const uint32_t t32 = static_cast<uint32_t>(total);
   const uint64_t blocks = (total + BS - 1) / BS;
-  launch(nt ? gather_rows_kernel<BS, true> : gather_rows_kernel<BS, false>, blocks, BS, 0, stream,
-         idx, s, vecs, t32, d);
+  if (nt) {
+    gather_rows_kernel<BS, true><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
+  } else {
+    gather_rows_kernel<BS, false><<<blocks, BS, 0, stream>>>(idx, s, vecs, t32, d);
+  }
 }
 
 int launch_gather(const int32_t* idx, const void* src, int n, int vecs, void* dst,
@@ -210,9 +212,9 @@ int norm_src(const NormArgs& a) {
 
 template <int TPR, int NV, bool NT>
 void launch_norm_tn(const NormArgs& a, hipStream_t stream) {
-#define RLK_NORM_LAUNCH(S)                                                                 \
-  launch(add_rmsnorm_kernel<TPR, NV, S, NT>, a.rows, TPR, 0, stream, a.res, a.del, a.w, a.vecs, \
-         a.hidden, a.eps, a.out, a.ids)
+#define RLK_NORM_LAUNCH(S)                                                                       \
+  add_rmsnorm_kernel<TPR, NV, S, NT>                                                             \
+      <<<a.rows, TPR, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, a.eps, a.out, a.ids)
   switch (norm_src(a)) {
     case kDelta: RLK_NORM_LAUNCH(kDelta); break;
     case kGather: RLK_NORM_LAUNCH(kGather); break;
@@ -274,9 +276,9 @@ void launch_norm(const NormArgs& a, hipStream_t stream) {
   bool launched = nt ? launch_norm_nt<true>(tpr, a, stream) : launch_norm_nt<false>(tpr, a, stream);
   if (!launched) launched = launch_norm_nt<false>(512, a, stream);
   if (launched) return;
-#define RLK_NORM_WIDE(S)                                                                  \
-  launch(add_rmsnorm_wide_kernel<S>, a.rows, 256, 0, stream, a.res, a.del, a.w, a.vecs, a.hidden, \
-         a.eps, a.out, a.ids)
+#define RLK_NORM_WIDE(S)                                                                   \
+  add_rmsnorm_wide_kernel<S><<<a.rows, 256, 0, stream>>>(a.res, a.del, a.w, a.vecs, a.hidden, \
+                                                         a.eps, a.out, a.ids)
   switch (norm_src(a)) {
     case kDelta: RLK_NORM_WIDE(kDelta); break;
     case kGather: RLK_NORM_WIDE(kGather); break;
@@ -337,9 +339,9 @@ template <int BS, bool NT>
 void launch_swiglu_bs(bool interleaved, uint64_t blocks, const u32x4* gu, uint32_t vecs,
                       uint32_t total, u32x4* o, hipStream_t stream) {
   if (interleaved) {
-    launch(silu_and_mul_interleaved_kernel<BS, NT>, blocks, BS, 0, stream, gu, total, o);
+    silu_and_mul_interleaved_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, total, o);
   } else {
-    launch(silu_and_mul_kernel<BS, NT>, blocks, BS, 0, stream, gu, vecs, total, o);
+    silu_and_mul_kernel<BS, NT><<<blocks, BS, 0, stream>>>(gu, vecs, total, o);
   }
 }
 
@@ -470,9 +472,9 @@ extern "C" int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, i
                   static_cast<uint32_t>(pairs / 8), reinterpret_cast<u32x4*>(out), stream);
   } else {
     const uint64_t blocks = (pairs + 255) / 256;
-    launch(silu_and_mul_interleaved_scalar_kernel, blocks, 256, 0, stream,
-           reinterpret_cast<const f16x2*>(gate_up), static_cast<int64_t>(pairs),
-           reinterpret_cast<_Float16*>(out));
+    silu_and_mul_interleaved_scalar_kernel<<<blocks, 256, 0, stream>>>(
+        reinterpret_cast<const f16x2*>(gate_up), static_cast<int64_t>(pairs),
+        reinterpret_cast<_Float16*>(out));
   }
   return launch_status("silu_and_mul_interleaved");
 }

@@ -25,7 +25,6 @@
 #include <cstdint>
 
 #include "device.hpp"
-#include "launch.hpp"
 #include "redline_amd/rlk.h"
 #include "status.hpp"
 
@@ -150,14 +149,14 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
 template <int D, bool kInt8>
 void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
   switch (wpt) {
-    case 1: launch(rope_kv_kernel<D, kInt8, 1>, a.num_tokens, 1 * kWave, 0, stream, a); break;
-    case 2: launch(rope_kv_kernel<D, kInt8, 2>, a.num_tokens, 2 * kWave, 0, stream, a); break;
-    case 3: launch(rope_kv_kernel<D, kInt8, 3>, a.num_tokens, 3 * kWave, 0, stream, a); break;
-    case 4: launch(rope_kv_kernel<D, kInt8, 4>, a.num_tokens, 4 * kWave, 0, stream, a); break;
-    case 5: launch(rope_kv_kernel<D, kInt8, 5>, a.num_tokens, 5 * kWave, 0, stream, a); break;
-    case 6: launch(rope_kv_kernel<D, kInt8, 6>, a.num_tokens, 6 * kWave, 0, stream, a); break;
-    case 7: launch(rope_kv_kernel<D, kInt8, 7>, a.num_tokens, 7 * kWave, 0, stream, a); break;
-    default: launch(rope_kv_kernel<D, kInt8, 8>, a.num_tokens, 8 * kWave, 0, stream, a); break;
+    case 1: rope_kv_kernel<D, kInt8, 1><<<a.num_tokens, 1 * kWave, 0, stream>>>(a); break;
+    case 2: rope_kv_kernel<D, kInt8, 2><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
+    case 3: rope_kv_kernel<D, kInt8, 3><<<a.num_tokens, 3 * kWave, 0, stream>>>(a); break;
+    case 4: rope_kv_kernel<D, kInt8, 4><<<a.num_tokens, 4 * kWave, 0, stream>>>(a); break;
+    case 5: rope_kv_kernel<D, kInt8, 5><<<a.num_tokens, 5 * kWave, 0, stream>>>(a); break;
+    case 6: rope_kv_kernel<D, kInt8, 6><<<a.num_tokens, 6 * kWave, 0, stream>>>(a); break;
+    case 7: rope_kv_kernel<D, kInt8, 7><<<a.num_tokens, 7 * kWave, 0, stream>>>(a); break;
+    default: rope_kv_kernel<D, kInt8, 8><<<a.num_tokens, 8 * kWave, 0, stream>>>(a); break;
   }
 }
 

@@ -14,14 +14,7 @@
 namespace rlk {
 namespace {
 thread_local char g_message[512] = "";
-thread_local LaunchEvents g_launch_events = {nullptr, nullptr};
 }  // namespace
-
-LaunchEvents take_launch_events() {
-  const LaunchEvents ev = g_launch_events;
-  g_launch_events = LaunchEvents{nullptr, nullptr};
-  return ev;
-}
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -115,13 +108,6 @@ int tune_knob(Knob knob, int fallback) {
 }  // namespace rlk
 
 extern "C" const char* rlk_last_error(void) { return rlk::g_message; }
-
-extern "C" int rlk_time_next_launch(hipEvent_t start, hipEvent_t stop) {
-  if ((start == nullptr) != (stop == nullptr))
-    return rlk::fail(RLK_EINVAL, "rlk_time_next_launch: give both events or neither");
-  rlk::g_launch_events = rlk::LaunchEvents{start, stop};
-  return RLK_OK;
-}
 
 extern "C" int rlk_set_tune_knob(const char* name, int value, int set) {
   std::call_once(rlk::g_knobs_once, rlk::read_knobs_from_env);

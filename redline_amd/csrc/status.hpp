@@ -20,14 +20,6 @@ int launch_status(const char* what);
 // fails).
 int compute_units();
 
-// Events armed by rlk_time_next_launch on the calling thread for its next
-// launch ({null, null} when none); the call disarms them.
-struct LaunchEvents {
-  hipEvent_t start;
-  hipEvent_t stop;
-};
-LaunchEvents take_launch_events();
-
 // Raises the dynamic-LDS limit of `kernel` on the current device to at least
 // `bytes` (hipFuncSetAttribute), once per (device, kernel) and size: later
 // calls are a lookup.

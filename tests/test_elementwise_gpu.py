@@ -281,29 +281,3 @@ def test_swiglu_qwen2_16k_sampled_rows(torch_cuda):
     sel = torch.arange(0, rows, 64, device="cuda")
     want = oracle.silu_and_mul(host(gu.index_select(0, sel)), inter)
     assert_close_f16(host(out.index_select(0, sel)), want, what="swiglu C5 rows")
-
-
-def test_timed_launch_records_dispatch(torch_cuda):
-    """A launch armed with rlk_time_next_launch runs the same kernel (same
-    output) and its events bound a positive duration."""
-    import ctypes as C
-    torch = torch_cuda
-    from redline_amd import kernels as K
-    from redline_amd._lib import check, lib
-    say("timed launch")
-    hip = C.CDLL("libamdhip64.so")
-    hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-    a, b = C.c_void_p(), C.c_void_p()
-    assert hip.hipEventCreate(C.byref(a)) == 0 and hip.hipEventCreate(C.byref(b)) == 0
-    rng = np.random.default_rng(4)
-    gu = randn_f16(rng, (32, 2 * 14336))
-    out = torch.empty((32, 14336), dtype=torch.float16, device="cuda")
-    check(lib().rlk_time_next_launch(a, b))
-    K.silu_and_mul(dev(torch, gu), 32, 14336, out)
-    assert hip.hipEventSynchronize(b) == 0
-    ms = C.c_float()
-    assert hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
-    assert 0 < ms.value < 1.0
-    assert_close_f16(host(out), oracle.silu_and_mul(gu, 14336), what="swiglu (timed)")
-    hip.hipEventDestroy(a)
-    hip.hipEventDestroy(b)

@@ -303,10 +303,3 @@ def test_tune_knobs_set_and_clear():
     assert b"unknown knob" in L.rlk_last_error()
     with _lib.tune_knob("RLK_TUNE_W4_CFG", 2):
         pass
-
-
-def test_time_next_launch_arguments():
-    L = ra.lib()
-    assert L.rlk_time_next_launch(C.c_void_p(16), None) == _lib.RLK_EINVAL
-    assert b"both events" in L.rlk_last_error()
-    assert L.rlk_time_next_launch(None, None) == 0
