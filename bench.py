@@ -109,6 +109,12 @@ class LayerData:
         s, m = self.sets[r], self.w.model
         self.K.silu_and_mul(s["gu"], self.T, m.inter, s["act"])
 
+    def stream_copy(self, r):
+        """Yardstick: a plain contiguous copy of T hidden rows (the identity
+        gather_rows), the embedding gather's bytes without the random rows."""
+        s, m = self.sets[r], self.w.model
+        self.K.gather_rows(s["res"], None, self.T, m.hidden, s["normed"])
+
     def norm_first(self, r):
         """The layer's first norm: fused_add_rmsnorm(delta=None) on the
         residual the embedding gather just wrote (llama.cpp:79-80)."""
@@ -146,6 +152,7 @@ class LayerData:
         return {
             "embedding_lookup": C.bytes_embedding(T, m.hidden),
             "embedding_rmsnorm": C.bytes_embedding_rmsnorm(T, m.hidden),
+            "stream_copy": 4 * T * m.hidden,
             "fused_add_rmsnorm_nodelta": C.bytes_add_rmsnorm(T, m.hidden, delta=False),
             "fused_add_rmsnorm": C.bytes_add_rmsnorm(T, m.hidden),
             "rope_and_write_kv": C.bytes_rope_kv(T, m.hq, m.hkv, m.head_dim, self.w.kv_int8,
@@ -239,7 +246,8 @@ STEP_EXTRA = ("embedding_rmsnorm", "fused_add_rmsnorm_nodelta")
 def kernel_fns(data):
     return {"embedding_lookup": data.embedding, "fused_add_rmsnorm": data.norm,
             "rope_and_write_kv": data.rope, "silu_and_mul": data.swiglu,
-            "embedding_rmsnorm": data.embedding_norm, "fused_add_rmsnorm_nodelta": data.norm_first}
+            "embedding_rmsnorm": data.embedding_norm, "fused_add_rmsnorm_nodelta": data.norm_first,
+            "stream_copy": data.stream_copy}
 
 
 def per_kernel(torch, data, reps, only=None, names=KERNELS):
@@ -624,7 +632,7 @@ def main():
     if args.only == "gemv_w4a16_swiglu" and not args.profile_calls:
         res = []
         for m in (1, 8, 16, 32):
-            for cfg in (range(8) if args.sweep else [None]):
+            for cfg in (range(12) if args.sweep else [None]):
                 if cfg is not None:
                     from redline_amd._lib import set_tune_knob
                     set_tune_knob("RLK_TUNE_W4_CFG", cfg)
@@ -752,7 +760,7 @@ def main():
             wx = make_workload(key)
             log(f"setting up {key} ({wx.model.name}, T={wx.num_tokens})")
             dx = LayerData(torch, K, wx)
-            extra[key] = per_kernel(torch, dx, max(3, args.reps // 4))
+            extra[key] = per_kernel(torch, dx, max(3, args.reps // 4), names=KERNELS + ("stream_copy",))
             del dx
             torch.cuda.empty_cache()
 

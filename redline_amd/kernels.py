@@ -162,10 +162,12 @@ def gemv_w4a16_swiglu(x, m, w, scales, offsets, group_size, n, k, y, stream=None
 
 
 def gather_rows(src, idx, n, cols, dst, stream=None):
-    """dst[i, :] = src[idx[i], :]."""
+    """dst[i, :] = src[idx[i], :] (idx None: dst[i, :] = src[i, :])."""
     if n > 0:
-        _need(idx, n, "idx"); _need(dst, n * cols, "dst")
-    check(lib().rlk_gather_rows(_ptr(src, torch.float16, "src"), _ptr(idx, torch.int32, "idx"), n, cols,
+        if idx is not None:
+            _need(idx, n, "idx")
+        _need(dst, n * cols, "dst")
+    check(lib().rlk_gather_rows(_ptr(src, torch.float16, "src"), _ptr(idx, torch.int32, "idx", True), n, cols,
                                 _ptr(dst, torch.float16, "dst"), _stream(stream)))
 
 
