@@ -177,9 +177,10 @@ def measured_traffic(workload, kernel_prefix):
     return None
 
 
-def trace_average_us(workload, kernel_prefix):
-    """Average dispatch duration (us) of a kernel in the committed rocprofv3
-    kernel-trace summary profiles/kernel_trace_C2_C5.md (None when absent)."""
+def trace_average_us(workload, kernel_prefix, name):
+    """Average dispatch duration (us) of kernel `name` (symbol prefix
+    kernel_prefix) in the committed rocprofv3 kernel-trace summary
+    profiles/kernel_trace_C2_C5.md (None when absent)."""
     path = os.path.join(ROOT, "profiles", "kernel_trace_C2_C5.md")
     try:
         lines = open(path).read().splitlines()
@@ -187,8 +188,9 @@ def trace_average_us(workload, kernel_prefix):
         return None
     for line in lines:
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) == 7 and cells[0] == workload and cells[1].startswith("`" + kernel_prefix):
-            return float(cells[3])
+        if (len(cells) == 10 and cells[0] == workload and cells[1].startswith("`" + kernel_prefix)
+                and cells[2] == name):
+            return float(cells[4])
     return None
 
 
@@ -737,7 +739,7 @@ def main():
     # rocprofv3 kernel trace of this command (profiles/kernel_trace_C2_C5.md).
     dominant = max(KERNELS, key=lambda k: nb[k])
     dk = kern[dominant]
-    trace_us = trace_average_us(w.key, KERNEL_SYMBOL[dominant])
+    trace_us = trace_average_us(w.key, KERNEL_SYMBOL[dominant], dominant)
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": dk["gb_per_s"],
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dk["frac_of_hbm_peak"],
                 "us_per_launch": dk["us_per_call"],

@@ -37,6 +37,7 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kPart = RLK_DECODE_PARTITION_SIZE;  // keys per partition
+constexpr int kRedPad = 4;  // floats of padding per row of the waves' partial outputs in LDS
 
 struct AttnArgs {
   rlk_attention_params p;
@@ -210,6 +211,18 @@ __device__ __forceinline__ float row_bcast(float v, int g) {
   }
 }
 
+// What the softmax hands to P . V: fp16 pairs of probabilities per pass pair
+// and head for the v_dot2 form, or the B operand of the MFMA form (this
+// lane's 8 keys for its head column).
+template <int D, int G, bool kMma>
+struct PvOperand {
+  f16x2 pp[Geo<D>::kPasses / 2][G];
+};
+template <int D, int G>
+struct PvOperand<D, G, true> {
+  f16x8 b;
+};
+
 // Scores s = scale * (q_g . k) * k_scale on the matrix cores, then the
 // softmax over the wave's keys per head: p = exp(s - m_g) (0 past the
 // context), with the wave's max m and sum l per head stored to stat[wave]
@@ -218,10 +231,10 @@ __device__ __forceinline__ float row_bcast(float v, int g) {
 // of this lane's key slot as fp16 pairs per head: the operands of
 // v_dot2_f32_f16.  `then` runs once the K rows are consumed (the persistent
 // form requests the next unit's K rows into the same registers there).
-template <int D, int G, bool kInt8, class Then>
+template <int D, int G, bool kInt8, bool kMma, class Then>
 __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _Float16* qs,
-                                            const float* ksc, float scale, int n, const LaneCoord& c,
-                                            f16x2 (&pp)[Geo<D>::kPasses / 2][G],
+                                            const float* ksc, const float* vsc, float scale, int n,
+                                            const LaneCoord& c, PvOperand<D, G, kMma>& po,
                                             float (&stat)[kWaves][G][2], Then then) {
   constexpr int kSteps = D / 32, kP = Geo<D>::kPasses;
   const int lane = c.tid % kWave, g = lane % 16, rho = lane / 16;
@@ -274,6 +287,22 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
     stat[c.wave][g][0] = m;
     stat[c.wave][g][1] = l;
   }
+  if constexpr (kMma) {
+    // B operand of the P . V MFMA (K = 32 keys x N = 16 head columns): lane
+    // (rho, g) supplies k = 8 rho + 4 t + i, the scores it holds, times the
+    // key's INT8 v scale
+    f16x8 b;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      float v = e[x / 4][x % 4];
+      if constexpr (kInt8) v *= vsc[mma_key<D>(c, x / 4, 4 * rho + x % 4)];
+      b[x] = static_cast<_Float16>(v);
+    }
+    po.b = b;
+    return;
+  } else {
+  auto& pp = po.pp;
+  (void)vsc;
   // to the P . V layout: pass u of this lane's key slot is (t, i) = (u / 4,
   // u % 4) of its row (D = 128), or (t, i) = (half of the row, u) (D = 64)
 #pragma unroll
@@ -293,6 +322,7 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
       }
       pp[h][gg] = f16x2{static_cast<_Float16>(pr[0]), static_cast<_Float16>(pr[1])};
     }
+  }
 }
 
 // P . V for this thread's 8 output dims and G heads, fp32 accumulation of
@@ -311,9 +341,10 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
 // unit's V rows into the same registers there).
 template <int D, int G, bool kInt8, class Then>
 __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const float* vsc,
-                                        const f16x2 (&pp)[Geo<D>::kPasses / 2][G], const LaneCoord& c,
-                                        float (&red)[kWaves][G][D], Then then) {
+                                        const PvOperand<D, G, false>& po, const LaneCoord& c,
+                                        float (&red)[kWaves][G][D + kRedPad], Then then) {
   constexpr int kP = Geo<D>::kPasses, kN = G * 8;
+  const auto& pp = po.pp;
   float v[kN];
 #pragma unroll
   for (int h = 0; h < kP / 2; ++h) {
@@ -370,11 +401,128 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const floa
   }
 }
 
+// INT8 codes of 8 keys (the 8 k-slots of an MFMA operand) at 4 dims to
+// fp16: w[kk] holds key kk's codes of the 4 dims, sign bits already flipped
+// (code + 128 in each byte); a[j][kk] = code of dim j of key kk, exactly.
+// Bytes of keys (2p, 2p + 1) are interleaved by two permutes, then each pair
+// gets the 0x64 high bytes (fp16 1024 + byte) and one packed subtract of 1152.
+__device__ __forceinline__ void int8_cols_to_f16(const uint32_t (&w)[8], f16x8 (&a)[4]) {
+#pragma unroll
+  for (int pr = 0; pr < 4; ++pr) {
+    // selectors 0-3 pick from the second source, 4-7 from the first
+    const uint32_t t01 = __builtin_amdgcn_perm(w[2 * pr + 1], w[2 * pr], 0x05010400u);
+    const uint32_t t23 = __builtin_amdgcn_perm(w[2 * pr + 1], w[2 * pr], 0x07030602u);
+    const uint32_t h[4] = {__builtin_amdgcn_perm(0x64646464u, t01, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, t01, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, t23, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, t23, 0x04030402u)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x2 v = __builtin_bit_cast(f16x2, h[j]) - static_cast<_Float16>(1152);
+      a[j][2 * pr] = v[0];
+      a[j][2 * pr + 1] = v[1];
+    }
+  }
+}
+
+// P . V on the matrix cores: per dim tile, one v_mfma_f32_16x16x32_f16 with V
+// as A (16 dims x 32 keys: the wave's keys) and the probabilities as B (32
+// keys x 16 head columns, from the softmax).  The dims of a tile are chosen
+// so that every lane feeds A from rows it already holds: lane (rho, m)
+// supplies A row m at k-slot rho, keys k = 8 rho + kk.
+//   D = 128 (16 lanes per key row): lane m holds dims 8m .. 8m + 7 of its key
+//     slot rho over the 8 passes kk; tile dt takes dim 8m + dt, i.e. element
+//     dt of each of the lane's 8 rows -- no data leaves the lane.
+//   D = 64 (8 lanes per key row): the k-slot's keys span slots 2 rho and
+//     2 rho + 1 (passes 0..3 each), held by lanes m and m ^ 8; tile dt takes
+//     dim 8 (m % 8) + 4 (m / 8) + dt, so each lane keeps half of its row
+//     elements and receives the other slot's half from lane m ^ 8 (one DPP
+//     row rotation by 8 per dword).
+// Output: lane (rho, g) receives rows 4 rho + i of head column g, i.e. head
+// g's partial output at the dims of rows 4 rho + i, written to red[wave] for
+// g < G.  `then` runs once the V rows are consumed.
+template <int D, int G, bool kInt8, class Then>
+__device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const PvOperand<D, G, true>& po,
+                                            const LaneCoord& c, float (&red)[kWaves][G][D + kRedPad],
+                                            Then then) {
+  constexpr int kTiles = D / 16;
+  const int lane = c.tid % kWave, rho = lane / 16, m = lane % 16;
+  f16x8 a[kTiles];
+  if constexpr (D == 128) {
+    if constexpr (!kInt8) {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const f16x8 row = __builtin_bit_cast(f16x8, vb.r[kk]);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) a[dt][kk] = row[dt];
+      }
+    } else {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {  // dims 4 half .. 4 half + 3 of the lane's 8
+        uint32_t w[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) w[kk] = vb.r[kk][half] ^ 0x80808080u;
+        f16x8 q[4];
+        int8_cols_to_f16(w, q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[4 * half + j] = q[j];
+      }
+    }
+  } else {  // D = 64: keep half the row elements, swap the other half with lane m ^ 8
+    const bool t1 = m >= 8;  // this lane's key slot is 2 rho + 1 (k-slots 4..7)
+    if constexpr (!kInt8) {
+      u32x2 own[4], other[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x4 r = vb.r[u];
+        const u32x2 lo = {r.x, r.y}, hi = {r.z, r.w};
+        own[u] = t1 ? hi : lo;
+        const u32x2 send = t1 ? lo : hi;  // what the partner keeps
+        other[u] = u32x2{static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(send.x), 0x128, 0xF, 0xF, false)),
+                         static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(send.y), 0x128, 0xF, 0xF, false))};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f16x4 mine = __builtin_bit_cast(f16x4, own[u]), theirs = __builtin_bit_cast(f16x4, other[u]);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          a[dt][u] = t1 ? theirs[dt] : mine[dt];      // slot 2 rho, pass u
+          a[dt][4 + u] = t1 ? mine[dt] : theirs[dt];  // slot 2 rho + 1, pass u
+        }
+      }
+    } else {
+      uint32_t w[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x2 r = vb.r[u];
+        const uint32_t own = t1 ? r.y : r.x, send = t1 ? r.x : r.y;
+        const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(send), 0x128, 0xF, 0xF, false));
+        w[u] = (t1 ? other : own) ^ 0x80808080u;
+        w[4 + u] = (t1 ? own : other) ^ 0x80808080u;
+      }
+      int8_cols_to_f16(w, a);
+    }
+  }
+  then();
+#pragma unroll
+  for (int dt = 0; dt < kTiles; ++dt) {
+    const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], po.b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    if (m < G) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * rho + i;
+        const int dim = D == 128 ? 8 * r + dt : 8 * (r % 8) + 4 * (r / 8) + dt;
+        red[c.wave][m][dim] = o[i];
+      }
+    }
+  }
+}
+
 // Combines the waves of a unit: M = max m_w, L = sum e^(m_w - M) l_w,
 // o = sum e^(m_w - M) o_w / L; written as the output row (one partition) or
 // as the unit's split-K partial row.
 template <int D, int G>
-__device__ __forceinline__ void combine_waves(const AttnArgs& args, const float (&red)[kWaves][G][D],
+__device__ __forceinline__ void combine_waves(const AttnArgs& args, const float (&red)[kWaves][G][D + kRedPad],
                                               const float (&stat)[kWaves][G][2], int tid, int item,
                                               int token, int num_parts, int part, int kvh) {
   const rlk_attention_params& p = args.p;
@@ -411,7 +559,7 @@ __device__ __forceinline__ void combine_waves(const AttnArgs& args, const float 
 // form (the next unit's are written while the current one computes).
 template <int D, int G>
 struct UnitLds {
-  float red[kWaves][G][D];   // each wave's P . V partial
+  float red[kWaves][G][D + kRedPad];  // each wave's P . V partial
   float stat[kWaves][G][2];  // each wave's (max, sum) per head
   int cell[2][kPart];        // cache cell of each key of the partition
   float ksc[2][kPart];       // its INT8 k and v scales
@@ -489,9 +637,8 @@ struct UnitPos {
   int item, part, kvh;
 };
 
-template <int D, int G, bool kInt8>
+template <int D, int G, bool kInt8, bool kMma>
 __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_persistent(AttnArgs args) {
-  constexpr int kP = Geo<D>::kPasses;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ UnitLds<D, G> s;
@@ -597,15 +744,21 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     u32x4 qn = {0, 0, 0, 0};
     if (has1 && q_piece<D, G>(c.tid)) qn = load_q_piece<D, G>(p, c.tid, it_tok[nxt.item], nxt.kvh);
 
-    f16x2 pp[kP / 2][G];
-    wave_softmax<D, G, kInt8>(kb, s.q[b], s.ksc[b], p.scale, keys_in(cur), c, pp, s.stat, [&] {
+    PvOperand<D, G, kMma> po;
+    wave_softmax<D, G, kInt8, kMma>(kb, s.q[b], s.ksc[b], s.vsc[b], p.scale, keys_in(cur), c, po,
+                                    s.stat, [&] {
       if (has1) issue_keys<D, kInt8>(kb, p.kv.k, s.cell[b ^ 1], keys_in(nxt), c);
     });
     // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
     if (has1 && q_piece<D, G>(c.tid)) store16(s.q[b ^ 1] + (c.tid - kPart) * 8, qn);
-    wave_pv<D, G, kInt8>(vb, s.vsc[b], pp, c, s.red, [&] {
+    auto next_rows = [&] {
       if (has1) issue_rows<D, kInt8>(vb, p.kv.v, s.cell[b ^ 1], keys_in(nxt), c);
-    });
+    };
+    if constexpr (kMma) {
+      wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, next_rows);
+    } else {
+      wave_pv<D, G, kInt8>(vb, s.vsc[b], po, c, s.red, next_rows);
+    }
     __syncthreads();
 
     // scales(n+1) go to the buffers unit n-1 read (free since its barriers);
@@ -626,9 +779,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
 
 // Grid form: one workgroup per (partition, kv head, item), exiting at once
 // when the partition lies past the item's context; the same stages, in order.
-template <int D, int G, bool kInt8>
+template <int D, int G, bool kInt8, bool kMma>
 __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_kernel(AttnArgs args) {
-  constexpr int kP = Geo<D>::kPasses;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ UnitLds<D, G> s;
@@ -653,9 +805,13 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   RowBatch<D, kInt8> vb;
   issue_keys<D, kInt8>(kb, p.kv.k, s.cell[0], n, c);
   issue_rows<D, kInt8>(vb, p.kv.v, s.cell[0], n, c);
-  f16x2 pp[kP / 2][G];
-  wave_softmax<D, G, kInt8>(kb, s.q[0], s.ksc[0], p.scale, n, c, pp, s.stat, [] {});
-  wave_pv<D, G, kInt8>(vb, s.vsc[0], pp, c, s.red, [] {});
+  PvOperand<D, G, kMma> po;
+  wave_softmax<D, G, kInt8, kMma>(kb, s.q[0], s.ksc[0], s.vsc[0], p.scale, n, c, po, s.stat, [] {});
+  if constexpr (kMma) {
+    wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, [] {});
+  } else {
+    wave_pv<D, G, kInt8>(vb, s.vsc[0], po, c, s.red, [] {});
+  }
   __syncthreads();
   combine_waves<D, G>(args, s.red, s.stat, tid, item, token,
                       min((ctx + kPart - 1) / kPart, w.max_partitions), part, kvh);
@@ -722,24 +878,34 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
 // The persistent form (two workgroups per CU) serves batches of up to
 // kMaxItemsLds decode items, the grid form larger ones.  RLK_TUNE_ATTN_PERSIST
 // overrides: workgroups per CU for the persistent form, or 0 for the grid form.
-template <int D, int G>
-void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
+template <int D, int G, bool kMma>
+void launch_gm(const AttnArgs& a, bool int8, hipStream_t stream) {
   const int mode = tune_knob(kAttnPersist, 2);
   if (mode > 0 && a.w.num_items <= kMaxItemsLds) {
     const int64_t units = static_cast<int64_t>(a.w.num_items) * a.w.max_partitions * a.p.kv.num_kv_heads;
     const int blocks = static_cast<int>(std::min<int64_t>(units, static_cast<int64_t>(compute_units()) * mode));
     if (int8) {
-      decode_attention_persistent<D, G, true><<<blocks, kThreads, 0, stream>>>(a);
+      decode_attention_persistent<D, G, true, kMma><<<blocks, kThreads, 0, stream>>>(a);
     } else {
-      decode_attention_persistent<D, G, false><<<blocks, kThreads, 0, stream>>>(a);
+      decode_attention_persistent<D, G, false, kMma><<<blocks, kThreads, 0, stream>>>(a);
     }
     return;
   }
   const dim3 grid(a.w.max_partitions, a.p.kv.num_kv_heads, a.w.num_items);
   if (int8) {
-    decode_attention_kernel<D, G, true><<<grid, kThreads, 0, stream>>>(a);
+    decode_attention_kernel<D, G, true, kMma><<<grid, kThreads, 0, stream>>>(a);
   } else {
-    decode_attention_kernel<D, G, false><<<grid, kThreads, 0, stream>>>(a);
+    decode_attention_kernel<D, G, false, kMma><<<grid, kThreads, 0, stream>>>(a);
+  }
+}
+
+// P . V on v_dot2 (RLK_TUNE_ATTN_PV = 0) or on the matrix cores (1).
+template <int D, int G>
+void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
+  if (tune_knob(kAttnPv, 0) == 1) {
+    launch_gm<D, G, true>(a, int8, stream);
+  } else {
+    launch_gm<D, G, false>(a, int8, stream);
   }
 }
 
