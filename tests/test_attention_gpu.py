@@ -42,15 +42,15 @@ def run_attention(torch, K, d_q, q_stride, hq, scale, cache, d_tables, max_block
     return out.cpu().numpy()
 
 
-@pytest.fixture(params=["default", "grid", "persistent", "grid-mfma", "persistent-mfma"])
+@pytest.fixture(params=["default", "grid", "persistent", "grid-dot2", "persistent-dot2"])
 def attention_form(request):
     """The launcher's two kernel forms -- one workgroup per (partition, kv
     head, item), or persistent workgroups over the in-context units only
     (RLK_TUNE_ATTN_PERSIST = 0 or workgroups per CU) -- each with P . V on
-    v_dot2 or on the matrix cores (RLK_TUNE_ATTN_PV = 0 or 1)."""
+    the matrix cores (the default) or on v_dot2 (RLK_TUNE_ATTN_PV = 0)."""
     from redline_amd._lib import tune_knob
     form = request.param.split("-")[0]
-    pv = 1 if request.param.endswith("mfma") else None
+    pv = 0 if request.param.endswith("dot2") else None
     with tune_knob("RLK_TUNE_ATTN_PERSIST", {"grid": 0, "persistent": 2}.get(form)), \
             tune_knob("RLK_TUNE_ATTN_PV", pv):
         yield request.param
