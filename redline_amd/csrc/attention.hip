@@ -15,9 +15,11 @@
 //     operand, the G heads of the group as B columns); the keys are numbered
 //     so that each lane receives scores of keys its own row of 16 lanes uses
 //     in P . V, and the softmax runs once per (key, head) on that output;
-//   * P . V reads V rows 8 elements per lane and accumulates fp16 pairs of
-//     probabilities with v_dot2_f32_f16 (fp32); the key slots of a wave are
-//     summed with permlane swaps and the 8 waves combined through LDS;
+//   * P . V runs on the matrix cores too: V rows (8 elements per lane) are
+//     the A operand in a dim order that keeps every element in the lane that
+//     loaded it, and the softmax output is the B operand as it stands; the 8
+//     waves' partial outputs are combined through LDS (a v_dot2 form of P . V
+//     remains selectable);
 //   * INT8 codes become exact fp16 values through byte permutes under an
 //     fp16 exponent, without conversion instructions.
 #include <hip/hip_runtime.h>
