@@ -145,6 +145,14 @@ int main(int argc, char** argv) {
     kernels::embedding_lookup(ids, table, 7, 256, out, stream);
     HIP_OK(hipStreamSynchronize(stream));
     check_exact("embedding_lookup", out, "emb_out");
+    // extension: the gather and RMSNorm (no delta) in one launch
+    auto* w = upload<half>("embnorm_w");
+    auto* res = upload<half>("emb_out", true);
+    auto* normed = upload<half>("emb_out", true);
+    kernels::embedding_rmsnorm(ids, table, 7, 256, w, 1e-5f, res, normed, stream);
+    HIP_OK(hipStreamSynchronize(stream));
+    check_exact("embedding_rmsnorm residual", res, "emb_out");
+    check_close("embedding_rmsnorm out", normed, "embnorm_out");
   }
   {  // fused_add_rmsnorm with delta, then without (on the original residual)
     auto* res = upload<half>("norm_res");

@@ -4,7 +4,8 @@ the C++ drop-in header (redline::kernels).  The expected outputs come from the
 CPU oracle (oracle/), itself pinned by tests/test_oracle.py.
 
 Cases mirror the reference's kernel tests (tests/cuda/test_kernels.cu in
-Neil456/Redline): fused_add_rmsnorm 5 x 512 with and without delta (:18-47),
+Neil456/Redline), plus the embedding_rmsnorm extension over the embedding case:
+fused_add_rmsnorm 5 x 512 with and without delta (:18-47),
 silu_and_mul and embedding_lookup (:48-69), rope_and_write_kv FP16 over a
 shuffled paged pool and decode attention over the cache it wrote (:90-148,
 geometry hq 8, hkv 1, D 64, lengths 48 and 17: :285), and the INT8 KV write
@@ -40,7 +41,11 @@ def main():
     # embedding_lookup: V 64, H 256, 7 ids
     table = f16(rng, 64, 256, scale=0.02)
     ids = rng.integers(0, 64, 7).astype(np.int32)
-    arrs.update(emb_table=table, emb_ids=ids, emb_out=oracle.embedding_lookup(ids, table, 256))
+    emb = oracle.embedding_lookup(ids, table, 256)
+    arrs.update(emb_table=table, emb_ids=ids, emb_out=emb)
+    # embedding_rmsnorm (extension): the gathered rows, then RMSNorm without delta
+    wn = (1 + 0.1 * rng.standard_normal(256)).astype(np.float16)
+    arrs.update(embnorm_w=wn, embnorm_out=oracle.fused_add_rmsnorm(emb, None, wn, 1e-5)[1])
 
     # fused_add_rmsnorm: 5 x 512, eps 1e-5, with delta and without
     res, delta = f16(rng, 5, 512), f16(rng, 5, 512)

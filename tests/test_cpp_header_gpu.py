@@ -1,7 +1,8 @@
 """The kernels launched through the C++ drop-in header (redline::kernels,
 include/redline_amd/kernels.h) by a compiled program, as the reference's own
 kernel tests call them (tests/cuda/test_kernels.cu:18-69,90-148,289-322 in
-Neil456/Redline): embedding, add+RMSNorm with and without delta, SwiGLU
+Neil456/Redline): embedding (and the embedding_rmsnorm extension), add+RMSNorm
+with and without delta, SwiGLU
 split and interleaved, RoPE + FP16 paged-KV write, decode attention over that
 cache, and the INT8 KV write with scales, against the oracle's fixtures in
 tests/golden/kernels_cpp.bin (bit-exact for the gather, residual, q, cells,

@@ -303,3 +303,13 @@ def test_tune_knobs_set_and_clear():
     assert b"unknown knob" in L.rlk_last_error()
     with _lib.tune_knob("RLK_TUNE_W4_CFG", 2):
         pass
+
+
+def test_embedding_rmsnorm_argument_errors():
+    L = ra.lib()
+    d = C.c_void_p(16)
+    assert L.rlk_embedding_rmsnorm(d, d, 0, 12, d, 1e-5, d, d, None) == 0  # n <= 0: no-op
+    assert L.rlk_embedding_rmsnorm(d, d, 4, 12, d, 1e-5, d, d, None) == _lib.RLK_EINVAL
+    assert b"multiple of 8" in L.rlk_last_error()
+    assert L.rlk_embedding_rmsnorm(d, None, 4, 16, d, 1e-5, d, d, None) == _lib.RLK_EINVAL
+    assert b"null pointer" in L.rlk_last_error()
