@@ -97,6 +97,11 @@ def ref() -> C.CDLL:
         L.ref_half_bits_to_float.restype, L.ref_half_bits_to_float.argtypes = C.c_float, [C.c_uint16]
         L.ref_float_to_half_many.argtypes = [_P, C.c_size_t, _P]
         L.ref_quantize_int8_rows.argtypes = [_P, _I, _I, _P, _P]
+        L.ref_model_config_json.restype = _I
+        L.ref_model_config_json.argtypes = [_I, _I, _I, _I, _I, _I, _I, C.c_double, C.c_double,
+                                            C.c_char_p, _I]
+        L.ref_model_forward.restype = _I
+        L.ref_model_forward.argtypes = [C.c_char_p, _P, _I, _P]
         L.ref_quantize_int4_groups.argtypes = [_P, _I, _I, _I, _P, _P, _P]
         L.ref_rope_inv_freq.argtypes = [C.c_double, _I, _I, C.c_double, C.c_double, C.c_double, _I, _P]
         L.ref_rope_cos_sin_tables.argtypes = [C.c_double, _I, _I, C.c_double, C.c_double,

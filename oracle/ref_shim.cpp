@@ -11,6 +11,7 @@
 #include "core/common.h"
 #include "core/model_config.h"
 #include "cpu/random_model.h"
+#include "cpu/reference_model.h"
 
 using namespace redline;
 
@@ -101,6 +102,45 @@ void ref_meta_layout(const int* shape7, int max_blocks, size_t* out19) {
                         m.param_row,   m.temperature, m.top_k,        m.top_p,
                         m.seed_lo,     m.seed_hi,     m.total_words};
   std::memcpy(out19, v, sizeof(v));
+}
+
+// The reference's model config JSON (ModelConfig::to_json) for tiny_test_config
+// with the given dimensions, FP16 weights; returns its length, or -1 when it
+// does not fit `cap` bytes or the reference rejects the config.
+int ref_model_config_json(int vocab, int hidden, int inter, int layers, int heads, int kv_heads,
+                          int head_dim, double theta, double eps, char* buf, int cap) {
+  try {
+    ModelConfig c = tiny_test_config(QuantType::kFP16);
+    c.vocab_size = vocab;
+    c.hidden_size = hidden;
+    c.intermediate_size = inter;
+    c.num_layers = layers;
+    c.num_heads = heads;
+    c.num_kv_heads = kv_heads;
+    c.head_dim = head_dim;
+    c.rope_theta = theta;
+    c.rms_norm_eps = eps;
+    c.validate();
+    const std::string s = c.to_json().dump();
+    if (static_cast<int>(s.size()) + 1 > cap) return -1;
+    std::memcpy(buf, s.c_str(), s.size() + 1);
+    return static_cast<int>(s.size());
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// Logits [n, vocab] of the reference's fp32 CPU model (CpuReferenceModel::
+// forward, src/cpu/reference_model.cpp:157-238) on a model file; 0 on success.
+int ref_model_forward(const char* path, const int32_t* tokens, int n, float* logits) {
+  try {
+    CpuReferenceModel m(path);
+    const std::vector<float> out = m.forward(std::vector<int32_t>(tokens, tokens + n));
+    std::memcpy(logits, out.data(), out.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
 }
 
 // The reference's weight quantisers (src/cpu/random_model.cpp:99-140): w is

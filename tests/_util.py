@@ -119,3 +119,52 @@ def interleave_rows(a: np.ndarray) -> np.ndarray:
     out[0::2] = a[:half]
     out[1::2] = a[half:]
     return out
+
+
+# A tiny Llama model for the end-to-end parity test: the reference's
+# tiny_test_config (src/cpu/random_model.cpp:148-166) with smaller dims.
+TINY_MODEL = dict(vocab=512, hidden=128, inter=256, layers=2, heads=2, kv_heads=1, head_dim=64,
+                  theta=1e4, eps=1e-5)
+
+
+def tiny_model_weights(seed: int = 7, cfg: dict = TINY_MODEL) -> dict:
+    """fp16 weights of a random model under the reference's tensor names and
+    layouts (src/cpu/random_model.cpp:62-85): embeddings ~N(0, 1), linear rows
+    ~N(0, gain^2 / k) with gain 4 for lm_head, norm weights U[0.8, 1.2], wqkv
+    rows q heads then k heads then v heads, w_gate_up rows gate then up."""
+    rng = np.random.default_rng(seed)
+    V, H, I, D = cfg["vocab"], cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    hq, hkv = cfg["heads"], cfg["kv_heads"]
+
+    def lin(n, k, gain=1.0):
+        return (rng.standard_normal((n, k)) * (gain / np.sqrt(k))).astype(np.float16)
+
+    def norm_w():
+        return rng.uniform(0.8, 1.2, H).astype(np.float16)
+
+    w = {"tok_embeddings.weight": rng.standard_normal((V, H)).astype(np.float16)}
+    for layer in range(cfg["layers"]):
+        p = f"layers.{layer}."
+        w[p + "attn_norm.weight"] = norm_w()
+        w[p + "wqkv.weight"] = lin((hq + 2 * hkv) * D, H)
+        w[p + "wo.weight"] = lin(H, hq * D)
+        w[p + "ffn_norm.weight"] = norm_w()
+        w[p + "w_gate_up.weight"] = lin(2 * I, H)
+        w[p + "w_down.weight"] = lin(H, I)
+    w["norm.weight"] = norm_w()
+    w["lm_head.weight"] = lin(V, H, 4.0)
+    return w
+
+
+def tiny_model_tokens(n: int = 150) -> np.ndarray:
+    """The token pattern of the reference's engine scoring test
+    (tests/cuda/test_engine.cpp:104-105)."""
+    return np.array([3 + (i * 37) % 500 for i in range(n)], np.int32)
+
+
+def next_token_logprobs(logits: np.ndarray, tokens: np.ndarray) -> np.ndarray:
+    """log p(tokens[i + 1] | prefix) from logits rows 0 .. n-2 (float64)."""
+    x = np.asarray(logits, np.float64)[:-1]
+    mx = x.max(axis=1, keepdims=True)
+    lse = mx[:, 0] + np.log(np.exp(x - mx).sum(axis=1))
+    return x[np.arange(x.shape[0]), tokens[1:]] - lse
