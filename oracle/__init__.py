@@ -99,7 +99,7 @@ def ref() -> C.CDLL:
         L.ref_quantize_int8_rows.argtypes = [_P, _I, _I, _P, _P]
         L.ref_model_config_json.restype = _I
         L.ref_model_config_json.argtypes = [_I, _I, _I, _I, _I, _I, _I, C.c_double, C.c_double,
-                                            C.c_char_p, _I]
+                                            _I, C.c_char_p, _I]
         L.ref_model_forward.restype = _I
         L.ref_model_forward.argtypes = [C.c_char_p, _P, _I, _P]
         L.ref_quantize_int4_groups.argtypes = [_P, _I, _I, _I, _P, _P, _P]

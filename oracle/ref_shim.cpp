@@ -105,12 +105,13 @@ void ref_meta_layout(const int* shape7, int max_blocks, size_t* out19) {
 }
 
 // The reference's model config JSON (ModelConfig::to_json) for tiny_test_config
-// with the given dimensions, FP16 weights; returns its length, or -1 when it
-// does not fit `cap` bytes or the reference rejects the config.
+// with the given dimensions, FP16 weights (int4 = 0) or INT4 layer weights
+// (int4 = 1, group size 64); returns its length, or -1 when it does not fit
+// `cap` bytes or the reference rejects the config.
 int ref_model_config_json(int vocab, int hidden, int inter, int layers, int heads, int kv_heads,
-                          int head_dim, double theta, double eps, char* buf, int cap) {
+                          int head_dim, double theta, double eps, int int4, char* buf, int cap) {
   try {
-    ModelConfig c = tiny_test_config(QuantType::kFP16);
+    ModelConfig c = tiny_test_config(int4 ? QuantType::kINT4 : QuantType::kFP16);
     c.vocab_size = vocab;
     c.hidden_size = hidden;
     c.intermediate_size = inter;

@@ -12,7 +12,24 @@ from __future__ import annotations
 import numpy as np
 
 import redline_amd as ra
-from tests._util import TINY_MODEL
+from tests._util import TINY_INT4_GROUP, TINY_MODEL, int4_dequantize, interleave_rows
+
+PROJ = ("wqkv", "wo", "w_gate_up", "w_down")
+
+
+def dense_weights(w):
+    """float32 projection weights (INT4 ones dequantized as the reference's
+    CPU model does)."""
+    out = {}
+    for name, v in w.items():
+        if name.endswith(".scales") or name.endswith(".offsets"):
+            continue
+        base = name[:-len(".weight")]
+        if base + ".scales" in w:
+            out[name] = int4_dequantize(v, w[base + ".scales"], w[base + ".offsets"], TINY_INT4_GROUP)
+        else:
+            out[name] = v.astype(np.float32)
+    return out
 
 BS = 16
 
@@ -38,12 +55,13 @@ def forward_oracle(w, tokens, cfg=TINY_MODEL):
     import oracle
     T, H, I, D = tokens.size, cfg["hidden"], cfg["inter"], cfg["head_dim"]
     hq, hkv, eps = cfg["heads"], cfg["kv_heads"], cfg["eps"]
+    w32 = dense_weights(w)
     meta, shape, lay, nblk = batch(T)
     g = lambda name, n: meta[lay[name]:lay[name] + n]  # noqa: E731
     pos, slots = g("positions", T), g("slot_mapping", T)
     tables = g("block_tables", nblk - 1).reshape(1, nblk - 1)
     cos, sin = oracle.rope_cos_sin_tables(cfg["theta"], D, T)
-    mm = lambda x, name: _f16(np.asarray(x, np.float32) @ w[name].astype(np.float32).T)  # noqa: E731
+    mm = lambda x, name: _f16(np.asarray(x, np.float32) @ w32[name].T)  # noqa: E731
     res = oracle.embedding_lookup(tokens, w["tok_embeddings.weight"], H)
     _, x = oracle.fused_add_rmsnorm(res, None, w["layers.0.attn_norm.weight"], eps)
     for layer in range(cfg["layers"]):
@@ -64,12 +82,26 @@ def forward_oracle(w, tokens, cfg=TINY_MODEL):
 
 class GpuModel:
     """The weights on the GPU, one paged KV cache per layer, and the forward
-    pass through the HIP kernels (C ABI)."""
+    pass through the HIP kernels (C ABI).  With INT4 projections, steps of at
+    most 32 tokens run them on the INT4 GEMV kernels (gate_up on the fused
+    SwiGLU epilogue over its rows interleaved as the reference's loader does,
+    src/cuda/model/weights.cpp:157-167); longer steps, where the reference
+    engine runs a GEMM, multiply by the dequantized weights."""
 
     def __init__(self, torch, w, total_tokens, cfg=TINY_MODEL):
         from redline_amd import kernels as K
         self.torch, self.K, self.cfg = torch, K, cfg
-        self.w = {k: torch.from_numpy(v).cuda() for k, v in w.items()}
+        self.int4 = any(k.endswith(".scales") for k in w)
+        # fp16 tensors as stored; INT4 projections also dequantized to fp32
+        self.w = {k: torch.from_numpy(v).cuda() for k, v in w.items() if v.dtype == np.float16}
+        self.w32 = {k: torch.from_numpy(v).cuda() for k, v in dense_weights(w).items()
+                    if k not in self.w}
+        self.q = {}
+        if self.int4:
+            for k, v in w.items():
+                self.q[k] = torch.from_numpy(np.ascontiguousarray(v)).cuda()
+                if "w_gate_up" in k:  # (gate_i, up_i) rows for the fused epilogue
+                    self.q[k + ".il"] = torch.from_numpy(np.ascontiguousarray(interleave_rows(v))).cuda()
         D = cfg["head_dim"]
         self.nblk = (total_tokens + BS - 1) // BS + 1
         self.caches = [K.KVCache(1, self.nblk, cfg["kv_heads"], D, BS) for _ in range(cfg["layers"])]
@@ -77,7 +109,32 @@ class GpuModel:
         self.cos, self.sin = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
 
     def mm(self, x, name):
-        return self.torch.matmul(x, self.w[name].t())
+        torch, K = self.torch, self.K
+        base = name[:-len(".weight")]
+        if self.int4 and base + ".scales" in self.q and x.shape[0] <= K.kGemvW4MaxM:
+            n, k = self.q[name].shape[0], x.shape[1]
+            y = torch.empty((x.shape[0], n), dtype=torch.float16, device="cuda")
+            K.gemv_w4a16(x.contiguous(), x.shape[0], self.q[name], self.q[base + ".scales"],
+                         self.q[base + ".offsets"], TINY_INT4_GROUP, None, n, k, y)
+            return y
+        if self.int4 and base + ".scales" in self.q:
+            return torch.matmul(x.float(), self.w32[name].t()).half()
+        return torch.matmul(x, self.w[name].t())
+
+    def gate_up_swiglu(self, x, name):
+        """silu(gate) * up of the gate/up projection: the fused INT4 GEMV
+        epilogue where it applies, else the projection then silu_and_mul."""
+        torch, K, I = self.torch, self.K, self.cfg["inter"]
+        n = x.shape[0]
+        act = torch.empty((n, I), dtype=torch.float16, device="cuda")
+        base = name[:-len(".weight")]
+        if self.int4 and n <= K.kGemvW4MaxM:
+            K.gemv_w4a16_swiglu(x.contiguous(), n, self.q[name + ".il"],
+                                self.q[base + ".scales.il"], self.q[base + ".offsets.il"],
+                                TINY_INT4_GROUP, 2 * I, x.shape[1], act)
+        else:
+            K.silu_and_mul(self.mm(x, name).contiguous(), n, I, act)
+        return act
 
     def step(self, tokens, start, total):
         """New tokens at positions start..: returns fp32 logits [n, V] (the
@@ -115,8 +172,7 @@ class GpuModel:
                     shape.num_prefill_seqs, shape.max_prefill_q_tiles))
             K.fused_add_rmsnorm(res, self.mm(att, p + "wo.weight").contiguous(),
                                 self.w[p + "ffn_norm.weight"], n, H, eps, x)
-            act = torch.empty((n, I), dtype=torch.float16, device="cuda")
-            K.silu_and_mul(self.mm(x, p + "w_gate_up.weight").contiguous(), n, I, act)
+            act = self.gate_up_swiglu(x, p + "w_gate_up.weight")
             nxt = f"layers.{layer + 1}.attn_norm.weight" if layer + 1 < cfg["layers"] else "norm.weight"
             K.fused_add_rmsnorm(res, self.mm(act, p + "w_down.weight").contiguous(), self.w[nxt],
                                 n, H, eps, x)

@@ -127,33 +127,58 @@ TINY_MODEL = dict(vocab=512, hidden=128, inter=256, layers=2, heads=2, kv_heads=
                   theta=1e4, eps=1e-5)
 
 
-def tiny_model_weights(seed: int = 7, cfg: dict = TINY_MODEL) -> dict:
-    """fp16 weights of a random model under the reference's tensor names and
+TINY_INT4_GROUP = 64  # the reference's tiny_test_config group size
+
+
+def tiny_model_weights(seed: int = 7, cfg: dict = TINY_MODEL, int4: bool = False) -> dict:
+    """Weights of a random model under the reference's tensor names and
     layouts (src/cpu/random_model.cpp:62-85): embeddings ~N(0, 1), linear rows
     ~N(0, gain^2 / k) with gain 4 for lm_head, norm weights U[0.8, 1.2], wqkv
-    rows q heads then k heads then v heads, w_gate_up rows gate then up."""
+    rows q heads then k heads then v heads, w_gate_up rows gate then up; all
+    fp16, or with int4 the four layer projections as the reference's INT4
+    format (prefix.weight packed codes, .scales, .offsets: its
+    quantize_int4_groups, restated by int4_quantize_groups, group 64)."""
     rng = np.random.default_rng(seed)
     V, H, I, D = cfg["vocab"], cfg["hidden"], cfg["inter"], cfg["head_dim"]
     hq, hkv = cfg["heads"], cfg["kv_heads"]
 
-    def lin(n, k, gain=1.0):
-        return (rng.standard_normal((n, k)) * (gain / np.sqrt(k))).astype(np.float16)
+    def lin32(n, k, gain=1.0):
+        return (rng.standard_normal((n, k)) * (gain / np.sqrt(k))).astype(np.float32)
 
     def norm_w():
         return rng.uniform(0.8, 1.2, H).astype(np.float16)
+
+    def add_linear(name, n, k):
+        v = lin32(n, k)
+        if int4:
+            packed, s, o = int4_quantize_groups(v, TINY_INT4_GROUP)
+            w[name + ".weight"], w[name + ".scales"], w[name + ".offsets"] = packed, s, o
+        else:
+            w[name + ".weight"] = v.astype(np.float16)
 
     w = {"tok_embeddings.weight": rng.standard_normal((V, H)).astype(np.float16)}
     for layer in range(cfg["layers"]):
         p = f"layers.{layer}."
         w[p + "attn_norm.weight"] = norm_w()
-        w[p + "wqkv.weight"] = lin((hq + 2 * hkv) * D, H)
-        w[p + "wo.weight"] = lin(H, hq * D)
+        add_linear(p + "wqkv", (hq + 2 * hkv) * D, H)
+        add_linear(p + "wo", H, hq * D)
         w[p + "ffn_norm.weight"] = norm_w()
-        w[p + "w_gate_up.weight"] = lin(2 * I, H)
-        w[p + "w_down.weight"] = lin(H, I)
+        add_linear(p + "w_gate_up", 2 * I, H)
+        add_linear(p + "w_down", H, I)
     w["norm.weight"] = norm_w()
-    w["lm_head.weight"] = lin(V, H, 4.0)
+    w["lm_head.weight"] = lin32(V, H, 4.0).astype(np.float16)
     return w
+
+
+def int4_dequantize(packed: np.ndarray, s: np.ndarray, o: np.ndarray, group_size: int) -> np.ndarray:
+    """float32 W = q * scale + offset per group (the reference's
+    dequantize_linear for INT4, src/cpu/reference_model.cpp:70-85)."""
+    q = np.empty((packed.shape[0], packed.shape[1] * 2), np.float32)
+    q[:, 0::2] = packed & 15
+    q[:, 1::2] = packed >> 4
+    sg = np.repeat(s.astype(np.float32), group_size, axis=1)
+    og = np.repeat(o.astype(np.float32), group_size, axis=1)
+    return q * sg + og
 
 
 def tiny_model_tokens(n: int = 150) -> np.ndarray:

@@ -74,3 +74,39 @@ def test_gpu_model_decode_step_matches_reference(golden):
     err = np.abs(ls(last) - ls(want))
     say(f"decode step: log-softmax error over the vocabulary max {err.max():.4f}")
     assert err.max() < 0.3 and int(last.argmax()) == int(z["argmax"][-1])
+
+
+def test_oracle_int4_model_matches_reference(golden):
+    """The same with the four layer projections in the reference's INT4
+    format (the oracle composition multiplies by the dequantized weights)."""
+    z = golden("tiny_model_int4_logits.npz")
+    tokens = z["tokens"]
+    logits = forward_oracle(tiny_model_weights(int(z["seed"]), int4=True), tokens)
+    _check(next_token_logprobs(logits, tokens), z["logprobs"], "oracle composition, INT4 weights")
+
+
+@pytest.mark.gpu
+def test_gpu_int4_model_decode_steps_match_reference(golden):
+    """INT4 weights: prefill of the first 146 tokens (dequantized weights, as
+    the reference engine's prefill GEMM), then the last 4 tokens as decode
+    steps whose projections run on the INT4 GEMV kernels, gate_up on the fused
+    SwiGLU epilogue: each step's next-token log-probability, and the last
+    step's whole row, against the reference's INT4 model."""
+    import torch
+    z = golden("tiny_model_int4_logits.npz")
+    tokens = z["tokens"]
+    n = tokens.size
+    say("tiny INT4 model e2e: prefill 146 + 4 decode steps")
+    m = GpuModel(torch, tiny_model_weights(int(z["seed"]), int4=True), n)
+    pre = m.step(tokens[:n - 4], 0, n)
+    _check(next_token_logprobs(pre, tokens[:n - 4]), z["logprobs"][:n - 5], "INT4 prefill")
+    rows = [pre[-1]]
+    for t in range(n - 4, n):
+        rows.append(m.step(tokens[t:t + 1], t, n)[0])
+    logits = np.stack(rows)  # predictions after tokens n-5 .. n-1
+    lp = next_token_logprobs(logits, tokens[n - 5:])  # rows after tokens n-5 .. n-2
+    _check(lp, z["logprobs"][n - 5:], "INT4 decode steps (GEMV kernels)")
+    ls = lambda v: v - v.max() - np.log(np.exp(v - v.max()).sum())  # noqa: E731
+    err = np.abs(ls(logits[-1].astype(np.float64)) - ls(z["last_logits"].astype(np.float64)))
+    say(f"INT4 last decode row: log-softmax error max {err.max():.4f}")
+    assert err.max() < 0.3
