@@ -49,14 +49,21 @@ struct AttnArgs {
 
 
 
+// the MFMA operand that takes the 1152 of the biased INT8 codes out of a sum
+__device__ __forceinline__ f16x8 minus1152x8() {
+  const _Float16 v = static_cast<_Float16>(-1152);
+  return f16x8{v, v, v, v, v, v, v, v};
+}
+
 template <bool kInt8>
 struct Row;
 
 template <>
 struct Row<false> {  // 8 fp16 elements, 16 bytes
   using Raw = u32x4;
-  __device__ static Raw load(const void* base, int64_t cell, int D, int e0) {
-    return ld16<true>(reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + cell * D + e0));
+  __device__ static Raw load(const void* base, uint32_t cell, int D, int e0) {
+    return ld16<true>(reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + e0 +
+                                                     static_cast<uint64_t>(cell) * D));
   }
   __device__ static f16x8 halves(Raw r) { return __builtin_bit_cast(f16x8, r); }
   __device__ static f32x8 floats(Raw r) { return unpack8(r); }
@@ -65,9 +72,9 @@ struct Row<false> {  // 8 fp16 elements, 16 bytes
 template <>
 struct Row<true> {  // 8 int8 codes, 8 bytes
   using Raw = u32x2;
-  __device__ static Raw load(const void* base, int64_t cell, int D, int e0) {
-    return __builtin_nontemporal_load(
-        reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(base) + cell * D + e0));
+  __device__ static Raw load(const void* base, uint32_t cell, int D, int e0) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(
+        static_cast<const int8_t*>(base) + e0 + static_cast<uint64_t>(cell) * D));
   }
   __device__ static f16x8 halves(Raw r) { return int8x8_to_f16(r); }
   __device__ static f32x8 floats(Raw r) {
@@ -133,13 +140,15 @@ struct RowBatch {
 // Requests every row of this thread's keys of a unit whose first `n` keys
 // are in context (cells: the unit's cache cells, in LDS).  Slots past the
 // context re-read the last valid row (a cache hit) and are masked out later,
-// which keeps every load unconditional.
-template <int D, bool kInt8>
+// which keeps every load unconditional: kClamp clamps the key to n - 1 here;
+// without it the cells past the context already hold key n - 1's cell
+// (write_cells with the unit's key count).
+template <int D, bool kInt8, bool kClamp>
 __device__ __forceinline__ void issue_rows(RowBatch<D, kInt8>& rb, const void* base,
                                            const int* cells, int n, const LaneCoord& c) {
 #pragma unroll
   for (int u = 0; u < Geo<D>::kPasses; ++u)
-    rb.r[u] = Row<kInt8>::load(base, cells[min(key_of<D>(c, u), n - 1)], D, c.e0);
+    rb.r[u] = Row<kInt8>::load(base, cells[kClamp ? min(key_of<D>(c, u), n - 1) : key_of<D>(c, u)], D, c.e0);
   // keeps the scheduler from moving the batch next to its first use
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -183,15 +192,16 @@ __device__ __forceinline__ int step_dim(int step, int j) {
   return kInt8 ? 64 * (step / 2) + 16 * j + 8 * (step % 2) : 32 * step + 8 * j;
 }
 
-template <int D, bool kInt8>
+template <int D, bool kInt8, bool kClamp>
 __device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* base,
                                            const int* cells, int n, const LaneCoord& c) {
   const int lane = c.tid % kWave, r = lane % 16, j = lane / 16;
   constexpr int kRowBytes = D * (kInt8 ? 1 : 2);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int64_t cell = cells[min(mma_key<D>(c, t, r), n - 1)];
-    const char* row = static_cast<const char*>(base) + cell * kRowBytes + 16 * j;
+    const int key = mma_key<D>(c, t, r);
+    const uint32_t cell = cells[kClamp ? min(key, n - 1) : key];  // cells are >= 0
+    const char* row = static_cast<const char*>(base) + 16 * j + static_cast<uint64_t>(cell) * kRowBytes;
 #pragma unroll
     for (int x = 0; x < KBatch<D, kInt8>::kLoads; ++x)
       kb.r[t][x] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 64 * x));
@@ -246,17 +256,26 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
     qb[st] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     if (g < G) qb[st] = *reinterpret_cast<const f16x8*>(qs + g * D + step_dim<D, kInt8>(st, rho));
   }
+  // INT8: A holds 1152 + code (int8x8_to_f16_biased), so every score starts
+  // from -1152 * sum_d q[g][d], one MFMA per step with A = -1152 everywhere
+  // (the same for every key row), instead of a subtract per pair of codes
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kInt8) {
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st)
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(minus1152x8(), qb[st], acc0, 0, 0, 0);
+  }
   f32x4 acc[2];
   float ks[8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[t] = acc0;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       f16x8 a;
       if constexpr (kInt8) {
         const u32x4 w = kb.r[t][st / 2];
-        a = int8x8_to_f16(st % 2 ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
+        a = int8x8_to_f16_biased(st % 2 ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
       } else {
         a = __builtin_bit_cast(f16x8, kb.r[t][st]);
       }
@@ -405,10 +424,11 @@ __device__ __forceinline__ void wave_pv(const RowBatch<D, kInt8>& vb, const floa
 
 // INT8 codes of 8 keys (the 8 k-slots of an MFMA operand) at 4 dims to
 // fp16: w[kk] holds key kk's codes of the 4 dims, sign bits already flipped
-// (code + 128 in each byte); a[j][kk] = code of dim j of key kk, exactly.
-// Bytes of keys (2p, 2p + 1) are interleaved by two permutes, then each pair
-// gets the 0x64 high bytes (fp16 1024 + byte) and one packed subtract of 1152.
-__device__ __forceinline__ void int8_cols_to_f16(const uint32_t (&w)[8], f16x8 (&a)[4]) {
+// (code + 128 in each byte); a[j][kk] = 1152 + code of dim j of key kk,
+// exactly.  Bytes of keys (2p, 2p + 1) are interleaved by two permutes, then
+// each pair gets the 0x64 high bytes (fp16 1024 + byte); the constant 1152
+// is removed from the P . V sums (wave_pv_mma), not per code.
+__device__ __forceinline__ void int8_cols_to_f16_biased(const uint32_t (&w)[8], f16x8 (&a)[4]) {
 #pragma unroll
   for (int pr = 0; pr < 4; ++pr) {
     // selectors 0-3 pick from the second source, 4-7 from the first
@@ -420,7 +440,7 @@ __device__ __forceinline__ void int8_cols_to_f16(const uint32_t (&w)[8], f16x8 (
                            __builtin_amdgcn_perm(0x64646464u, t23, 0x04030402u)};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const f16x2 v = __builtin_bit_cast(f16x2, h[j]) - static_cast<_Float16>(1152);
+      const f16x2 v = __builtin_bit_cast(f16x2, h[j]);
       a[j][2 * pr] = v[0];
       a[j][2 * pr + 1] = v[1];
     }
@@ -465,7 +485,7 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) w[kk] = vb.r[kk][half] ^ 0x80808080u;
         f16x8 q[4];
-        int8_cols_to_f16(w, q);
+        int8_cols_to_f16_biased(w, q);
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[4 * half + j] = q[j];
       }
@@ -502,13 +522,17 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
         w[u] = (t1 ? other : own) ^ 0x80808080u;
         w[4 + u] = (t1 ? own : other) ^ 0x80808080u;
       }
-      int8_cols_to_f16(w, a);
+      int8_cols_to_f16_biased(w, a);
     }
   }
   then();
+  // INT8: A holds 1152 + code, so every tile starts from -1152 * sum_k b[k][g]
+  // (one MFMA with A = -1152 everywhere, the same for every dim row)
+  f32x4 o0 = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kInt8) o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(minus1152x8(), po.b, o0, 0, 0, 0);
 #pragma unroll
   for (int dt = 0; dt < kTiles; ++dt) {
-    const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], po.b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], po.b, o0, 0, 0, 0);
     if (m < G) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -570,18 +594,20 @@ struct UnitLds {
 };
 
 // Cache cells of a partition's keys, from this thread's block-table entry
-// `blk` for key `tid` (threads tid < 256; blk < 0 past the table).
-// (threads tid >= 256 or past the table: nothing); the key's INT8 scales
-// are requested into ks / vs (0 when there is no cell).
+// `blk` for key min(tid, nkeys - 1) (threads tid < 256; blk < 0 past the
+// table: nothing written); the key's INT8 scales are requested into ks / vs
+// (0 when there is no cell).  With nkeys = the partition's keys in context,
+// the keys past the context get the last key's cell and scales.
 template <bool kInt8>
 __device__ __forceinline__ void write_cells(int* cells, const AttnArgs& args, int tid, int blk,
-                                            int part, int kvh, float& ks, float& vs) {
+                                            int part, int kvh, float& ks, float& vs,
+                                            int nkeys = kPart) {
   const rlk_attention_params& p = args.p;
   ks = 0.f;
   vs = 0.f;
   if (tid < kPart && blk >= 0) {
     const int bs = p.kv.block_size;
-    const int pos = part * kPart + tid;
+    const int pos = part * kPart + min(tid, nkeys - 1);
     const int cell = (blk * p.kv.num_kv_heads + kvh) * bs + (pos - (pos / bs) * bs);
     cells[tid] = cell;
     if constexpr (kInt8) {
@@ -609,11 +635,12 @@ __device__ __forceinline__ u32x4 load_q_piece(const rlk_attention_params& p, int
   return load16(q);
 }
 
-// Block-table entry of key `tid` of a partition (threads tid < 256), or -1
-// past the table.  Table rows are padded with block 0, so every entry inside
+// Block-table entry of key min(tid, nkeys - 1) of a partition (threads
+// tid < 256), or -1 past the table.  Table rows are padded with block 0, so every entry inside
 // the row is a valid block.
-__device__ __forceinline__ int table_entry(const rlk_attention_params& p, int tid, int seq, int part) {
-  const int bi = (part * kPart + tid) / p.kv.block_size;
+__device__ __forceinline__ int table_entry(const rlk_attention_params& p, int tid, int seq, int part,
+                                           int nkeys = kPart) {
+  const int bi = (part * kPart + min(tid, nkeys - 1)) / p.kv.block_size;
   if (tid >= kPart || bi >= p.max_blocks_per_seq) return -1;
   return p.block_tables[static_cast<int64_t>(seq) * p.max_blocks_per_seq + bi];
 }
@@ -714,16 +741,16 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   float sk_next = 0.f, sv_next = 0.f;
   {
     float ks0, vs0;
-    write_cells<kInt8>(s.cell[0], args, tid, table_entry(p, tid, it_seq[cur.item], cur.part), cur.part,
-                       cur.kvh, ks0, vs0);
+    write_cells<kInt8>(s.cell[0], args, tid, table_entry(p, tid, it_seq[cur.item], cur.part, keys_in(cur)),
+                       cur.part, cur.kvh, ks0, vs0, keys_in(cur));
     if (kInt8 && tid < kPart) {
       s.ksc[0][tid] = ks0;
       s.vsc[0][tid] = vs0;
     }
   }
   if (u0 + 1 < u1)
-    write_cells<kInt8>(s.cell[1], args, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part), nxt.part,
-                       nxt.kvh, sk_next, sv_next);
+    write_cells<kInt8>(s.cell[1], args, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part, keys_in(nxt)),
+                       nxt.part, nxt.kvh, sk_next, sv_next, keys_in(nxt));
   if (q_piece<D, G>(tid))
     store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, it_tok[cur.item], cur.kvh));
   __syncthreads();
@@ -732,8 +759,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   RowBatch<D, kInt8> vb;
   {
     const LaneCoord c = lane_coord<D>();
-    issue_keys<D, kInt8>(kb, p.kv.k, s.cell[0], keys_in(cur), c);
-    issue_rows<D, kInt8>(vb, p.kv.v, s.cell[0], keys_in(cur), c);
+    issue_keys<D, kInt8, false>(kb, p.kv.k, s.cell[0], keys_in(cur), c);
+    issue_rows<D, kInt8, false>(vb, p.kv.v, s.cell[0], keys_in(cur), c);
   }
   for (int u = u0; u < u1; ++u) {
     const int b = (u - u0) & 1;
@@ -742,19 +769,19 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     const LaneCoord c = lane_coord<D>();
     // block-table entries of unit n+2 and the q piece of unit n+1, consumed
     // after the first barrier
-    const int blk2 = has2 ? table_entry(p, c.tid, it_seq[nn.item], nn.part) : -1;
+    const int blk2 = has2 ? table_entry(p, c.tid, it_seq[nn.item], nn.part, keys_in(nn)) : -1;
     u32x4 qn = {0, 0, 0, 0};
     if (has1 && q_piece<D, G>(c.tid)) qn = load_q_piece<D, G>(p, c.tid, it_tok[nxt.item], nxt.kvh);
 
     PvOperand<D, G, kMma> po;
     wave_softmax<D, G, kInt8, kMma>(kb, s.q[b], s.ksc[b], s.vsc[b], p.scale, keys_in(cur), c, po,
                                     s.stat, [&] {
-      if (has1) issue_keys<D, kInt8>(kb, p.kv.k, s.cell[b ^ 1], keys_in(nxt), c);
+      if (has1) issue_keys<D, kInt8, false>(kb, p.kv.k, s.cell[b ^ 1], keys_in(nxt), c);
     });
     // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
     if (has1 && q_piece<D, G>(c.tid)) store16(s.q[b ^ 1] + (c.tid - kPart) * 8, qn);
     auto next_rows = [&] {
-      if (has1) issue_rows<D, kInt8>(vb, p.kv.v, s.cell[b ^ 1], keys_in(nxt), c);
+      if (has1) issue_rows<D, kInt8, false>(vb, p.kv.v, s.cell[b ^ 1], keys_in(nxt), c);
     };
     if constexpr (kMma) {
       wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, next_rows);
@@ -770,7 +797,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
       s.ksc[b ^ 1][c.tid] = sk_next;
       s.vsc[b ^ 1][c.tid] = sv_next;
     }
-    if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next);
+    if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next, keys_in(nn));
     combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
                         cur.part, cur.kvh);
     __syncthreads();
@@ -805,8 +832,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   const LaneCoord c = lane_coord<D>();
   KBatch<D, kInt8> kb;
   RowBatch<D, kInt8> vb;
-  issue_keys<D, kInt8>(kb, p.kv.k, s.cell[0], n, c);
-  issue_rows<D, kInt8>(vb, p.kv.v, s.cell[0], n, c);
+  issue_keys<D, kInt8, true>(kb, p.kv.k, s.cell[0], n, c);
+  issue_rows<D, kInt8, true>(vb, p.kv.v, s.cell[0], n, c);
   PvOperand<D, G, kMma> po;
   wave_softmax<D, G, kInt8, kMma>(kb, s.q[0], s.ksc[0], s.vsc[0], p.scale, n, c, po, s.stat, [] {});
   if constexpr (kMma) {

@@ -128,8 +128,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // becomes the low byte of an fp16 whose high byte is 0x64, i.e. the value
 // 1024 + code + 128 (fp16 spacing is 1 on [1024, 2048)); one packed fp16
 // subtract of 1152 leaves the code.  2 XORs + 4 byte permutes + 4 packed
-// subtracts for 8 codes.
-__device__ __forceinline__ f16x8 int8x8_to_f16(u32x2 r) {
+// subtracts for 8 codes.  The _biased form stops before the subtract
+// (1152 + code, exactly), for callers that remove the constant once from a
+// sum instead of once per code.
+__device__ __forceinline__ f16x8 int8x8_to_f16_biased(u32x2 r) {
   const uint32_t lo = r.x ^ 0x80808080u, hi = r.y ^ 0x80808080u;
   // v_perm_b32 selectors: bytes 0-3 of the second source, 4 = byte 0 of the
   // first (0x64)
@@ -137,7 +139,10 @@ __device__ __forceinline__ f16x8 int8x8_to_f16(u32x2 r) {
                    __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
                    __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
                    __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
-  return __builtin_bit_cast(f16x8, w) - static_cast<_Float16>(1152);
+  return __builtin_bit_cast(f16x8, w);
+}
+__device__ __forceinline__ f16x8 int8x8_to_f16(u32x2 r) {
+  return int8x8_to_f16_biased(r) - static_cast<_Float16>(1152);
 }
 
 // The codes of two rows, paired by element: out[x] = {a[x], b[x]} as exact
