@@ -146,6 +146,8 @@ struct RowBatch {
 template <int D, bool kInt8, bool kClamp>
 __device__ __forceinline__ void issue_rows(RowBatch<D, kInt8>& rb, const void* base,
                                            const int* cells, int n, const LaneCoord& c) {
+  // keeps the last reads of the registers being refilled before the loads
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < Geo<D>::kPasses; ++u)
     rb.r[u] = Row<kInt8>::load(base, cells[kClamp ? min(key_of<D>(c, u), n - 1) : key_of<D>(c, u)], D, c.e0);
@@ -195,6 +197,7 @@ __device__ __forceinline__ int step_dim(int step, int j) {
 template <int D, bool kInt8, bool kClamp>
 __device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* base,
                                            const int* cells, int n, const LaneCoord& c) {
+  __builtin_amdgcn_sched_barrier(0);  // as in issue_rows
   const int lane = c.tid % kWave, r = lane % 16, j = lane / 16;
   constexpr int kRowBytes = D * (kInt8 ? 1 : 2);
 #pragma unroll
@@ -525,6 +528,12 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
       int8_cols_to_f16_biased(w, a);
     }
   }
+  // The operands are complete here: the V registers are free for the next
+  // unit's rows (then()).  Without this point the compiler sinks part of the
+  // operand build below the refill, keeps both batches live and copies one
+  // of them at the loop edge, which waits for every load in flight.
+#pragma unroll
+  for (int dt = 0; dt < kTiles; ++dt) asm volatile("" : "+v"(a[dt])::"memory");
   then();
   // INT8: A holds 1152 + code, so every tile starts from -1152 * sum_k b[k][g]
   // (one MFMA with A = -1152 everywhere, the same for every dim row)
@@ -596,15 +605,17 @@ struct UnitLds {
 // Cache cells of a partition's keys, from this thread's block-table entry
 // `blk` for key min(tid, nkeys - 1) (threads tid < 256; blk < 0 past the
 // table: nothing written); the key's INT8 scales are requested into ks / vs
-// (0 when there is no cell).  With nkeys = the partition's keys in context,
-// the keys past the context get the last key's cell and scales.
+// as raw bits (0 when there is no cell; scale_value converts them where they
+// are written to LDS, so no wait follows the request).  With nkeys = the
+// partition's keys in context, the keys past the context get the last key's
+// cell and scales.
 template <bool kInt8>
 __device__ __forceinline__ void write_cells(int* cells, const AttnArgs& args, int tid, int blk,
-                                            int part, int kvh, float& ks, float& vs,
+                                            int part, int kvh, uint32_t& ks, uint32_t& vs,
                                             int nkeys = kPart) {
   const rlk_attention_params& p = args.p;
-  ks = 0.f;
-  vs = 0.f;
+  ks = 0;
+  vs = 0;
   if (tid < kPart && blk >= 0) {
     const int bs = p.kv.block_size;
     const int pos = part * kPart + min(tid, nkeys - 1);
@@ -612,14 +623,20 @@ __device__ __forceinline__ void write_cells(int* cells, const AttnArgs& args, in
     cells[tid] = cell;
     if constexpr (kInt8) {
       if (args.scale16) {  // uniform
-        ks = static_cast<float>(reinterpret_cast<const _Float16*>(p.kv.k_scale)[cell]);
-        vs = static_cast<float>(reinterpret_cast<const _Float16*>(p.kv.v_scale)[cell]);
+        ks = reinterpret_cast<const uint16_t*>(p.kv.k_scale)[cell];
+        vs = reinterpret_cast<const uint16_t*>(p.kv.v_scale)[cell];
       } else {
-        ks = p.kv.k_scale[cell];
-        vs = p.kv.v_scale[cell];
+        ks = reinterpret_cast<const uint32_t*>(p.kv.k_scale)[cell];
+        vs = reinterpret_cast<const uint32_t*>(p.kv.v_scale)[cell];
       }
     }
   }
+}
+
+// An INT8 scale from its raw bits (fp16 in the low half with scale16).
+__device__ __forceinline__ float scale_value(uint32_t raw, int scale16) {
+  return scale16 ? static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(raw)))
+                 : __builtin_bit_cast(float, raw);
 }
 
 // q of the G heads of a kv head: G * D fp16 contiguous in the token's row,
@@ -674,7 +691,14 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   __shared__ int it_tok[kMaxItemsLds], it_seq[kMaxItemsLds], it_ctx[kMaxItemsLds];
   __shared__ int it_pfx[kMaxItemsLds + 1];  // partitions before item i
   __shared__ int wave_tot[kWaves];
+  // Cells of the requests issued past a workgroup's last unit: all cell 0
+  // (block 0 exists in every pool), so every lane re-reads one cached row.
+  // Issuing them keeps the next unit's loads unconditional; a load issued
+  // only on some path makes the compiler copy the batch registers at the
+  // loop edge, and a copy waits for every load in flight.
+  __shared__ int zero_cells[kPart];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  if (tid < kPart) zero_cells[tid] = 0;
   const int items = w.num_items, hkv = p.kv.num_kv_heads;
 
   // Items are split into kThreads contiguous runs; each thread sums its run,
@@ -738,14 +762,14 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   UnitPos nxt = u0 + 1 < u1 ? advance(cur) : cur;
   // INT8 scales of key tid of unit n+1, requested in unit n-1 and written to
   // LDS in unit n (the cells of unit n+2 are written there too)
-  float sk_next = 0.f, sv_next = 0.f;
+  uint32_t sk_next = 0, sv_next = 0;
   {
-    float ks0, vs0;
+    uint32_t ks0, vs0;
     write_cells<kInt8>(s.cell[0], args, tid, table_entry(p, tid, it_seq[cur.item], cur.part, keys_in(cur)),
                        cur.part, cur.kvh, ks0, vs0, keys_in(cur));
     if (kInt8 && tid < kPart) {
-      s.ksc[0][tid] = ks0;
-      s.vsc[0][tid] = vs0;
+      s.ksc[0][tid] = scale_value(ks0, args.scale16);
+      s.vsc[0][tid] = scale_value(vs0, args.scale16);
     }
   }
   if (u0 + 1 < u1)
@@ -776,12 +800,12 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     PvOperand<D, G, kMma> po;
     wave_softmax<D, G, kInt8, kMma>(kb, s.q[b], s.ksc[b], s.vsc[b], p.scale, keys_in(cur), c, po,
                                     s.stat, [&] {
-      if (has1) issue_keys<D, kInt8, false>(kb, p.kv.k, s.cell[b ^ 1], keys_in(nxt), c);
+      issue_keys<D, kInt8, false>(kb, p.kv.k, has1 ? s.cell[b ^ 1] : zero_cells, 0, c);
     });
     // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
     if (has1 && q_piece<D, G>(c.tid)) store16(s.q[b ^ 1] + (c.tid - kPart) * 8, qn);
     auto next_rows = [&] {
-      if (has1) issue_rows<D, kInt8, false>(vb, p.kv.v, s.cell[b ^ 1], keys_in(nxt), c);
+      issue_rows<D, kInt8, false>(vb, p.kv.v, has1 ? s.cell[b ^ 1] : zero_cells, 0, c);
     };
     if constexpr (kMma) {
       wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, next_rows);
@@ -794,8 +818,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     // cells(n+2) to the buffer cells(n) used, free once every wave has
     // requested V(n), i.e. after this barrier
     if (kInt8 && has1 && c.tid < kPart) {
-      s.ksc[b ^ 1][c.tid] = sk_next;
-      s.vsc[b ^ 1][c.tid] = sv_next;
+      s.ksc[b ^ 1][c.tid] = scale_value(sk_next, args.scale16);
+      s.vsc[b ^ 1][c.tid] = scale_value(sv_next, args.scale16);
     }
     if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next, keys_in(nn));
     combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
@@ -820,11 +844,11 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   if (part >= (ctx + kPart - 1) / kPart) return;  // uniform over the workgroup (part < max_partitions)
   const int n = min(kPart, ctx - part * kPart);
   {
-    float ks0, vs0;
+    uint32_t ks0, vs0;
     write_cells<kInt8>(s.cell[0], args, tid, blk, part, kvh, ks0, vs0);
     if (kInt8 && tid < kPart) {
-      s.ksc[0][tid] = ks0;
-      s.vsc[0][tid] = vs0;
+      s.ksc[0][tid] = scale_value(ks0, args.scale16);
+      s.vsc[0][tid] = scale_value(vs0, args.scale16);
     }
   }
   if (q_piece<D, G>(tid)) store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, token, kvh));
