@@ -227,10 +227,16 @@ def capture(torch, fn):
     return g
 
 
-def time_graph(torch, graph, reps):
-    """Average ms per replay, HIP events on the replay stream."""
-    graph.replay()
-    torch.cuda.synchronize()
+def time_graph(torch, graph, reps, warm_ms=20.0):
+    """Average ms per replay, HIP events on the replay stream, after at least
+    `warm_ms` of untimed replays (a single warm-up replay left the first of
+    several back-to-back timings of one kernel up to 10% slow)."""
+    t0 = time.perf_counter()
+    while True:
+        graph.replay()
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= warm_ms:
+            break
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):

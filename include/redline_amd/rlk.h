@@ -123,7 +123,8 @@ int rlk_silu_and_mul_interleaved(const uint16_t* gate_up, int rows, int inter, u
  * random_model.cpp:99-115); fp32 accumulation.  y fp16 [m, n], or fp32 when
  * y_fp32 != 0; bias fp16 [n] or NULL.  m <= 0: no-op.  m > RLK_GEMV_W8_MAX_M:
  * RLK_EUNSUPPORTED (the reference serves m <= 16).  k % 16 != 0: RLK_EINVAL;
- * x and w 16-byte aligned.
+ * x and w 16-byte aligned.  A weight over 2 GiB (n * k bytes): RLK_EUNSUPPORTED
+ * (split n over calls).
  * Replaces kernels::gemv_w8a16, gemv_weight_only.cu:217-226 (kernels.h:162-163). */
 #define RLK_GEMV_W8_MAX_M 32
 int rlk_gemv_w8a16(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales,

@@ -180,6 +180,13 @@ __device__ __forceinline__ void store_tile(const W4Args& a, f32x4 v, int m0, int
 // SIMD): a wave may use up to 256 VGPRs, which pays for a deep ring of loads
 // in flight.
 constexpr int kMaxWaves = 8;
+// Word 3 of a buffer resource for raw byte-addressed loads (32-bit data
+// format, no swizzle), and the cache-policy operand of the buffer-load
+// builtins that marks a load non-temporal.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kNtLoad = 2;
+// Largest weight the pair kernel addresses through 32-bit buffer offsets.
+constexpr uint64_t kMaxBufferBytes = 0x7FFFFFFFu;
 
 template <int S, int P, int KC, int MT, int MODE, int PR = 1>
 __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
@@ -454,18 +461,28 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   const int row = row0 + r16;                       // this lane's output row
   const int kb = kW8 ? a.k : a.k / 2;  // bytes per weight row
   const int pc0 = (low ? qd : 4 + qd) * 16, pc1 = (low ? 4 + qd : qd) * 16;
-  const uint8_t* wp0 = a.w + static_cast<size_t>(min(row0 + (low ? r16 : r16 - 8), a.n - 1)) * kb;
-  const uint8_t* wp1 = a.w + static_cast<size_t>(min(row0 + (low ? r16 + 8 : r16), a.n - 1)) * kb;
+  // The codes are read through buffer loads: the lane's row offset in a
+  // VGPR, the pair's offset (uniform) in the scalar offset, so a refill costs
+  // no VALU.  The weight is < 4 GiB (launch_pairs).  A load through `none`
+  // (no records) returns zeros without a memory access.
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.w), 0, static_cast<int>(static_cast<uint32_t>(a.n) * static_cast<uint32_t>(kb)),
+      kBufferFlags);
+  const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, 0, kBufferFlags);
+  const uint32_t rb0 = static_cast<uint32_t>(min(row0 + (low ? r16 : r16 - 8), a.n - 1)) * kb;
+  const uint32_t rb1 = static_cast<uint32_t>(min(row0 + (low ? r16 + 8 : r16), a.n - 1)) * kb;
   u32x4 ring[P][2];
-  auto fetch = [&](int s, int q) {
-    int o0 = q * 128 + pc0, o1 = q * 128 + pc1;
-    if constexpr (kW8) {  // pieces past the row end (x is zero there)
-      o0 = min(o0, kb - 16);
-      o1 = min(o1, kb - 16);
+  auto fetch_from = [&](int s, int q, __amdgpu_buffer_rsrc_t res) {
+    if constexpr (kW8) {  // pieces past the row end are clamped to its last 16 bytes (x is zero there)
+      const int o0 = min(q * 128 + pc0, kb - 16), o1 = min(q * 128 + pc1, kb - 16);
+      ring[s][0] = __builtin_amdgcn_raw_buffer_load_b128(res, static_cast<int>(rb0) + o0, 0, kNtLoad);
+      ring[s][1] = __builtin_amdgcn_raw_buffer_load_b128(res, static_cast<int>(rb1) + o1, 0, kNtLoad);
+    } else {
+      ring[s][0] = __builtin_amdgcn_raw_buffer_load_b128(res, static_cast<int>(rb0) + pc0, q * 128, kNtLoad);
+      ring[s][1] = __builtin_amdgcn_raw_buffer_load_b128(res, static_cast<int>(rb1) + pc1, q * 128, kNtLoad);
     }
-    ring[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp0 + o0));
-    ring[s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp1 + o1));
   };
+  auto fetch = [&](int s, int q) { fetch_from(s, q, wres); };
 
   // x of pairs [qa, qa + cpp) -> LDS (INT4: permuted to the codes' order);
   // vectors past the end re-load the last one (same value, no branch).
@@ -549,7 +566,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
       const auto pr = x_addr(tid + u * threads, 0, xvecs);
       *reinterpret_cast<f16x8*>(pr.second) = xcvt(xv[u]);
     }
-    if (!kMulti) zero_x_tail(0, npairs);
+    zero_x_tail(0, min(a.cpp, npairs));
     if (svec) {
       if (qd < gn / 8) so_put(gv0 * 8, s4, o4);
       stage_so(0, gn, qd + 4);
@@ -627,6 +644,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   // pair) are straight-line code, so the compiler waits per ring slot; a
   // closing round of exactly P pairs is straight-line too.  Any other shape
   // of the last rounds tests each slot.
+  // One x pass over all pairs, a whole number of rounds (the single-pass
+  // kernel): every round in one loop, the closing round's refills reading
+  // nothing (`none`).  As straight-line code after the loop, the closing
+  // round made the compiler copy the ring on the way in, and the copy waited
+  // for every pair in flight; so did a second, general form of the rounds in
+  // the same kernel.
+  auto run_all = [&]() {
+    for (int qb = 0; qb < npairs; qb += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        consume(qb + s, s, 0);
+        fetch_from(s, qb + s + P, qb + s + P < npairs ? wres : none);
+        __builtin_amdgcn_sched_barrier(0x78F);  // only vector-memory instructions stay put
+      }
+    }
+  };
   auto run_pass = [&](int qa, int qe) {
     int qb = qa;
     for (; qb + P <= qe && qb + 2 * P <= npairs; qb += P) {
@@ -656,12 +689,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   };
   __syncthreads();
   if constexpr (!kMulti) {
-    // one pass: the rounds follow the prologue directly.  (A second inlined
-    // copy of the rounds, or a loop around them, made the compiler copy the
-    // ring registers at loop entry -- a copy waits for every load in flight.)
-    run_pass(0, npairs);
+    run_all();
   } else {
-    run_pass(0, a.cpp);
+    run_pass(0, min(a.cpp, npairs));
     for (int qa = a.cpp; qa < npairs; qa += a.cpp) {  // further x passes (workgroup-uniform)
       __syncthreads();  // every wave is done with the previous pass's x and scales
       stage_x_rest(qa, tid);
@@ -731,6 +761,7 @@ int launch_pairs(W4Args a, hipStream_t stream) {
   constexpr int kKP = kW8 ? 128 : 256;
   const int gq = kW8 ? 1 : a.group_size / 128;
   if (a.nchunks % 2 != 0 || (gq & (gq - 1)) != 0) return kNoFit;
+  if (static_cast<uint64_t>(a.n) * static_cast<uint64_t>(kW8 ? a.k : a.k / 2) > kMaxBufferBytes) return kNoFit;
   a.gq_shift = __builtin_ctz(gq);
   const int npairs = a.nchunks / 2;
   const int unit = std::max(P, gq / 2);  // both powers of two
@@ -764,7 +795,8 @@ int launch_pairs(W4Args a, hipStream_t stream) {
     kernel<<<(tiles + nw - 1) / nw, threads, lds, stream>>>(a);
     return RLK_OK;
   };
-  if (npass > 1) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, true, kW8>);
+  // the single-pass kernel takes a whole number of rounds; the rest is general
+  if (npass > 1 || npairs % P != 0) return go(gemv_w4_pairs_kernel<P, MT, MODE, 8, true, kW8>);
   if constexpr (P == 4 || P == 2) {  // the defaults: x staged by as many loads per thread as needed
     if (xper <= 2) return go(gemv_w4_pairs_kernel<P, MT, MODE, 2, false, kW8>);
     if (xper <= 4) return go(gemv_w4_pairs_kernel<P, MT, MODE, 4, false, kW8>);
@@ -894,6 +926,9 @@ int gemv_w8(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales, c
     return fail(RLK_EUNSUPPORTED, "%s: k=%d exceeds %d", what, k, 1 << 20);
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
     return fail(RLK_EINVAL, "%s: x and w must be 16-byte aligned", what);
+  if (static_cast<uint64_t>(n) * static_cast<uint64_t>(k) > kMaxBufferBytes)
+    return fail(RLK_EUNSUPPORTED, "%s: a weight of n*k = %llu bytes exceeds 2 GiB; split n", what,
+                static_cast<unsigned long long>(n) * static_cast<unsigned long long>(k));
   W4Args a{};
   a.x = x;
   a.w = reinterpret_cast<const uint8_t*>(w);
