@@ -313,3 +313,13 @@ def test_embedding_rmsnorm_argument_errors():
     assert b"multiple of 8" in L.rlk_last_error()
     assert L.rlk_embedding_rmsnorm(d, None, 4, 16, d, 1e-5, d, d, None) == _lib.RLK_EINVAL
     assert b"null pointer" in L.rlk_last_error()
+
+
+def test_gemv_w8_weight_over_2gib_refused():
+    # checked before any launch: the pointers are never dereferenced
+    L = ra.lib()
+    fake = C.c_void_p(1 << 20)  # 16-byte aligned, never read
+    y = C.c_void_p(2 << 20)
+    assert L.rlk_gemv_w8a16(fake, 1, fake, fake, None, 65536, 65536, y, 0, None) == \
+        _lib.RLK_EUNSUPPORTED
+    assert b"exceeds 2 GiB" in L.rlk_last_error()
