@@ -872,27 +872,38 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
 
 // Merges the split-K partials of one (item, head), one lane per output dim
 // (the merge rule of attention.cu:193-210).  Weight of partition i:
-// exp(m_i - max_j m_j) * l_i.  The partition statistics are read by all lanes
-// together and the weights kept in LDS; each lane then sums its dim over the
-// partitions with kUnroll partial-row loads in flight.
+// exp(m_i - max_j m_j) * l_i.  The workspace addresses depend only on the
+// (item, head), so the statistics of the first D partitions and the first
+// kEarly partial rows are requested before the context is known (token ->
+// position is two dependent reads), and masked once the partition count is:
+// the merge then costs about two memory round trips instead of five.
+// Entries past the count are never used (they may hold anything).
 constexpr int kReduceMaxParts = 4096;  // weights kept in LDS (contexts up to 1M keys)
 
 template <int D>
 __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
-  constexpr int kUnroll = 8;
+  constexpr int kEarly = 16;  // partial rows requested up front
+  constexpr int kUnroll = 8;  // rows in flight per step past them
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ float wgt[kReduceMaxParts];
   __shared__ float part_red[D / kWave];
   const int item = blockIdx.x, h = blockIdx.y, d = threadIdx.x, lane = d % kWave, wv = d / kWave;
+  const int mp = w.max_partitions;
+  const int64_t base = (static_cast<int64_t>(item) * p.num_heads + h) * mp;
+  const float* src = w.ws_out + base * D + d;
+  const float m0 = d < mp ? w.ws_max[base + d] : -FLT_MAX;
+  const float l0 = d < mp ? w.ws_sum[base + d] : 0.f;
+  float v0[kEarly];
+#pragma unroll
+  for (int u = 0; u < kEarly; ++u) v0[u] = u < mp ? src[static_cast<int64_t>(u) * D] : 0.f;
   const int token = w.item_token[item];
   const int ctx = p.positions[token] + 1;
-  const int num_parts = min((ctx + kPart - 1) / kPart, w.max_partitions);
+  const int num_parts = min((ctx + kPart - 1) / kPart, mp);
   if (num_parts <= 1) return;  // uniform: written directly by the attention kernel
-  const int64_t base = (static_cast<int64_t>(item) * p.num_heads + h) * w.max_partitions;
 
-  float mx = -FLT_MAX;
-  for (int i = d; i < num_parts; i += D) mx = fmaxf(mx, w.ws_max[base + i]);
+  float mx = d < num_parts ? m0 : -FLT_MAX;
+  for (int i = d + D; i < num_parts; i += D) mx = fmaxf(mx, w.ws_max[base + i]);
   mx = rows_max<true>(rows_max<false>(group_max<16>(mx)));
   if (lane == 0) part_red[wv] = mx;
   __syncthreads();
@@ -901,7 +912,12 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   for (int i = 1; i < D / kWave; ++i) mx = fmaxf(mx, part_red[i]);
   __syncthreads();  // part_red is reused below
   float total = 0.f;
-  for (int i = d; i < num_parts; i += D) {
+  if (d < num_parts) {
+    const float g = __expf(m0 - mx) * l0;
+    wgt[d] = g;
+    total = g;
+  }
+  for (int i = d + D; i < num_parts; i += D) {
     const float g = __expf(w.ws_max[base + i] - mx) * w.ws_sum[base + i];
     wgt[i] = g;
     total += g;
@@ -913,9 +929,11 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
 #pragma unroll
   for (int i = 1; i < D / kWave; ++i) total += part_red[i];
 
-  const float* src = w.ws_out + base * D + d;
   float o = 0.f;
-  int i = 0;
+#pragma unroll
+  for (int u = 0; u < kEarly; ++u)
+    if (u < num_parts) o += wgt[u] * v0[u];
+  int i = kEarly;
   for (; i + kUnroll <= num_parts; i += kUnroll) {
     float v[kUnroll];
 #pragma unroll
