@@ -28,6 +28,7 @@
 #include <cfloat>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "device.hpp"
 #include "redline_amd/rlk.h"
@@ -285,27 +286,35 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], acc[t], 0, 0, 0);
     }
   }
+  // INT8: the k scales of the lane's keys, from LDS, already multiplied by
+  // the softmax scale (scale * k_scale, the same product as scale * ks here)
 #pragma unroll
-  for (int x = 0; x < 8; ++x)  // INT8 k scales of the lane's keys, from LDS
-    ks[x] = kInt8 ? ksc[mma_key<D>(c, x / 4, 4 * rho + x % 4)] : 1.f;
+  for (int x = 0; x < 8; ++x) ks[x] = kInt8 ? ksc[mma_key<D>(c, x / 4, 4 * rho + x % 4)] : scale;
   then();
-  float e[2][4];
+  float e[2][4], m, l;
+  // keys past the context are masked only in a unit that has such keys
+  // (uniform branch: a full unit skips the compares and selects)
+  auto softmax = [&](auto masked) {
+    constexpr bool kMasked = decltype(masked)::value;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      e[t][i] = mma_key<D>(c, t, 4 * rho + i) < n ? acc[t][i] * (scale * ks[4 * t + i]) : -FLT_MAX;
-  float m = e[0][0];
+      for (int i = 0; i < 4; ++i)
+        e[t][i] = !kMasked || mma_key<D>(c, t, 4 * rho + i) < n ? acc[t][i] * ks[4 * t + i] : -FLT_MAX;
+    m = e[0][0];
 #pragma unroll
-  for (int x = 1; x < 8; ++x) m = fmaxf(m, e[x / 4][x % 4]);
-  m = rows_max<true>(rows_max<false>(m));
-  float l = 0.f;
+    for (int x = 1; x < 8; ++x) m = fmaxf(m, e[x / 4][x % 4]);
+    m = rows_max<true>(rows_max<false>(m));
+    l = 0.f;
 #pragma unroll
-  for (int x = 0; x < 8; ++x) {
-    const float v = mma_key<D>(c, x / 4, 4 * rho + x % 4) < n ? __expf(e[x / 4][x % 4] - m) : 0.f;
-    e[x / 4][x % 4] = v;
-    l += v;
-  }
+    for (int x = 0; x < 8; ++x) {
+      const float v = !kMasked || mma_key<D>(c, x / 4, 4 * rho + x % 4) < n ? __expf(e[x / 4][x % 4] - m) : 0.f;
+      e[x / 4][x % 4] = v;
+      l += v;
+    }
+  };
+  if (n >= kPart) softmax(std::false_type{});
+  else softmax(std::true_type{});
   l = rows_sum<true>(rows_sum<false>(l));
   if (rho == 0 && g < G) {
     stat[c.wave][g][0] = m;
@@ -554,8 +563,8 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
 }
 
 // Combines the waves of a unit: M = max m_w, L = sum e^(m_w - M) l_w,
-// o = sum e^(m_w - M) o_w / L; written as the output row (one partition) or
-// as the unit's split-K partial row.
+// o = sum e^(m_w - M) o_w; written as the output row o / L (one partition)
+// or as the unit's split-K partial row o with its (M, L).
 template <int D, int G>
 __device__ __forceinline__ void combine_waves(const AttnArgs& args, const float (&red)[kWaves][G][D + kRedPad],
                                               const float (&stat)[kWaves][G][2], int tid, int item,
@@ -574,12 +583,11 @@ __device__ __forceinline__ void combine_waves(const AttnArgs& args, const float 
       L += f * stat[ww][g][1];
       o += f * red[ww][g][d];
     }
-    o /= L;
     const int h = kvh * G + g;
     if (num_parts == 1) {
       reinterpret_cast<_Float16*>(p.out)[static_cast<int64_t>(token) * p.num_heads * D + h * D + d] =
-          static_cast<_Float16>(o);
-    } else {
+          static_cast<_Float16>(o / L);
+    } else {  // the partition's partial, not divided by its sum L (the merge weighs it by e^(M - max))
       const int64_t row = (static_cast<int64_t>(item) * p.num_heads + h) * w.max_partitions + part;
       w.ws_out[row * D + d] = o;
       if (d == 0) {
@@ -597,7 +605,7 @@ struct UnitLds {
   float red[kWaves][G][D + kRedPad];  // each wave's P . V partial
   float stat[kWaves][G][2];  // each wave's (max, sum) per head
   int cell[2][kPart];        // cache cell of each key of the partition
-  float ksc[2][kPart];       // its INT8 k and v scales
+  float ksc[2][kPart];       // its INT8 k scale times the softmax scale, and v scale
   float vsc[2][kPart];
   alignas(16) _Float16 q[2][G * D];
 };
@@ -768,7 +776,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     write_cells<kInt8>(s.cell[0], args, tid, table_entry(p, tid, it_seq[cur.item], cur.part, keys_in(cur)),
                        cur.part, cur.kvh, ks0, vs0, keys_in(cur));
     if (kInt8 && tid < kPart) {
-      s.ksc[0][tid] = scale_value(ks0, args.scale16);
+      s.ksc[0][tid] = p.scale * scale_value(ks0, args.scale16);
       s.vsc[0][tid] = scale_value(vs0, args.scale16);
     }
   }
@@ -818,7 +826,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     // cells(n+2) to the buffer cells(n) used, free once every wave has
     // requested V(n), i.e. after this barrier
     if (kInt8 && has1 && c.tid < kPart) {
-      s.ksc[b ^ 1][c.tid] = scale_value(sk_next, args.scale16);
+      s.ksc[b ^ 1][c.tid] = p.scale * scale_value(sk_next, args.scale16);
       s.vsc[b ^ 1][c.tid] = scale_value(sv_next, args.scale16);
     }
     if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next, keys_in(nn));
@@ -847,7 +855,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
     uint32_t ks0, vs0;
     write_cells<kInt8>(s.cell[0], args, tid, blk, part, kvh, ks0, vs0);
     if (kInt8 && tid < kPart) {
-      s.ksc[0][tid] = scale_value(ks0, args.scale16);
+      s.ksc[0][tid] = p.scale * scale_value(ks0, args.scale16);
       s.vsc[0][tid] = scale_value(vs0, args.scale16);
     }
   }
@@ -871,8 +879,9 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
 }
 
 // Merges the split-K partials of one (item, head), one lane per output dim
-// (the merge rule of attention.cu:193-210).  Weight of partition i:
-// exp(m_i - max_j m_j) * l_i.  The workspace addresses depend only on the
+// (the merge rule of attention.cu:193-210).  A partition's partial row is
+// sum_k e^(s_k - m_i) v_k, not divided by its sum l_i; the output is
+// sum_i e^(m_i - M) row_i / sum_i e^(m_i - M) l_i with M = max_i m_i.  The workspace addresses depend only on the
 // (item, head), so the statistics of the first D partitions and the first
 // kEarly partial rows are requested before the context is known (token ->
 // position is two dependent reads), and masked once the partition count is:
@@ -913,14 +922,14 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   __syncthreads();  // part_red is reused below
   float total = 0.f;
   if (d < num_parts) {
-    const float g = __expf(m0 - mx) * l0;
-    wgt[d] = g;
-    total = g;
+    const float f = __expf(m0 - mx);
+    wgt[d] = f;
+    total = f * l0;
   }
   for (int i = d + D; i < num_parts; i += D) {
-    const float g = __expf(w.ws_max[base + i] - mx) * w.ws_sum[base + i];
-    wgt[i] = g;
-    total += g;
+    const float f = __expf(w.ws_max[base + i] - mx);
+    wgt[i] = f;
+    total += f * w.ws_sum[base + i];
   }
   total = wave_sum(total);
   if (lane == 0) part_red[wv] = total;
