@@ -258,10 +258,12 @@ def kernel_fns(data):
             "stream_copy": data.stream_copy}
 
 
-def per_kernel(torch, data, reps, only=None, names=KERNELS):
+def per_kernel(torch, data, reps, only=None, names=KERNELS, warm=True):
     """Per-call time of each kernel: a graph of R back-to-back launches (one
-    per rotating input set), replayed `reps` times between HIP events on the
-    launch stream."""
+    per rotating input set, so the inputs come from HBM: the cold figure the
+    roofline uses), replayed `reps` times between HIP events on the launch
+    stream; with `warm`, also R launches on input set 0 (the warm figure:
+    inputs left in the caches by the previous launch where they fit)."""
     fns = kernel_fns(data)
     nbytes = data.bytes()
     out = {}
@@ -271,13 +273,20 @@ def per_kernel(torch, data, reps, only=None, names=KERNELS):
         f = fns[name]
         g = capture(torch, lambda: [f(r) for r in range(data.R)])
         ms = time_graph(torch, g, reps) / data.R
+        del g
         gbs = nbytes[name] / (ms * 1e-3) / 1e9
         out[name] = {"us_per_call": round(ms * 1e3, 3), "gb_per_s": round(gbs, 1),
                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_call": nbytes[name]}
-        log(f"  {data.w.key} {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s "
-            f"({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)  R={data.R}")
-        del g
+        msg = (f"  {data.w.key} {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s "
+               f"({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)  R={data.R}")
+        if warm:
+            g = capture(torch, lambda: [f(0) for _ in range(data.R)])
+            ms_w = time_graph(torch, g, reps) / data.R
+            del g
+            out[name]["us_per_call_warm"] = round(ms_w * 1e3, 3)
+            msg += f"; warm {ms_w * 1e3:9.2f} us"
+        log(msg)
     return out
 
 
@@ -302,7 +311,7 @@ def sweep(torch, data, reps, only=None):
         for vals in itertools.product(*knobs.values()):
             for n, v in zip(names, vals):
                 set_tune_knob(n, v)
-            r = per_kernel(torch, data, reps, kern, names=(kern,))[kern]
+            r = per_kernel(torch, data, reps, kern, names=(kern,), warm=False)[kern]
             print(json.dumps({"workload": data.w.key, "kernel": kern, "knobs": dict(zip(names, vals)),
                               "us_per_call": r["us_per_call"], "gb_per_s": r["gb_per_s"]}),
                   flush=True)
