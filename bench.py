@@ -559,31 +559,41 @@ def cpu_baseline(torch, data, seconds=8.0, max_threads=16):
                   nb["fused_add_rmsnorm"] + nb["silu_and_mul"])
     affinity = L.cps_affinity_cores()
 
+    ops = ("embedding_lookup", "fused_add_rmsnorm_nodelta", "rope_and_write_kv", "fused_add_rmsnorm",
+           "silu_and_mul")
+
     def run(threads):
+        """Steps for `seconds`; returns (steps, seconds, each op's seconds)."""
         pool = L.cps_create(threads)
         if not pool:
             raise RuntimeError("CPU baseline needs AVX2 and F16C")
+        op_s = np.zeros(len(ops), np.float64)
         try:
             for _ in range(3):
                 L.cps_layer_step(pool, *args)  # warm: page in the table rows and the cache
             n, t0 = 0, time.perf_counter()
             while True:
-                L.cps_layer_step(pool, *args)
+                L.cps_layer_step_timed(pool, *args, p(op_s))
                 n += 1
                 dt = time.perf_counter() - t0
                 if dt >= seconds:
                     break
         finally:
             L.cps_destroy(pool)
-        return n, dt
+        return n, dt, op_s
 
-    n1, dt1 = run(1)
+    def per_op(n, op_s):
+        return {k: {"us_per_call": round(op_s[i] / n * 1e6, 2),
+                    "gb_per_s": round(nb[k] / (op_s[i] / n) / 1e9, 3)} for i, k in enumerate(ops)}
+
+    n1, dt1, op1 = run(1)
     threads = max(1, min(affinity, max_threads))
-    nm, dtm = run(threads)
+    nm, dtm, opm = run(threads)
     gbs = lambda n, dt: round(step_bytes * n / dt / 1e9, 3)  # noqa: E731
     return {"value": gbs(nm, dtm), "unit": "GB/s", "cores": threads, "kind": "port",
-            "ms_per_step": round(dtm / nm * 1e3, 4),
-            "single_thread": {"value": gbs(n1, dt1), "ms_per_step": round(dt1 / n1 * 1e3, 4)},
+            "ms_per_step": round(dtm / nm * 1e3, 4), "per_kernel": per_op(nm, opm),
+            "single_thread": {"value": gbs(n1, dt1), "ms_per_step": round(dt1 / n1 * 1e3, 4),
+                              "per_kernel": per_op(n1, op1)},
             "affinity_cores": affinity,
             "sample": f"{w.key} layer steps (embedding, RMSNorm, RoPE+KV, add+RMSNorm, SwiGLU: the "
                       f"reference's five launches) on one "

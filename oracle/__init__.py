@@ -80,6 +80,8 @@ def cpu_step_lib() -> C.CDLL:
         L.cps_destroy.restype, L.cps_destroy.argtypes = None, [_P]
         L.cps_layer_step.restype = None
         L.cps_layer_step.argtypes = [_P] + list(lib().orc_layer_step.argtypes)
+        L.cps_layer_step_timed.restype = None
+        L.cps_layer_step_timed.argtypes = [_P] + list(lib().orc_layer_step.argtypes) + [_P]
         _c = L
     return _c
 

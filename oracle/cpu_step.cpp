@@ -18,14 +18,18 @@
 // to stay obviously correct), this port converts 8 values per instruction with
 // the x86 F16C unit (IEEE round-to-nearest-even, the same results), and splits
 // every op over a persistent pool of std::threads by rows (tokens), or by
-// element ranges for SwiGLU.  Threads are pinned to the cores of the process's
-// affinity mask (sched_getaffinity).
+// ranges of 8-element groups for SwiGLU, whose exp is an AVX2 routine of its
+// own (exp8: Cody-Waite reduction and a Taylor polynomial, about 1 ulp; the
+// SwiGLU output stays within fp16 tolerance of the oracle's libm exp).
+// Threads are pinned to the cores of the process's affinity mask
+// (sched_getaffinity).
 #include <immintrin.h>
 #include <pthread.h>
 #include <sched.h>
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <condition_variable>
 #include <cstdint>
@@ -226,15 +230,40 @@ void rope_kv(Pool& pool, uint16_t* qkv, const int32_t* pos, const int32_t* slots
   });
 }
 
+// e^x for 8 floats (AVX2, no FMA): Cody-Waite range reduction x = n ln2 + r
+// with ln2 split in two parts (the first exact in 9 bits), e^r on
+// [-ln2/2, ln2/2] by its Taylor polynomial to degree 6 (truncation error
+// below 1.3e-7 relative), and 2^n built in the exponent field.  Inputs are
+// clamped to [-87.3, 88.7], where e^x is a normal float.
+inline __m256 exp8(__m256 x) {
+  x = _mm256_min_ps(_mm256_max_ps(x, _mm256_set1_ps(-87.3f)), _mm256_set1_ps(88.7f));
+  const __m256 n = _mm256_round_ps(_mm256_mul_ps(x, _mm256_set1_ps(1.44269504088896341f)),
+                                   _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+  __m256 r = _mm256_sub_ps(x, _mm256_mul_ps(n, _mm256_set1_ps(0.693359375f)));
+  r = _mm256_sub_ps(r, _mm256_mul_ps(n, _mm256_set1_ps(-2.12194440054690583e-4f)));
+  __m256 p = _mm256_set1_ps(1.f / 720.f);
+  const float c[6] = {1.f / 120.f, 1.f / 24.f, 1.f / 6.f, 0.5f, 1.f, 1.f};
+  for (float k : c) p = _mm256_add_ps(_mm256_mul_ps(p, r), _mm256_set1_ps(k));
+  const __m256i e = _mm256_slli_epi32(_mm256_add_epi32(_mm256_cvtps_epi32(n), _mm256_set1_epi32(127)), 23);
+  return _mm256_mul_ps(p, _mm256_castsi256_ps(e));
+}
+
+// fp16(fp16(silu(g)) * u), 8 elements at a time (inter is a multiple of 8).
 void silu_and_mul(Pool& pool, const uint16_t* gu, int T, int I, uint16_t* out) {
-  pool.run(static_cast<int64_t>(T) * I, [&](int64_t b, int64_t e) {
-    int64_t r = b / I, i = b - r * I;
-    for (int64_t g = b; g < e; ++g) {
-      const float x = h2f(gu[r * 2 * I + i]);
-      const float sg = roundh(x / (1.0f + std::exp(-x)));
-      out[g] = f2h(sg * h2f(gu[r * 2 * I + I + i]));
-      if (++i == I) {
-        i = 0;
+  const int gpr = I / 8;  // groups of 8 per row
+  pool.run(static_cast<int64_t>(T) * gpr, [&](int64_t b, int64_t e) {
+    int64_t r = b / gpr, j = b - r * gpr;
+    const __m256 one = _mm256_set1_ps(1.f);
+    for (int64_t q = b; q < e; ++q) {
+      const uint16_t* row = gu + r * 2 * I + 8 * j;
+      const __m256 x = _mm256_cvtph_ps(_mm_loadu_si128(reinterpret_cast<const __m128i*>(row)));
+      const __m256 u = _mm256_cvtph_ps(_mm_loadu_si128(reinterpret_cast<const __m128i*>(row + I)));
+      __m256 s = _mm256_div_ps(x, _mm256_add_ps(one, exp8(_mm256_sub_ps(_mm256_setzero_ps(), x))));
+      s = _mm256_cvtph_ps(_mm256_cvtps_ph(s, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+      _mm_storeu_si128(reinterpret_cast<__m128i*>(out + r * I + 8 * j),
+                       _mm256_cvtps_ph(_mm256_mul_ps(s, u), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+      if (++j == gpr) {
+        j = 0;
         ++r;
       }
     }
@@ -261,6 +290,14 @@ void* cps_create(int threads) {
 
 void cps_destroy(void* pool) { delete static_cast<Pool*>(pool); }
 
+void cps_layer_step_timed(void* pool_, const int32_t* ids, const uint16_t* table, int T, int H,
+                          uint16_t* emb, uint16_t* residual, const uint16_t* delta,
+                          const uint16_t* w_norm, float eps, uint16_t* normed, uint16_t* qkv,
+                          const int32_t* positions, const int32_t* slots, int Hq, int Hkv, int D,
+                          const float* cos_t, const float* sin_t, void* k_cache, void* v_cache,
+                          float* k_scale, float* v_scale, int bs, int int8,
+                          const uint16_t* gate_up, int I, uint16_t* act, double* seconds);
+
 // One layer step, the same arguments as the oracle's orc_layer_step.
 // head_dim must be 64 or 128, hidden and inter multiples of 8.
 void cps_layer_step(void* pool_, const int32_t* ids, const uint16_t* table, int T, int H,
@@ -270,13 +307,41 @@ void cps_layer_step(void* pool_, const int32_t* ids, const uint16_t* table, int 
                     const float* cos_t, const float* sin_t, void* k_cache, void* v_cache,
                     float* k_scale, float* v_scale, int bs, int int8, const uint16_t* gate_up,
                     int I, uint16_t* act) {
+  cps_layer_step_timed(pool_, ids, table, T, H, emb, residual, delta, w_norm, eps, normed, qkv,
+                       positions, slots, Hq, Hkv, D, cos_t, sin_t, k_cache, v_cache, k_scale,
+                       v_scale, bs, int8, gate_up, I, act, nullptr);
+}
+
+// The same step; with seconds != null, adds each op's wall time (its rows
+// split over the pool, dispatch and join included) to seconds[0..4]:
+// embedding, RMSNorm without delta, RoPE + KV, add + RMSNorm, SwiGLU.
+void cps_layer_step_timed(void* pool_, const int32_t* ids, const uint16_t* table, int T, int H,
+                          uint16_t* emb, uint16_t* residual, const uint16_t* delta,
+                          const uint16_t* w_norm, float eps, uint16_t* normed, uint16_t* qkv,
+                          const int32_t* positions, const int32_t* slots, int Hq, int Hkv, int D,
+                          const float* cos_t, const float* sin_t, void* k_cache, void* v_cache,
+                          float* k_scale, float* v_scale, int bs, int int8,
+                          const uint16_t* gate_up, int I, uint16_t* act, double* seconds) {
   Pool& pool = *static_cast<Pool*>(pool_);
+  using clock = std::chrono::steady_clock;
+  auto t = clock::now();
+  auto lap = [&](int op) {
+    if (seconds == nullptr) return;
+    const auto now = clock::now();
+    seconds[op] += std::chrono::duration<double>(now - t).count();
+    t = now;
+  };
   embedding(pool, ids, table, T, H, emb);
+  lap(0);
   add_rmsnorm(pool, emb, nullptr, w_norm, T, H, eps, normed);
+  lap(1);
   rope_kv(pool, qkv, positions, slots, T, Hq, Hkv, D, cos_t, sin_t, k_cache, v_cache, k_scale,
           v_scale, bs, int8);
+  lap(2);
   add_rmsnorm(pool, residual, delta, w_norm, T, H, eps, normed);
+  lap(3);
   silu_and_mul(pool, gate_up, T, I, act);
+  lap(4);
 }
 
 }  // extern "C"

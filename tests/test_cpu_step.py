@@ -9,13 +9,13 @@ import pytest
 import oracle
 
 
-def _step(fn, pool, a):
+def _step(fn, pool, a, extra=()):
     p = oracle.p
     args = (p(a["ids"]), p(a["table"]), a["T"], a["H"], p(a["emb"]), p(a["res"]), p(a["delta"]),
             p(a["w"]), np.float32(a["eps"]).item(), p(a["normed"]), p(a["qkv"]), p(a["pos"]),
             p(a["slot"]), a["hq"], a["hkv"], a["D"], p(a["cos"]), p(a["sin"]), p(a["kc"]),
             p(a["vc"]), p(a["ks"]), p(a["vs"]), 16, int(a["int8"]), p(a["gu"]), a["I"],
-            p(a["act"]))
+            p(a["act"])) + tuple(extra)
     fn(*((pool,) + args if pool is not None else args))
 
 
@@ -61,3 +61,47 @@ def test_cpu_step_matches_oracle(threads, int8, D):
 
 def test_affinity_cores():
     assert oracle.cpu_step_lib().cps_affinity_cores() >= 1
+
+
+def test_cpu_step_timed_same_results_and_op_times():
+    """cps_layer_step_timed: the same outputs as cps_layer_step on the same
+    inputs, and each of the five ops' wall times added to its slot (the
+    bench's per-kernel CPU figures)."""
+    rng = np.random.default_rng(5)
+    a = _inputs(rng, False, 128)
+    b = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in a.items()}
+    L = oracle.cpu_step_lib()
+    pool = L.cps_create(2)
+    if not pool:
+        pytest.skip("CPU lacks AVX2/F16C")
+    t = np.zeros(5, np.float64)
+    try:
+        _step(L.cps_layer_step, pool, a)
+        _step(L.cps_layer_step_timed, pool, b, (oracle.p(t),))
+    finally:
+        L.cps_destroy(pool)
+    for k in ("emb", "res", "normed", "qkv", "kc", "vc", "act"):
+        assert np.array_equal(a[k], b[k]), k
+    assert np.all(t > 0) and t.sum() < 10.0
+
+
+def test_cpu_step_swiglu_wide_gate():
+    """The port's vectorised exp over gates from -100 to 100 (its clamps at
+    -87.3 and 88.7 included): SwiGLU within the fp16 tolerance of the oracle."""
+    rng = np.random.default_rng(11)
+    a = _inputs(rng, False, 64)
+    g = np.linspace(-100, 100, a["T"] * a["I"]).reshape(a["T"], a["I"]).astype(np.float16)
+    u = rng.uniform(-2, 2, (a["T"], a["I"])).astype(np.float16)
+    a["gu"] = np.ascontiguousarray(np.concatenate([g, u], axis=1)).view(np.uint16)
+    b = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in a.items()}
+    _step(oracle.lib().orc_layer_step, None, a)
+    L = oracle.cpu_step_lib()
+    pool = L.cps_create(2)
+    if not pool:
+        pytest.skip("CPU lacks AVX2/F16C")
+    try:
+        _step(L.cps_layer_step, pool, b)
+    finally:
+        L.cps_destroy(pool)
+    x, y = a["act"].view(np.float16).astype(np.float64), b["act"].view(np.float16).astype(np.float64)
+    assert np.all(np.abs(x - y) <= 2e-3 + 1e-2 * np.abs(x))
