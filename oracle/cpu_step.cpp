@@ -57,7 +57,10 @@ inline uint16_t f2h(float f) { return _cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT); }
 inline float roundh(float f) { return h2f(f2h(f)); }
 
 // Persistent pool: run(n, fn) calls fn(i) for i in [0, n) over the threads
-// (the caller is thread 0) and returns when all are done.
+// (the caller is thread 0) and returns when all are done.  An idle worker
+// spins on the generation counter for a while (about a millisecond) before it
+// sleeps on the condition variable, so back-to-back ops of a step are handed
+// out in about a microsecond instead of a futex wake-up each.
 class Pool {
  public:
   explicit Pool(int threads) : n_(std::max(1, threads)) {
@@ -81,7 +84,7 @@ class Pool {
     {
       std::lock_guard<std::mutex> l(mu_);
       stop_ = true;
-      ++gen_;
+      gen_.fetch_add(1, std::memory_order_release);
     }
     cv_.notify_all();
     for (auto& w : workers_) w.join();
@@ -99,7 +102,7 @@ class Pool {
       fn_ = &fn;
       total_ = total;
       pending_.store(n_ - 1, std::memory_order_relaxed);
-      ++gen_;
+      gen_.fetch_add(1, std::memory_order_release);
     }
     cv_.notify_all();
     range(0, fn);
@@ -115,10 +118,15 @@ class Pool {
     uint64_t seen = 0;
     for (;;) {
       const std::function<void(int64_t, int64_t)>* fn;
+      bool fresh = false;
+      for (int i = 0; i < kSpin && !fresh; ++i) {
+        fresh = gen_.load(std::memory_order_acquire) != seen;
+        if (!fresh) _mm_pause();
+      }
       {
         std::unique_lock<std::mutex> l(mu_);
-        cv_.wait(l, [&] { return gen_ != seen; });
-        seen = gen_;
+        if (!fresh) cv_.wait(l, [&] { return gen_.load(std::memory_order_acquire) != seen; });
+        seen = gen_.load(std::memory_order_acquire);
         if (stop_) return;
         fn = fn_;
       }
@@ -130,7 +138,8 @@ class Pool {
   std::vector<std::thread> workers_;
   std::mutex mu_;
   std::condition_variable cv_;
-  uint64_t gen_ = 0;
+  static constexpr int kSpin = 1 << 14;  // pause instructions before sleeping
+  std::atomic<uint64_t> gen_{0};
   bool stop_ = false;
   const std::function<void(int64_t, int64_t)>* fn_ = nullptr;
   int64_t total_ = 0;
