@@ -20,8 +20,10 @@
 //     loaded it, and the softmax output is the B operand as it stands; the 8
 //     waves' partial outputs are combined through LDS (a v_dot2 form of P . V
 //     remains selectable);
-//   * INT8 codes become exact fp16 values through byte permutes under an
-//     fp16 exponent, without conversion instructions.
+//   * INT8 codes become exact fp16 values (1152 + code) through byte
+//     permutes under an fp16 exponent, without conversion instructions; the
+//     constant leaves the q . k and P . V sums through one more MFMA each,
+//     whose A operand is -1152 everywhere.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>

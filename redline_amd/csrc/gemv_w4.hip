@@ -427,9 +427,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_kernel(W4Args a) {
 // that its partner lane r16 ^ 8 keeps (chunk 1), handed over by one DPP
 // row_ror:8 per dword -- no LDS round trip.
 //
+// The ring is read through buffer loads (the lane's row offset in a VGPR, the
+// pair's offset in the scalar offset), and the last round's refills go
+// through a buffer resource with no records, which reads nothing.
+//
 // Measured against the slab kernel above (same MFMA math): a ring of P = 4
-// pairs per wave (8 KB in flight) beats deeper rings; the last round issues
-// no refills (re-fetching the last pair in every slot cost ~2 us at the
+// pairs per wave (8 KB in flight) beats deeper rings; the last round fetches
+// nothing (re-fetching the last pair in every slot cost ~2 us at the
 // Llama-3.1-8B gate_up shape); x is staged in one batch of loads; and each
 // wave stages the scales and offsets of its own 16 rows into its own LDS rows
 // with 16-byte loads, so that only x needs the workgroup barrier.
@@ -640,10 +644,6 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
     chunk(2 * (q - qa) + 1, recv);
   };
 
-  // The pairs [qa, qe) of one x pass.  Full rounds (every refill a valid
-  // pair) are straight-line code, so the compiler waits per ring slot; a
-  // closing round of exactly P pairs is straight-line too.  Any other shape
-  // of the last rounds tests each slot.
   // One x pass over all pairs, a whole number of rounds (the single-pass
   // kernel): every round in one loop, the closing round's refills reading
   // nothing (`none`).  As straight-line code after the loop, the closing
@@ -660,6 +660,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
       }
     }
   };
+  // The pairs [qa, qe) of one x pass (the multi-pass kernel).  Full rounds
+  // (every refill a valid pair) are straight-line code, so the compiler waits
+  // per ring slot; a closing round of exactly P pairs is straight-line too.
+  // Any other shape of the last rounds tests each slot.
   auto run_pass = [&](int qa, int qe) {
     int qb = qa;
     for (; qb + P <= qe && qb + 2 * P <= npairs; qb += P) {
