@@ -256,28 +256,20 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
                                             float (&stat)[kWaves][G][2], Then then) {
   constexpr int kSteps = D / 32, kP = Geo<D>::kPasses;
   const int lane = c.tid % kWave, g = lane % 16, rho = lane / 16;
-  f16x8 qb[kSteps];
+  // q of one MFMA step at a time (B: column g = head g), so only one step's
+  // operand is live.  INT8: A holds 1152 + code (int8x8_to_f16_biased), so
+  // the scores also collect -1152 * sum_d q[g][d], one MFMA per step with
+  // A = -1152 everywhere (the same for every key row), added at the end,
+  // instead of a subtract per pair of codes
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) {
-    qb[st] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (g < G) qb[st] = *reinterpret_cast<const f16x8*>(qs + g * D + step_dim<D, kInt8>(st, rho));
-  }
-  // INT8: A holds 1152 + code (int8x8_to_f16_biased), so every score starts
-  // from -1152 * sum_d q[g][d], one MFMA per step with A = -1152 everywhere
-  // (the same for every key row), instead of a subtract per pair of codes
-  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (kInt8) {
+    f16x8 qb = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (g < G) qb = *reinterpret_cast<const f16x8*>(qs + g * D + step_dim<D, kInt8>(st, rho));
+    if constexpr (kInt8) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(minus1152x8(), qb, acc0, 0, 0, 0);
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st)
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(minus1152x8(), qb[st], acc0, 0, 0, 0);
-  }
-  f32x4 acc[2];
-  float ks[8];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    acc[t] = acc0;
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
+    for (int t = 0; t < 2; ++t) {
       f16x8 a;
       if constexpr (kInt8) {
         const u32x4 w = kb.r[t][st / 2];
@@ -285,14 +277,17 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
       } else {
         a = __builtin_bit_cast(f16x8, kb.r[t][st]);
       }
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[st], acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb, acc[t], 0, 0, 0);
     }
   }
+  if constexpr (kInt8) {
+    acc[0] += acc0;
+    acc[1] += acc0;
+  }
+  then();
   // INT8: the k scales of the lane's keys, from LDS, already multiplied by
   // the softmax scale (scale * k_scale, the same product as scale * ks here)
-#pragma unroll
-  for (int x = 0; x < 8; ++x) ks[x] = kInt8 ? ksc[mma_key<D>(c, x / 4, 4 * rho + x % 4)] : scale;
-  then();
+  auto ks = [&](int x) { return kInt8 ? ksc[mma_key<D>(c, x / 4, 4 * rho + x % 4)] : scale; };
   float e[2][4], m, l;
   // keys past the context are masked only in a unit that has such keys
   // (uniform branch: a full unit skips the compares and selects)
@@ -302,7 +297,7 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        e[t][i] = !kMasked || mma_key<D>(c, t, 4 * rho + i) < n ? acc[t][i] * ks[4 * t + i] : -FLT_MAX;
+        e[t][i] = !kMasked || mma_key<D>(c, t, 4 * rho + i) < n ? acc[t][i] * ks(4 * t + i) : -FLT_MAX;
     m = e[0][0];
 #pragma unroll
     for (int x = 1; x < 8; ++x) m = fmaxf(m, e[x / 4][x % 4]);
@@ -539,13 +534,6 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
       int8_cols_to_f16_biased(w, a);
     }
   }
-  // The operands are complete here: the V registers are free for the next
-  // unit's rows (then()).  Without this point the compiler sinks part of the
-  // operand build below the refill, keeps both batches live and copies one
-  // of them at the loop edge, which waits for every load in flight.
-#pragma unroll
-  for (int dt = 0; dt < kTiles; ++dt) asm volatile("" : "+v"(a[dt])::"memory");
-  then();
   // INT8: A holds 1152 + code, so every tile starts from -1152 * sum_k b[k][g]
   // (one MFMA with A = -1152 everywhere, the same for every dim row)
   f32x4 o0 = {0.f, 0.f, 0.f, 0.f};
@@ -562,6 +550,10 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
       }
     }
   }
+  // The V registers are free once every tile is consumed: the next unit's
+  // rows go out only now, so the operand tiles need not all be live beside
+  // the refilled batch.
+  then();
 }
 
 // Combines the waves of a unit: M = max m_w, L = sum e^(m_w - M) l_w,
