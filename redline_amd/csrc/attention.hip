@@ -558,24 +558,37 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
 
 // Combines the waves of a unit: M = max m_w, L = sum e^(m_w - M) l_w,
 // o = sum e^(m_w - M) o_w; written as the output row o / L (one partition)
-// or as the unit's split-K partial row o with its (M, L).
+// or as the unit's split-K partial row o with its (M, L).  With D a multiple
+// of 64 every lane of a wave serves the same head g, so the weights are
+// computed once per wave: lane l takes wave l % 8's statistics, the max is a
+// reduction over 8 lanes, and lanes 0-7 leave e^(m_w - M) and l_w in the
+// wave's own LDS slots `wgt`, which the wave reads back (LDS accesses of one
+// wave complete in order; no barrier).  The sums run in wave order as fmas,
+// so every lane forms the same L and o as a per-lane loop over the waves.
 template <int D, int G>
 __device__ __forceinline__ void combine_waves(const AttnArgs& args, const float (&red)[kWaves][G][D + kRedPad],
-                                              const float (&stat)[kWaves][G][2], int tid, int item,
+                                              const float (&stat)[kWaves][G][2],
+                                              float (&wgt)[kWaves][2][kWaves], int tid, int item,
                                               int token, int num_parts, int part, int kvh) {
+  static_assert(kWaves == 8 && D % kWave == 0, "one head per wave, 8 waves per workgroup");
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
-  for (int i = tid; i < G * D; i += kThreads) {
+  const int wave = tid / kWave, lane = tid % kWave;
+  for (int i = tid; i < G * D; i += kThreads) {  // uniform over a wave
     const int g = i / D, d = i % D;
-    float M = stat[0][g][0];
-#pragma unroll
-    for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, stat[ww][g][0]);
+    const int ww = lane % kWaves;
+    const float mw = stat[ww][g][0];
+    const float M = group_max<kWaves>(mw);
+    if (lane < kWaves) {
+      wgt[wave][0][lane] = __expf(mw - M);
+      wgt[wave][1][lane] = stat[lane][g][1];
+    }
     float L = 0.f, o = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
-      const float f = __expf(stat[ww][g][0] - M);
-      L += f * stat[ww][g][1];
-      o += f * red[ww][g][d];
+    for (int v = 0; v < kWaves; ++v) {
+      const float f = wgt[wave][0][v];
+      L += f * wgt[wave][1][v];
+      o += f * red[v][g][d];
     }
     const int h = kvh * G + g;
     if (num_parts == 1) {
@@ -598,6 +611,7 @@ template <int D, int G>
 struct UnitLds {
   float red[kWaves][G][D + kRedPad];  // each wave's P . V partial
   float stat[kWaves][G][2];  // each wave's (max, sum) per head
+  float wgt[kWaves][2][kWaves];  // per wave: the combine's e^(m_w - M) and l_w of every wave
   int cell[2][kPart];        // cache cell of each key of the partition
   float ksc[2][kPart];       // its INT8 k scale times the softmax scale, and v scale
   float vsc[2][kPart];
@@ -824,7 +838,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
       s.vsc[b ^ 1][c.tid] = scale_value(sv_next, args.scale16);
     }
     if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next, keys_in(nn));
-    combine_waves<D, G>(args, s.red, s.stat, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
+    combine_waves<D, G>(args, s.red, s.stat, s.wgt, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
                         cur.part, cur.kvh);
     __syncthreads();
     cur = nxt;
@@ -868,7 +882,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
     wave_pv<D, G, kInt8>(vb, s.vsc[0], po, c, s.red, [] {});
   }
   __syncthreads();
-  combine_waves<D, G>(args, s.red, s.stat, tid, item, token,
+  combine_waves<D, G>(args, s.red, s.stat, s.wgt, tid, item, token,
                       min((ctx + kPart - 1) / kPart, w.max_partitions), part, kvh);
 }
 
