@@ -228,22 +228,24 @@ def capture(torch, fn):
 
 
 def time_graph(torch, graph, reps, warm_ms=20.0):
-    """Average ms per replay, HIP events on the replay stream, after at least
-    `warm_ms` of untimed replays (a single warm-up replay left the first of
-    several back-to-back timings of one kernel up to 10% slow)."""
+    """Median ms per replay over `reps` (at least 20) replays, each between its
+    own pair of HIP events on the replay stream, after at least `warm_ms` of
+    untimed replays (a single warm-up replay left the first of several
+    back-to-back timings of one kernel up to 10% slow)."""
+    reps = max(reps, 20)
     t0 = time.perf_counter()
     while True:
         graph.replay()
         torch.cuda.synchronize()
         if (time.perf_counter() - t0) * 1e3 >= warm_ms:
             break
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(reps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record()
+    for i in range(reps):
         graph.replay()
-    b.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / reps
+    return float(np.median([ev[i].elapsed_time(ev[i + 1]) for i in range(reps)]))
 
 
 KERNELS = ("embedding_lookup", "fused_add_rmsnorm", "rope_and_write_kv", "silu_and_mul")
@@ -607,7 +609,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="C2")
-    ap.add_argument("--reps", type=int, default=20, help="graph replays per kernel timing")
+    ap.add_argument("--reps", type=int, default=20, help="graph replays per kernel timing (their median is reported; at least 20)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3-C5 per-kernel figures")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention figures")
