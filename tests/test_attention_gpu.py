@@ -60,7 +60,10 @@ REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
              (6, 2, 128, False, [700]), (8, 1, 64, False, [48, 17]),
              (8, 2, 128, True, [33, 280]), (4, 2, 64, True, [520]),
              # G = 8 at D = 128: the largest LDS footprint of either form
-             (8, 1, 128, False, [300, 40]), (8, 1, 128, True, [260])]
+             (8, 1, 128, False, [300, 40]), (8, 1, 128, True, [260]),
+             # G = 5 and 7; sequences ending on a partition boundary
+             (8, 2, 128, True, [256, 512]), (10, 2, 128, False, [256, 1, 513]),
+             (7, 1, 64, True, [768, 255])]
 
 
 @pytest.mark.parametrize("hq,hkv,D,int8,lens", REF_CASES)
