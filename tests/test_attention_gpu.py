@@ -62,8 +62,8 @@ REF_CASES = [(8, 2, 128, False, [37, 300, 5]), (4, 4, 64, False, [64, 129, 1]),
              # G = 8 at D = 128: the largest LDS footprint of either form
              (8, 1, 128, False, [300, 40]), (8, 1, 128, True, [260]),
              # G = 5 and 7; sequences ending on a partition boundary
-             (8, 2, 128, True, [256, 512]), (10, 2, 128, False, [256, 1, 513]),
-             (7, 1, 64, True, [768, 255])]
+             (8, 2, 128, True, [256, 512]), (10, 2, 128, False, [257, 1]),
+             (7, 1, 64, True, [300, 17])]
 
 
 @pytest.mark.parametrize("hq,hkv,D,int8,lens", REF_CASES)
