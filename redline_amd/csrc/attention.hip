@@ -103,9 +103,12 @@ __device__ __forceinline__ float slots_max(float v) {
 
 // ---- one work unit = one (item, kv head, 256-key partition), processed by
 // the 8 waves of a workgroup in stages.  A wave owns kPasses passes of kKPP
-// keys (key j of pass u is (u * kWaves + wave) * kKPP + slot); the K rows of
-// a unit and its V rows are two separate batches of loads, so the persistent
-// form can keep one batch in flight while it computes with the other.
+// keys, 32 consecutive keys in all (key j of pass u is (wave * kPasses + u) *
+// kKPP + slot), so a matrix-core tile of 16 keys lies in one or two 16-key
+// cache blocks and each K load instruction stays inside them (one address
+// translation, few cache lines); the K rows of a unit and its V rows are two
+// separate batches of loads, so the persistent form can keep one batch in
+// flight while it computes with the other.
 
 template <int D>
 struct Geo {
@@ -131,7 +134,7 @@ __device__ __forceinline__ LaneCoord lane_coord() {
 }
 template <int D>
 __device__ __forceinline__ int key_of(const LaneCoord& c, int pass) {
-  return (pass * kWaves + c.wave) * Geo<D>::kKPP + c.slot;
+  return (c.wave * Geo<D>::kPasses + pass) * Geo<D>::kKPP + c.slot;
 }
 
 // The V rows of this thread's keys, in flight.
@@ -179,7 +182,7 @@ __device__ __forceinline__ int mma_pass(int t, int r) {
 }
 template <int D>
 __device__ __forceinline__ int mma_key(const LaneCoord& c, int t, int r) {
-  return (mma_pass<D>(t, r) * kWaves + c.wave) * Geo<D>::kKPP + mma_slot<D>(t, r);
+  return (c.wave * Geo<D>::kPasses + mma_pass<D>(t, r)) * Geo<D>::kKPP + mma_slot<D>(t, r);
 }
 
 // K rows of a unit in the matrix-core layout: per tile, lane (j, r) holds the
