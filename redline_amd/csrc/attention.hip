@@ -211,9 +211,13 @@ __device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* bas
     const int key = mma_key<D>(c, t, r);
     const uint32_t cell = cells[kClamp ? min(key, n - 1) : key];  // cells are >= 0
     const char* row = static_cast<const char*>(base) + 16 * j + static_cast<uint64_t>(cell) * kRowBytes;
+    // Ordinary (temporal) loads: an instruction takes 64 bytes of each of 16
+    // rows, half of a cache line, and the next one takes the other half;
+    // with the streaming hint the second half was fetched again (the V rows,
+    // read as whole lines, keep it).
 #pragma unroll
     for (int x = 0; x < KBatch<D, kInt8>::kLoads; ++x)
-      kb.r[t][x] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 64 * x));
+      kb.r[t][x] = *reinterpret_cast<const u32x4*>(row + 64 * x);
   }
   __builtin_amdgcn_sched_barrier(0);
 }
