@@ -117,17 +117,18 @@ struct Geo {
   static constexpr int kPasses = kPart / (kKPP * kWaves);  // 8 or 4
 };
 
-// This thread's coordinates inside a unit.  The thread index passes through
-// an empty asm (no instruction) so that the lane-dependent address arithmetic
-// is re-derived per unit rather than hoisted out of the persistent loop and
-// kept live across it.
+// This thread's coordinates inside a unit.  With kPin the thread index passes
+// through an empty asm (no instruction), so that the lane-dependent address
+// arithmetic is re-derived per unit rather than hoisted out of the persistent
+// loop and kept live across it: the FP16 form needs the registers (hoisted it
+// spills), the INT8 form has them and saves the instructions.
 struct LaneCoord {
   int tid, wave, slot, e0;
 };
-template <int D>
+template <int D, bool kPin = true>
 __device__ __forceinline__ LaneCoord lane_coord() {
   int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
+  if constexpr (kPin) asm volatile("" : "+v"(tid));
   const int lane = tid % kWave;
   return {tid, __builtin_amdgcn_readfirstlane(tid / kWave), lane / Geo<D>::kLPK,
           (lane % Geo<D>::kLPK) * 8};
@@ -805,7 +806,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   KBatch<D, kInt8> kb;
   RowBatch<D, kInt8> vb;
   {
-    const LaneCoord c = lane_coord<D>();
+    const LaneCoord c = lane_coord<D, !kInt8>();
     issue_keys<D, kInt8, false>(kb, p.kv.k, s.cell[0], keys_in(cur), c);
     issue_rows<D, kInt8, false>(vb, p.kv.v, s.cell[0], keys_in(cur), c);
   }
@@ -813,7 +814,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     const int b = (u - u0) & 1;
     const bool has1 = u + 1 < u1, has2 = u + 2 < u1;
     const UnitPos nn = has2 ? advance(nxt) : nxt;
-    const LaneCoord c = lane_coord<D>();
+    const LaneCoord c = lane_coord<D, !kInt8>();
     // block-table entries of unit n+2 and the q piece of unit n+1, consumed
     // after the first barrier
     const int blk2 = has2 ? table_entry(p, c.tid, it_seq[nn.item], nn.part, keys_in(nn)) : -1;
