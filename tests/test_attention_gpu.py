@@ -72,11 +72,25 @@ def test_decode_attention_reference_geometries(torch_cuda, hq, hkv, D, int8, len
                                                attention_form):
     """Every token of every sequence is a decode item attending to its causal
     prefix, over a cache written by rope_and_write_kv (shuffled blocks)."""
-    torch = torch_cuda
-    from redline_amd import kernels as K
     say(f"attention hq={hq} hkv={hkv} D={D} int8={int8} lens={lens} static={static_parts} "
         f"form={attention_form}")
-    bs = 16
+    _causal_prefix_case(torch_cuda, hq, hkv, D, int8, lens, static_parts, 16)
+
+
+@pytest.mark.parametrize("bs", [8, 32])
+@pytest.mark.parametrize("hq,hkv,D,int8,lens", [(8, 2, 128, False, [300, 17]),
+                                                (8, 2, 128, True, [270]),
+                                                (4, 2, 64, True, [140, 33])])
+def test_decode_attention_other_block_sizes(torch_cuda, hq, hkv, D, int8, lens, bs,
+                                            attention_form):
+    """Cache blocks of 8 and 32 keys (the reference uses 16): a 256-key
+    partition then spans 32 or 8 blocks."""
+    say(f"attention bs={bs} hq={hq} hkv={hkv} D={D} int8={int8} lens={lens} form={attention_form}")
+    _causal_prefix_case(torch_cuda, hq, hkv, D, int8, lens, False, bs)
+
+
+def _causal_prefix_case(torch, hq, hkv, D, int8, lens, static_parts, bs):
+    from redline_amd import kernels as K
     rng = np.random.default_rng(hq * 7 + D + sum(lens))
     S, T, max_len = len(lens), sum(lens), max(lens)
     nblocks = 1 + sum((L + bs - 1) // bs for L in lens)
