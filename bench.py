@@ -298,6 +298,11 @@ SWEEP_KNOBS = {
     "silu_and_mul": {"RLK_TUNE_SWIGLU_BS": [64, 128, 256], "RLK_TUNE_SWIGLU_NT": [0, 1]},
     "rope_and_write_kv": {"RLK_TUNE_ROPE_WPT": [1, 2, 3, 4, 5, 6, 8]},
 }
+# Launch forms of rope_and_write_kv, swept as explicit settings (WPT 0 = the
+# default, waves enough to cover a token's heads in one pass).
+ROPE_FORMS = ([{"RLK_TUNE_ROPE_FORM": 0, "RLK_TUNE_ROPE_WPT": w} for w in (0, 8)] +
+              [{"RLK_TUNE_ROPE_FORM": 1, "RLK_TUNE_ROPE_WPT": w} for w in (0, 3, 2)] +
+              [{"RLK_TUNE_ROPE_FORM": 2, "RLK_TUNE_ROPE_WGS": g} for g in (1, 2, 3, 4, 5, 6, 8)])
 
 
 def sweep(torch, data, reps, only=None):
@@ -310,7 +315,11 @@ def sweep(torch, data, reps, only=None):
         if only and kern != only:
             continue
         names = list(knobs)
-        for vals in itertools.product(*knobs.values()):
+        settings = list(itertools.product(*knobs.values()))
+        if kern == "rope_and_write_kv":
+            names = ["RLK_TUNE_ROPE_FORM", "RLK_TUNE_ROPE_WPT", "RLK_TUNE_ROPE_WGS"]
+            settings = [tuple(f.get(n) or None for n in names) for f in ROPE_FORMS]
+        for vals in settings:
             for n, v in zip(names, vals):
                 set_tune_knob(n, v)
             r = per_kernel(torch, data, reps, kern, names=(kern,), warm=False)[kern]
@@ -661,7 +670,7 @@ def main():
     if args.only == "gemv_w4a16_swiglu" and not args.profile_calls:
         res = []
         for m in (1, 8, 16, 32):
-            for cfg in (range(12) if args.sweep else [None]):
+            for cfg in ((0, 9, 11, 12, 13, 14, 15) if args.sweep else [None]):
                 if cfg is not None:
                     from redline_amd._lib import set_tune_knob
                     set_tune_knob("RLK_TUNE_W4_CFG", cfg)
@@ -685,7 +694,7 @@ def main():
 
     if args.profile_calls:
         fns = kernel_fns(data)
-        for name in KERNELS + STEP_EXTRA:
+        for name in KERNELS + STEP_EXTRA + ("stream_copy",):
             if args.only and args.only not in (name, "elementwise"):
                 continue
             for i in range(args.profile_calls):
@@ -712,37 +721,44 @@ def main():
                           "rotating_input_sets": data.R}))
         return
 
-    def time_steps(step):
-        """K timed steps after W warmup steps: (K // R) replays of a graph
-        holding all R rotating steps plus one graph of the remaining K % R
-        steps (warmup likewise), between HIP events on the launch stream."""
-        full = capture(torch, lambda: [step(r) for r in range(data.R)])
-        part = lambda n: capture(torch, lambda: [step(r) for r in range(n)]) if n else None  # noqa: E731
-        rem, wrem = part(args.steps % data.R), part(args.warmup % data.R)
-        for _ in range(args.warmup // data.R):
+    def time_steps(step, data, steps=None, warmup=None):
+        """K timed steps after W warmup steps, every step on its own rotating
+        input set.  The warm-up takes the last W % R sets of the rotation (and
+        W // R full rotations before them); the timed steps start at set 0 and
+        walk the rotation in order, so no timed step reads a set the warm-up
+        touched less than R - W % R sets earlier (R sets > 2x the Infinity
+        Cache).  Replays of graphs of R (or fewer) steps, between HIP events on
+        the launch stream."""
+        steps = args.steps if steps is None else steps
+        warmup = args.warmup if warmup is None else warmup
+        R = data.R
+        full = capture(torch, lambda: [step(r) for r in range(R)])
+        rem = capture(torch, lambda: [step(r) for r in range(steps % R)]) if steps % R else None
+        wrem = (capture(torch, lambda: [step(r) for r in range(R - warmup % R, R)])
+                if warmup % R else None)
+        for _ in range(warmup // R):
             full.replay()
         if wrem is not None:
             wrem.replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        for _ in range(args.steps // data.R):
+        for _ in range(steps // R):
             full.replay()
         if rem is not None:
             rem.replay()
         end.record()
         torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / args.steps
+        ms = start.elapsed_time(end) / steps
         del full, rem, wrem
         return ms
-
     result = {}
     if args.only is None:
-        ms_step = time_steps(data.step)
+        ms_step = time_steps(data.step, data)
         value = step_bytes / (ms_step * 1e-3) / 1e9
         log(f"{w.key} step (4 launches, embedding_rmsnorm): {ms_step * 1e3:.2f} us, {value:.1f} GB/s")
         result.update(ms_per_step=round(ms_step, 5), value=round(value, 2))
-        ms_plain = time_steps(data.step_plain)
+        ms_plain = time_steps(data.step_plain, data)
         log(f"{w.key} step of the reference's 5 launches: {ms_plain * 1e3:.2f} us, "
             f"{plain_bytes / (ms_plain * 1e-3) / 1e9:.1f} GB/s")
         result["step_plain"] = {"us_per_step": round(ms_plain * 1e3, 3),
@@ -789,7 +805,25 @@ def main():
             wx = make_workload(key)
             log(f"setting up {key} ({wx.model.name}, T={wx.num_tokens})")
             dx = LayerData(torch, K, wx)
-            extra[key] = per_kernel(torch, dx, max(3, args.reps // 4), names=KERNELS + ("stream_copy",))
+            extra[key] = per_kernel(torch, dx, max(3, args.reps // 4),
+                                    names=KERNELS + STEP_EXTRA + ("stream_copy",))
+            if key == "C3":
+                # the layer step at the prefill shape, in both launch orders:
+                # 2 x R steps after R warm-up steps (every set cold)
+                nbx = dx.bytes()
+                for name, fn, nbytes in (
+                        ("step", dx.step, nbx["embedding_rmsnorm"] + nbx["rope_and_write_kv"] +
+                         nbx["fused_add_rmsnorm"] + nbx["silu_and_mul"]),
+                        ("step_plain", dx.step_plain, nbx["embedding_lookup"] +
+                         nbx["fused_add_rmsnorm_nodelta"] + nbx["rope_and_write_kv"] +
+                         nbx["fused_add_rmsnorm"] + nbx["silu_and_mul"])):
+                    ms = time_steps(fn, dx, steps=2 * dx.R * 4, warmup=dx.R)
+                    gbs = nbytes / (ms * 1e-3) / 1e9
+                    extra[key][name] = {"us_per_step": round(ms * 1e3, 3), "gb_per_s": round(gbs, 1),
+                                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                        "bytes_per_step": nbytes}
+                    log(f"  {key} {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s "
+                        f"({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)")
             del dx
             torch.cuda.empty_cache()
 

@@ -62,10 +62,17 @@ const char* rlk_version(void);
 /* Tuning hook (no counterpart in the reference): sets (set != 0) or clears
  * the launch-policy override `name` (one of RLK_TUNE_GATHER_BS, _GATHER_NT,
  * _NORM_TPR, _NORM_NT, _SWIGLU_BS, _SWIGLU_NT, _ROPE_WPT, _ATTN_PERSIST,
- * _W4_CFG, _W8_CFG, _PREFILL_DMA, _PREFILL_QS, _ATTN_PV).  The environment variables of
+ * _W4_CFG, _W8_CFG, _PREFILL_DMA, _PREFILL_QS, _ATTN_PV, _ROPE_FORM,
+ * _ROPE_WGS).  The environment variables of
  * the same names are read once, at the first launch of the process; later
- * changes go through this call only.  Unknown name: RLK_EINVAL. */
+ * changes go through this call only.  Unknown name: RLK_EINVAL.
+ * The knobs are process-wide, not per stream or thread: a change applies to
+ * every later launch from any thread, so change them only while no other
+ * thread launches (tuning runs and tests). */
 int rlk_set_tune_knob(const char* name, int value, int set);
+/* Reads the override `name`: *is_set = 1 and *value = its value when set,
+ * else *is_set = 0 and *value = 0.  Unknown name or null output: RLK_EINVAL. */
+int rlk_get_tune_knob(const char* name, int* value, int* is_set);
 
 /* ------------------------------------------------------------ elementwise */
 
@@ -88,7 +95,10 @@ int rlk_fused_add_rmsnorm(uint16_t* residual, const uint16_t* delta, const uint1
  * n, hidden, residual) and fused_add_rmsnorm(residual, NULL, weight, n,
  * hidden, eps, out) that start its forward pass (src/cuda/model/llama.cpp:79-80),
  * with one launch and one pass over the rows instead of two.
- * n <= 0: no-op.  hidden % 8 != 0: RLK_EINVAL.  ids are not bounds-checked. */
+ * n <= 0: no-op.  hidden % 8 != 0: RLK_EINVAL.  ids are not bounds-checked.
+ * table, weight, residual and out are read and written as 16-byte vectors:
+ * each must be 16-byte aligned (else RLK_EINVAL), and residual and out must
+ * not overlap each other or the table. */
 int rlk_embedding_rmsnorm(const int32_t* ids, const uint16_t* table, int n, int hidden,
                           const uint16_t* weight, float eps, uint16_t* residual, uint16_t* out,
                           hipStream_t stream);
@@ -248,9 +258,11 @@ int rlk_paged_attention_decode(const rlk_attention_params* params,
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): rlk_paged_attention_decode with the split-K partials in a
- * library-owned device array of RLK_DECODE_SCRATCH_BYTES per GPU (held until
- * the process ends) instead of work->ws_out / ws_max / ws_sum, which are
- * ignored.  Allocates nothing.  Needs num_items * num_heads * max_partitions *
+ * library-owned device array of RLK_DECODE_SCRATCH_BYTES per GPU instead of
+ * work->ws_out / ws_max / ws_sum, which are ignored.  The array is a static
+ * device variable: it is reserved (32 MiB of HBM) on every GPU the library's
+ * code object is loaded on, whether or not this entry point is ever called,
+ * and is held until the process ends.  max_partitions == 1 uses no scratch.  Allocates nothing.  Needs num_items * num_heads * max_partitions *
  * (head_dim + 2) * 4 bytes (each of the three regions rounded up to 256);
  * more than RLK_DECODE_SCRATCH_BYTES: RLK_EINVAL.  Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or

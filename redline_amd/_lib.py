@@ -107,6 +107,7 @@ _SIGNATURES = {
     "rlk_last_error": (C.c_char_p, []),
     "rlk_version": (C.c_char_p, []),
     "rlk_set_tune_knob": (_I, [C.c_char_p, _I, _I]),
+    "rlk_get_tune_knob": (_I, [C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "rlk_embedding_lookup": (_I, [_P, _P, _I, _I, _P, _P]),
     "rlk_fused_add_rmsnorm": (_I, [_P, _P, _P, _I, _I, C.c_float, _P, _P]),
     "rlk_embedding_rmsnorm": (_I, [_P, _P, _I, _I, _P, C.c_float, _P, _P, _P]),
@@ -177,18 +178,29 @@ def set_tune_knob(name: str, value: int | None) -> None:
                                   0 if value is None else 1))
 
 
+def get_tune_knob(name: str) -> int | None:
+    """The current value of launch-policy override `name`, None when unset."""
+    value, is_set = C.c_int(0), C.c_int(0)
+    check(lib().rlk_get_tune_knob(name.encode(), C.byref(value), C.byref(is_set)))
+    return value.value if is_set.value else None
+
+
 class tune_knob:
-    """Context manager: the knob set to `value` inside the block, cleared after."""
+    """Context manager: the knob set to `value` inside the block, restored to
+    its previous value (or cleared, if it was unset) after.  Knobs are
+    process-wide: use it only while no other thread launches kernels."""
 
     def __init__(self, name: str, value: int | None):
         self.name, self.value = name, value
+        self.prev = None
 
     def __enter__(self):
+        self.prev = get_tune_knob(self.name)
         set_tune_knob(self.name, self.value)
         return self
 
     def __exit__(self, *exc):
-        set_tune_knob(self.name, None)
+        set_tune_knob(self.name, self.prev)
         return False
 
 

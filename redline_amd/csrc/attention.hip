@@ -1127,6 +1127,15 @@ extern "C" int rlk_paged_attention_decode_noalloc(const rlk_attention_params* p,
   if (w->max_partitions < 1 || p->num_heads <= 0 || p->kv.head_dim <= 0)
     return fail(RLK_EINVAL, "paged_attention_decode_noalloc: bad max_partitions %d, num_heads %d "
                             "or head_dim %d", w->max_partitions, p->num_heads, p->kv.head_dim);
+  // One partition: the kernel writes the output rows directly and reads no
+  // split-K scratch, so the array is not resolved at all.
+  if (w->max_partitions == 1) {
+    rlk_decode_attention_work ws = *w;
+    ws.ws_out = nullptr;
+    ws.ws_max = nullptr;
+    ws.ws_sum = nullptr;
+    return attention_launch(p, &ws, 0, stream);
+  }
   // partials [items, heads, partitions, D] then max and sum [items, heads,
   // partitions], each region 256-byte aligned; no zeroing is needed (every
   // partition a merge reads is written first by the same call)

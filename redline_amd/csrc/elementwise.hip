@@ -427,6 +427,9 @@ extern "C" int rlk_embedding_rmsnorm(const int32_t* ids, const uint16_t* table, 
   if (ids == nullptr || table == nullptr || weight == nullptr || residual == nullptr ||
       out == nullptr)
     return fail(RLK_EINVAL, "embedding_rmsnorm: null pointer argument");
+  if (((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(weight) |
+        reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+    return fail(RLK_EINVAL, "embedding_rmsnorm: table, weight, residual and out must be 16-byte aligned");
   NormArgs a;
   a.res = reinterpret_cast<u32x4*>(residual);
   a.del = reinterpret_cast<const u32x4*>(table);

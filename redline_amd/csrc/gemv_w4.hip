@@ -503,6 +503,33 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
         a.x + static_cast<size_t>(r) * a.k + static_cast<size_t>(qa) * kKP + e * 8,
         x_lds + r * a.xstride + e * 8);
   };
+  // INT4: sum(x) over each 128-K chunk of the pass and each activation row,
+  // [chunk][16 MT rows] in fp32 after x, taken while x is staged.  Vector v
+  // of the pass holds K [8e, 8e + 8) of row r (v = r * per + e), and the 16
+  // vectors of one (row, chunk) sit in 16 consecutive lanes of one aligned
+  // group (v = tid + multiples of the block size, per a multiple of 16), so
+  // one 16-lane DPP sum gives the chunk's sum.  Every wave reads these sums
+  // instead of computing them with MFMAs against a ones operand.
+  constexpr int kMP = 16 * MT;
+  float* xsum_lds = reinterpret_cast<float*>(x_lds + static_cast<size_t>(a.m) * a.xstride);
+  auto x_put = [&](int v, int qa, int xvecs, u32x4 raw) {
+    const auto pr = x_addr(v, qa, xvecs);
+    const f16x8 h = xcvt(raw);
+    *reinterpret_cast<f16x8*>(pr.second) = h;
+    if constexpr (!kW8) {
+      const f16x2 one = {static_cast<_Float16>(1), static_cast<_Float16>(1)};
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sum = __builtin_amdgcn_fdot2(f16x2{h[2 * j], h[2 * j + 1]}, one, sum, false);
+      sum = group_sum<16>(sum);
+      if ((lane & 15) == 0 && v < xvecs) {
+        const int per = min(kpass, a.k - qa * kKP) / 8;
+        const int r = quot(v, 1.0f / static_cast<float>(per)), e = v - r * per;
+        xsum_lds[(e >> 4) * kMP + r] = sum;
+      }
+    }
+  };
   auto stage_x_rest = [&](int qa, int v_from) {  // in batches of 8 loads per thread
     const int xvecs = a.m * (min(kpass, a.k - qa * kKP) / 8);
     for (int v0 = v_from; v0 < xvecs; v0 += 8 * threads) {
@@ -510,8 +537,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
 #pragma unroll
       for (int u = 0; u < 8; ++u) val[u] = load16(x_addr(v0 + u * threads, qa, xvecs).first);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        *reinterpret_cast<f16x8*>(x_addr(v0 + u * threads, qa, xvecs).second) = xcvt(val[u]);
+      for (int u = 0; u < 8; ++u) x_put(v0 + u * threads, qa, xvecs, val[u]);
     }
   };
   // INT8: zeros from k to the end of the last pair (LDS stores only)
@@ -566,10 +592,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
 #pragma unroll
     for (int p = 0; p < P; ++p) fetch(p, min(p, lastp));
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const auto pr = x_addr(tid + u * threads, 0, xvecs);
-      *reinterpret_cast<f16x8*>(pr.second) = xcvt(xv[u]);
-    }
+    for (int u = 0; u < NB; ++u) x_put(tid + u * threads, 0, xvecs, xv[u]);
     zero_x_tail(0, min(a.cpp, npairs));
     if (svec) {
       if (qd < gn / 8) so_put(gv0 * 8, s4, o4);
@@ -587,7 +610,6 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  constexpr f16x8 kOnes = {1, 1, 1, 1, 1, 1, 1, 1};
   const uint32_t magic = opaque(0x54005400u);
 
   // one 128-K chunk: c = chunk index within the pass
@@ -608,13 +630,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
     f16x8 xa[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      xs[mt] = *reinterpret_cast<const f32x4*>(xsum_lds + c * kMP + 16 * mt + 4 * qd);
       d[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xa[mt][j] = *reinterpret_cast<const f16x8*>(xl[mt] + c * 128 + 8 * j);
-        xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], kOnes, xs[mt], 0, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j) xa[mt][j] = *reinterpret_cast<const f16x8*>(xl[mt] + c * 128 + 8 * j);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -715,6 +734,181 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
   for (int mt = 0; mt < MT; ++mt) store_tile<MODE>(a, acc[mt], 16 * mt + 4 * qd, row, r16);
 }
 
+// The K-slice kernel: the default for INT4 weights whose K is 8 or fewer
+// slices of CPW 128-K chunks (the Llama-3.1-8B gate_up: 8 slices of 512 K)
+// and whose rows are whole 16-row tiles.  A workgroup owns T consecutive
+// 16-row tiles; wave w owns K slice w (chunks w CPW .. w CPW + CPW - 1) of
+// every one of them.  So each wave needs only its own slice of x, which it
+// loads once, straight into the MFMA A-operand layout in registers (no x in
+// LDS: no staging pass, no per-chunk LDS reads of x, no bank conflicts), and
+// computes that slice's per-chunk sum(x) once with MFMAs against a ones
+// operand, for all of its tiles.  The wave then walks its tiles, fetching
+// each tile's slice as chunk pairs of full cache lines (the pair kernel's
+// loads and DPP hand-over) through a ring of U tiles' pairs, and leaves one
+// partial 16x16 result per tile in LDS; after one barrier, wave w adds the
+// nw partials of tile w (w + nw, ...) in slice order -- a fixed order, so the
+// result is deterministic -- and stores it through the epilogue.  Scales and
+// offsets of the workgroup's rows are staged once into LDS (coalesced:
+// [n, groups] is contiguous over the workgroup's rows).
+// Waves per workgroup of the K-slice kernel: 16 when a slice's x fits in
+// half the registers (two 128-K chunks of one activation tile), else 8.
+template <int CPW, int MT>
+constexpr int kslice_max_waves() { return CPW * MT <= 2 ? 16 : kMaxWaves; }
+
+template <int CPW, int U, int MT, int MODE>
+__global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_kslice_kernel(W4Args a) {
+  constexpr int kPPT = CPW / 2;  // chunk pairs per tile and wave
+  constexpr int P = kPPT * U;    // ring depth in pairs: U tiles
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int threads = blockDim.x, nw = threads / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, qd = lane >> 4;
+  const bool low = (lane & 8) == 0;
+  const int T = a.cpp;  // tiles per workgroup, a multiple of U
+  const int ntiles = a.n / 16;
+  const int tile0 = blockIdx.x * T;
+  const int sstride = a.groups + 1;  // odd: the 16 rows' reads of one group fall in 16 banks
+  uint32_t* so_lds = reinterpret_cast<uint32_t*>(lds);   // [16 T rows][groups + 1]: s | o << 16
+  f32x4* red = reinterpret_cast<f32x4*>(lds + a.slab_off);  // [T][nw][MT][64 lanes]
+  const int kb = a.k / 2;
+  const int c0 = wave * CPW;  // first chunk of this wave's slice
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.w), 0, static_cast<int>(static_cast<uint32_t>(a.n) * static_cast<uint32_t>(kb)),
+      kBufferFlags);
+  const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, 0, kBufferFlags);
+  // pair loads as in the pair kernel: instruction 0 covers rows 0..7 of the
+  // tile (full 128-byte lines), instruction 1 rows 8..15
+  const int pc0 = (low ? qd : 4 + qd) * 16, pc1 = (low ? 4 + qd : qd) * 16;
+  const int vo0 = (low ? r16 : r16 - 8) * kb + pc0;
+  const int vo1 = (low ? r16 + 8 : r16) * kb + pc1;
+  const int nq = T * kPPT;  // (tile, pair) steps of this wave
+  u32x4 ring[P][2];
+  // step q: local tile q / kPPT, pair q % kPPT of the slice; tiles past the
+  // last one (and steps past the end) read nothing
+  auto fetch = [&](int s, int q) {
+    const int t = tile0 + q / kPPT;
+    const __amdgpu_buffer_rsrc_t res = (q < nq && t < ntiles) ? wres : none;
+    const int soff = t * 16 * kb + (c0 / 2 + q % kPPT) * 128;
+    ring[s][0] = __builtin_amdgcn_raw_buffer_load_b128(res, vo0, soff, kNtLoad);
+    ring[s][1] = __builtin_amdgcn_raw_buffer_load_b128(res, vo1, soff, kNtLoad);
+  };
+
+  // x of this wave's slice in the A-operand layout: lane (qd, r16) holds
+  // row min(16 mt + r16, m - 1), K (c0 + c) 128 + 32 qd + 8 j .. + 7,
+  // permuted to the codes' nibble order
+  f16x8 xa[CPW][MT][4];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xa[c][mt][j] = x_perm(load16(a.x + static_cast<size_t>(min(16 * mt + r16, a.m - 1)) * a.k +
+                                     (c0 + c) * 128 + qd * 32 + 8 * j));
+  // scales and offsets of the workgroup's rows, requested before the ring
+  constexpr int kSoBatch = 8;
+  const int staged = 16 * T * a.groups;
+  const float inv_groups = 1.0f / static_cast<float>(a.groups);
+  const size_t so_base = static_cast<size_t>(tile0) * 16 * a.groups;
+  const size_t so_last = static_cast<size_t>(a.n) * a.groups - 1;
+  uint32_t sov[kSoBatch];
+  auto so_load = [&](int i0) {
+#pragma unroll
+    for (int u = 0; u < kSoBatch; ++u) {
+      const size_t src = min(so_base + min(i0 + u * threads, staged - 1), so_last);
+      sov[u] = a.scales[src] | (static_cast<uint32_t>(a.offsets[src]) << 16);
+    }
+  };
+  auto so_store = [&](int i0) {
+#pragma unroll
+    for (int u = 0; u < kSoBatch; ++u) {  // past the end: the last entry again, same value
+      const int i = min(i0 + u * threads, staged - 1);
+      const int r = quot(i, inv_groups), g = i - r * a.groups;
+      so_lds[r * sstride + g] = sov[u];
+    }
+  };
+  so_load(tid);
+#pragma unroll
+  for (int p = 0; p < P; ++p) fetch(p, p);
+  so_store(tid);
+  for (int i0 = tid + threads * kSoBatch; i0 < staged; i0 += threads * kSoBatch) {
+    so_load(i0);
+    so_store(i0);
+  }
+  // sum(x) per chunk of the slice and activation row (all 16 columns equal)
+  constexpr f16x8 kOnes = {1, 1, 1, 1, 1, 1, 1, 1};
+  f32x4 xs[CPW][MT];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      xs[c][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xs[c][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c][mt][j], kOnes, xs[c][mt], 0, 0, 0);
+    }
+  const uint32_t magic = opaque(0x54005400u);
+  __syncthreads();  // scales and offsets staged
+
+  for (int qb = 0; qb < nq; qb += P) {  // U tiles per round (wave-uniform)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = qb / kPPT + u;  // local tile
+      f32x4 acc[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint32_t* so_row = so_lds + (t * 16 + r16) * sstride;
+#pragma unroll
+      for (int p = 0; p < kPPT; ++p) {
+        const int s = u * kPPT + p;
+        u32x4 words[2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          words[0][e] = low ? ring[s][0][e] : ring[s][1][e];
+          words[1][e] = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(
+              static_cast<int>(low ? ring[s][1][e] : ring[s][0][e]), 0x128, 0xF, 0xF, false));  // row_ror:8
+        }
+        fetch(s, qb + s + P);
+        __builtin_amdgcn_sched_barrier(0x78F);  // only vector-memory instructions stay put
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int c = 2 * p + h;
+          const uint32_t so = so_row[(c0 + c) >> a.gq_shift];
+          const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
+          const float of = fmaf(-kCodeBias, sc,
+                                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16))));
+          f32x4 d[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) d[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const f16x8 q = codes_f16(words[h][j], magic);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              d[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c][mt][j], q, d[mt], 0, 0, 0);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(of, xs[c][mt][e], fmaf(sc, d[mt][e], acc[mt][e]));
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((t * nw + wave) * MT + mt) * kWave + lane] = acc[mt];
+    }
+  }
+  __syncthreads();  // every slice's partial of every tile is in LDS
+  for (int t = wave; t < T; t += nw) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 sum = red[((t * nw) * MT + mt) * kWave + lane];
+      for (int w = 1; w < nw; ++w) sum += red[((t * nw + w) * MT + mt) * kWave + lane];
+      store_tile<MODE>(a, sum, 16 * mt + 4 * qd, (tile0 + t) * 16 + r16, r16);
+    }
+  }
+}
+
 // LDS a workgroup may take: the device allows 160 KiB per workgroup.
 constexpr size_t kLdsBudget = 160 * 1024;
 constexpr int kNoFit = 1;  // launch(): the policy's smallest x pass exceeds the LDS budget
@@ -772,10 +966,11 @@ int launch_pairs(W4Args a, hipStream_t stream) {
   const int tiles = (a.n + 15) / 16;
   const int cus = compute_units();
   const int nw = std::max(1, std::min(kMaxWaves, (tiles + cus - 1) / cus));
-  auto lds_for = [&](int cpp) {
+  auto lds_for = [&](int cpp) {  // scales and offsets, x, and (INT4) the chunk sums of x
     const size_t gpp = kW8 ? 0 : static_cast<size_t>(cpp) * 2 / gq;
     return static_cast<size_t>(nw) * 16 * (gpp + 1) * 4 +
-           static_cast<size_t>(a.m) * (static_cast<size_t>(cpp) * kKP + 8) * 2;
+           static_cast<size_t>(a.m) * (static_cast<size_t>(cpp) * kKP + 8) * 2 +
+           (kW8 ? 0 : static_cast<size_t>(cpp) * 2 * 16 * MT * 4);
   };
   int cpp = (npairs + unit - 1) / unit * unit;
   while (cpp > unit && lds_for(cpp) > kLdsBudget) cpp -= unit;
@@ -812,10 +1007,48 @@ int launch_pairs(W4Args a, hipStream_t stream) {
   return go(gemv_w4_pairs_kernel<P, MT, MODE, 24, false, kW8>);  // the rest in a loop
 }
 
+// The K-slice kernel's launch: nw = nchunks / CPW waves (at most 8 or 16), T tiles
+// per workgroup -- about one workgroup per compute unit, fewer when the
+// partials of T tiles would not fit the LDS budget.
+template <int CPW, int U, int MT, int MODE>
+int launch_kslice(W4Args a, hipStream_t stream) {
+  const int gq = a.group_size / 128;
+  if (a.group_size % 128 != 0 || (gq & (gq - 1)) != 0 || a.n % 16 != 0 ||
+      a.nchunks % CPW != 0 || a.nchunks / CPW > kslice_max_waves<CPW, MT>())
+    return kNoFit;
+  if (static_cast<uint64_t>(a.n) * static_cast<uint64_t>(a.k / 2) > kMaxBufferBytes) return kNoFit;
+  a.gq_shift = __builtin_ctz(gq);
+  const int nw = a.nchunks / CPW;
+  const int ntiles = a.n / 16;
+  const int cus = compute_units();
+  auto lds_for = [&](int t) {
+    const size_t so = (static_cast<size_t>(16) * t * (a.groups + 1) * 4 + 15) / 16 * 16;
+    return so + static_cast<size_t>(t) * nw * MT * kWave * sizeof(f32x4);
+  };
+  int T = (ntiles + cus - 1) / cus;
+  T = (T + U - 1) / U * U;
+  while (T > U && lds_for(T) > kLdsBudget) T -= U;
+  if (lds_for(T) > kLdsBudget) return kNoFit;
+  a.cpp = T;
+  a.slab_off = static_cast<int>((static_cast<size_t>(16) * T * (a.groups + 1) * 4 + 15) / 16 * 16);
+  const size_t lds = lds_for(T);
+  auto kernel = gemv_w4_kslice_kernel<CPW, U, MT, MODE>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = grant_dynamic_lds(reinterpret_cast<const void*>(kernel), kLdsBudget);
+    if (e != hipSuccess)
+      return fail(RLK_EUNSUPPORTED, "gemv_w4a16: %zu bytes of LDS refused (%s)", lds,
+                  hipGetErrorString(e));
+  }
+  kernel<<<(ntiles + T - 1) / T, 64 * nw, lds, stream>>>(a);
+  return RLK_OK;
+}
+
 // Launch policies, selectable for tuning sweeps through RLK_TUNE_W4_CFG.
 // Entry 0, the default, is the pair kernel with 4 pairs in flight per wave up
-// to m = 8 and 2 above; 9, 10 and 11 are the pair kernel with 2, 8 and 4
-// pairs at every m; 8 is the slab kernel with 8
+// to m = 8 and 2 up to m = 16, and the K-slice kernel (4 chunks per slice, one
+// tile's pairs in flight) above; 9, 10 and 11 are the pair kernel with 2, 8
+// and 4 pairs at every m; 12-15 the K-slice kernel with (chunks per slice,
+// tiles in flight) = (4, 1), (4, 2), (2, 2), (2, 4); 8 is the slab kernel with 8
 // chunk pairs in flight; 1-7 are slab-kernel variants (K-split ways, slots in
 // flight per wave, most row waves per workgroup, chunks per slot).  Shapes the
 // pair kernel does not take (an odd chunk count, group_size / 128 not a power
@@ -829,6 +1062,10 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
       case 9: st = launch_pairs<2, MT, MODE>(a, s); break;
       case 10: st = launch_pairs<8, MT, MODE>(a, s); break;
       case 11: st = launch_pairs<4, MT, MODE>(a, s); break;
+      case 12: st = launch_kslice<4, 1, MT, MODE>(a, s); break;
+      case 13: st = launch_kslice<4, 2, MT, MODE>(a, s); break;
+      case 14: st = launch_kslice<2, 2, MT, MODE>(a, s); break;
+      case 15: st = launch_kslice<2, 4, MT, MODE>(a, s); break;
       case 1: st = launch<1, 8, KC, MT, MODE>(a, 8, s); break;
       case 2: st = launch<1, 4, KC, MT, MODE, 2>(a, 8, s); break;
       case 3: st = launch<1, 6, KC, MT, MODE, 2>(a, 8, s); break;
@@ -836,8 +1073,14 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
       case 5: st = launch<1, 12, KC, MT, MODE>(a, 8, s); break;
       case 6: st = launch<1, 8, KC, MT, MODE, 2>(a, 4, s); break;
       case 7: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
-      default:  // measured at the Llama-3.1-8B gate_up shape: 4 pairs in flight up to m = 8, 2 above
-        st = a.m <= 8 ? launch_pairs<4, MT, MODE>(a, s) : launch_pairs<2, MT, MODE>(a, s);
+      default:
+        // measured at the Llama-3.1-8B gate_up shape: the pair kernel with 4
+        // pairs in flight up to m = 8 and 2 up to m = 16; the K-slice kernel
+        // above m = 16 (two activation tiles), where staging x per workgroup
+        // and reading it back from LDS per chunk cost the most
+        if (a.m > 16) st = launch_kslice<4, 1, MT, MODE>(a, s);
+        if (st == kNoFit)
+          st = a.m <= 8 ? launch_pairs<4, MT, MODE>(a, s) : launch_pairs<2, MT, MODE>(a, s);
         break;
     }
     if (st == kNoFit) st = launch<1, 8, KC, MT, MODE, 2>(a, 8, s);

@@ -22,6 +22,7 @@
 // deterministic function of the inputs.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "device.hpp"
@@ -49,16 +50,109 @@ struct RopeArgs {
   int block_size;
 };
 
-template <int D, bool kInt8, int WPT>
-__global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
+// Token-level metadata of one row: the cell coordinates of its KV slot and
+// the lane's 8 cos / sin values (two float4 of each).
+template <int D>
+struct TokenMeta {
+  f32x8 c, s;
+  int slot, blk, off;
+};
+
+template <int D>
+__device__ __forceinline__ TokenMeta<D> token_meta(const RopeArgs& a, int pos, int slot, int p0) {
+  constexpr int kHalf = D / 2;
+  TokenMeta<D> m;
+  const float* cp = a.cos_t + static_cast<int64_t>(pos) * kHalf + p0;
+  const float* sp = a.sin_t + static_cast<int64_t>(pos) * kHalf + p0;
+  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp), c1 = *reinterpret_cast<const f32x4*>(cp + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+  m.c = f32x8{c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  m.s = f32x8{s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  m.slot = slot;
+  m.blk = 0;
+  m.off = 0;
+  if (slot >= 0) {
+    m.blk = slot / a.block_size;
+    m.off = slot - m.blk * a.block_size;
+  }
+  return m;
+}
+
+// One head h of a token row: the lane's 8 pairs (v0 = elements p0..p0+7,
+// v1 = the partners D/2 later) are biased, rotated (q, k) and stored back in
+// place (q) or into the KV cell of the token's slot (k, v; FP16 or INT8 with
+// the per-(token, head) scale).  Every lane of the head's group calls it.
+template <int D, bool kInt8>
+__device__ __forceinline__ void rope_head(const RopeArgs& a, _Float16* hp, int h, int p0,
+                                          u32x4 v0, u32x4 v1, const TokenMeta<D>& m) {
 #pragma clang fp contract(off)
   constexpr bool NT = true;  // streaming accesses: measured faster at every batch size
   constexpr int kHalf = D / 2;
+  constexpr int kLPH = kHalf / 8;
+  f32x8 x0 = unpack8(v0);
+  f32x8 x1 = unpack8(v1);
+  if (a.bias != nullptr) {  // extension: QKV bias, fp16-rounded sum
+    x0 = round_f16(x0 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + p0)));
+    x1 = round_f16(x1 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0)));
+  }
+  if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
+    const f32x8 y0 = x0 * m.c - x1 * m.s;
+    const f32x8 y1 = x1 * m.c + x0 * m.s;
+    x0 = round_f16(y0);
+    x1 = round_f16(y1);
+  }
+  if (h < a.hq) {  // query: back in place
+    st16<NT>(reinterpret_cast<u32x4*>(hp + p0), pack8(x0));
+    st16<NT>(reinterpret_cast<u32x4*>(hp + kHalf + p0), pack8(x1));
+    return;
+  }
+  if (m.slot < 0) return;
+  const bool is_v = h >= a.hq + a.hkv;
+  const int kvh = is_v ? h - a.hq - a.hkv : h - a.hq;
+  const int64_t cell = (static_cast<int64_t>(m.blk) * a.hkv + kvh) * a.block_size + m.off;
+  if constexpr (!kInt8) {
+    _Float16* dst = static_cast<_Float16*>(is_v ? a.v : a.k) + cell * D;
+    st16<NT>(reinterpret_cast<u32x4*>(dst + p0), pack8(x0));
+    st16<NT>(reinterpret_cast<u32x4*>(dst + kHalf + p0), pack8(x1));
+  } else {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fmaxf(__builtin_fabsf(x0[j]), __builtin_fabsf(x1[j])));
+    amax = group_max<kLPH>(amax);
+    float scale = amax > 0.f ? amax / 127.f : 1.f;
+    if (a.scale16) scale = round_f16(scale);  // extension: quantise against the stored fp16 scale
+    const float inv = 1.f / scale;
+    i8x8 q0, q1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      q0[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x0[j] * inv, -127.f), 127.f)));
+      q1[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x1[j] * inv, -127.f), 127.f)));
+    }
+    int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
+    st8<NT>(reinterpret_cast<u32x2*>(dst + p0), __builtin_bit_cast(u32x2, q0));
+    st8<NT>(reinterpret_cast<u32x2*>(dst + kHalf + p0), __builtin_bit_cast(u32x2, q1));
+    if (p0 == 0) {
+      void* sp = is_v ? a.v_scale : a.k_scale;
+      if (a.scale16) {
+        static_cast<_Float16*>(sp)[cell] = static_cast<_Float16>(scale);
+      } else {
+        static_cast<float*>(sp)[cell] = scale;
+      }
+    }
+  }
+}
+
+// The heads of token t that wave `wave` of `nwaves` covers: head group hg =
+// wave * heads_per_wave + lane / LPH, then every nwaves * heads_per_wave-th
+// head after it.
+template <int D, bool kInt8>
+__device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t t, int wave, int nwaves,
+                                           int lane) {
+  constexpr bool NT = true;
+  constexpr int kHalf = D / 2;
   constexpr int kLPH = kHalf / 8;            // lanes per head
   constexpr int kHeadsPerWave = kWave / kLPH;
-  constexpr int kGroups = kHeadsPerWave * WPT;  // heads of one token in flight
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t t = blockIdx.x;  // one token per workgroup of WPT waves
+  const int groups = kHeadsPerWave * nwaves;  // heads of one token in flight
   const int hg = wave * kHeadsPerWave + lane / kLPH;
   const int p0 = (lane % kLPH) * 8;  // first pair index owned by this lane
   const int heads = a.hq + 2 * a.hkv;
@@ -71,83 +165,103 @@ __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
     v0 = ld16<NT>(reinterpret_cast<const u32x4*>(row + hg * D + p0));
     v1 = ld16<NT>(reinterpret_cast<const u32x4*>(row + hg * D + kHalf + p0));
   }
-  const int pos = a.positions[t];
-  const int slot = a.slots[t];
-
-  const float* cp = a.cos_t + static_cast<int64_t>(pos) * kHalf + p0;
-  const float* sp = a.sin_t + static_cast<int64_t>(pos) * kHalf + p0;
-  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp), c1 = *reinterpret_cast<const f32x4*>(cp + 4);
-  const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
-  const f32x8 c = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-  const f32x8 s = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-
-  int blk = 0, off = 0;
-  if (slot >= 0) {
-    blk = slot / a.block_size;
-    off = slot - blk * a.block_size;
-  }
-  for (int h = hg; h < heads; h += kGroups) {  // all lanes of a head share h
+  const TokenMeta<D> m = token_meta<D>(a, a.positions[t], a.slots[t], p0);
+  for (int h = hg; h < heads; h += groups) {  // all lanes of a head share h
     _Float16* hp = row + h * D;
     if (h != hg) {
       v0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
       v1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
     }
-    f32x8 x0 = unpack8(v0);
-    f32x8 x1 = unpack8(v1);
-    if (a.bias != nullptr) {  // extension: QKV bias, fp16-rounded sum
-      x0 = round_f16(x0 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + p0)));
-      x1 = round_f16(x1 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0)));
-    }
-    if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
-      const f32x8 y0 = x0 * c - x1 * s;
-      const f32x8 y1 = x1 * c + x0 * s;
-      x0 = round_f16(y0);
-      x1 = round_f16(y1);
-    }
-    if (h < a.hq) {  // query: back in place
-      st16<NT>(reinterpret_cast<u32x4*>(hp + p0), pack8(x0));
-      st16<NT>(reinterpret_cast<u32x4*>(hp + kHalf + p0), pack8(x1));
-      continue;
-    }
-    if (slot < 0) continue;
-    const bool is_v = h >= a.hq + a.hkv;
-    const int kvh = is_v ? h - a.hq - a.hkv : h - a.hq;
-    const int64_t cell = (static_cast<int64_t>(blk) * a.hkv + kvh) * a.block_size + off;
-    if constexpr (!kInt8) {
-      _Float16* dst = static_cast<_Float16*>(is_v ? a.v : a.k) + cell * D;
-      st16<NT>(reinterpret_cast<u32x4*>(dst + p0), pack8(x0));
-      st16<NT>(reinterpret_cast<u32x4*>(dst + kHalf + p0), pack8(x1));
-    } else {
-      float amax = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fmaxf(__builtin_fabsf(x0[j]), __builtin_fabsf(x1[j])));
-      amax = group_max<kLPH>(amax);
-      float scale = amax > 0.f ? amax / 127.f : 1.f;
-      if (a.scale16) scale = round_f16(scale);  // extension: quantise against the stored fp16 scale
-      const float inv = 1.f / scale;
-      i8x8 q0, q1;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        q0[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x0[j] * inv, -127.f), 127.f)));
-        q1[j] = static_cast<int8_t>(__builtin_rintf(fminf(fmaxf(x1[j] * inv, -127.f), 127.f)));
+    rope_head<D, kInt8>(a, hp, h, p0, v0, v1, m);
+  }
+}
+
+// Form 0: one token per workgroup of WPT waves.
+template <int D, bool kInt8, int WPT>
+__global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
+  rope_token<D, kInt8>(a, blockIdx.x, threadIdx.x / kWave, WPT, threadIdx.x % kWave);
+}
+
+// Form 1: one wave per workgroup; workgroup b is wave b % nwaves of token
+// b / nwaves.
+template <int D, bool kInt8>
+__global__ __launch_bounds__(kWave) void rope_kv_wave_kernel(RopeArgs a, int nwaves) {
+  const int64_t t = blockIdx.x / nwaves;
+  rope_token<D, kInt8>(a, t, blockIdx.x - t * nwaves, nwaves, threadIdx.x);
+}
+
+// Form 2: a grid of workgroups of WPT waves that together cover every head
+// of a token (heads <= WPT * heads_per_wave) walks the tokens with a stride
+// of the grid, two-stage pipelined: the next token's activations, position
+// and slot are requested before the current token is rotated and stored.
+template <int D, bool kInt8, int WPT>
+__global__ __launch_bounds__(kWave * WPT) void rope_kv_stream_kernel(RopeArgs a) {
+  constexpr bool NT = true;
+  constexpr int kHalf = D / 2;
+  constexpr int kLPH = kHalf / 8;
+  constexpr int kHeadsPerWave = kWave / kLPH;
+  const int lane = threadIdx.x % kWave;
+  const int h = (threadIdx.x / kWave) * kHeadsPerWave + lane / kLPH;
+  const int p0 = (lane % kLPH) * 8;
+  const int heads = a.hq + 2 * a.hkv;
+  const bool active = h < heads;
+  const int64_t row_elems = static_cast<int64_t>(heads) * D;
+  int64_t t = blockIdx.x;
+  if (t >= a.num_tokens) return;
+  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+  if (active) {
+    const _Float16* hp = a.qkv + t * row_elems + h * D;
+    v0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
+    v1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
+  }
+  int pos = a.positions[t], slot = a.slots[t];
+  for (;;) {
+    const int64_t tn = t + gridDim.x;
+    const bool more = tn < a.num_tokens;  // uniform over the workgroup
+    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
+    int npos = 0, nslot = -1;
+    if (more) {
+      if (active) {
+        const _Float16* hp = a.qkv + tn * row_elems + h * D;
+        n0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
+        n1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
       }
-      int8_t* dst = static_cast<int8_t*>(is_v ? a.v : a.k) + cell * D;
-      st8<NT>(reinterpret_cast<u32x2*>(dst + p0), __builtin_bit_cast(u32x2, q0));
-      st8<NT>(reinterpret_cast<u32x2*>(dst + kHalf + p0), __builtin_bit_cast(u32x2, q1));
-      if (p0 == 0) {
-        void* sp = is_v ? a.v_scale : a.k_scale;
-        if (a.scale16) {
-          static_cast<_Float16*>(sp)[cell] = static_cast<_Float16>(scale);
-        } else {
-          static_cast<float*>(sp)[cell] = scale;
-        }
-      }
+      npos = a.positions[tn];
+      nslot = a.slots[tn];
     }
+    if (active) {
+      const TokenMeta<D> m = token_meta<D>(a, pos, slot, p0);
+      rope_head<D, kInt8>(a, a.qkv + t * row_elems + h * D, h, p0, v0, v1, m);
+    }
+    if (!more) break;
+    t = tn;
+    v0 = n0;
+    v1 = n1;
+    pos = npos;
+    slot = nslot;
   }
 }
 
 template <int D, bool kInt8>
-void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
+void launch_d(const RopeArgs& a, int wpt, int form, int stream_wgs, hipStream_t stream) {
+  if (form == 1) {
+    rope_kv_wave_kernel<D, kInt8><<<static_cast<unsigned>(a.num_tokens) * wpt, kWave, 0, stream>>>(a, wpt);
+    return;
+  }
+  if (form == 2) {
+    const int g = stream_wgs < a.num_tokens ? stream_wgs : a.num_tokens;
+    switch (wpt) {
+      case 1: rope_kv_stream_kernel<D, kInt8, 1><<<g, 1 * kWave, 0, stream>>>(a); break;
+      case 2: rope_kv_stream_kernel<D, kInt8, 2><<<g, 2 * kWave, 0, stream>>>(a); break;
+      case 3: rope_kv_stream_kernel<D, kInt8, 3><<<g, 3 * kWave, 0, stream>>>(a); break;
+      case 4: rope_kv_stream_kernel<D, kInt8, 4><<<g, 4 * kWave, 0, stream>>>(a); break;
+      case 5: rope_kv_stream_kernel<D, kInt8, 5><<<g, 5 * kWave, 0, stream>>>(a); break;
+      case 6: rope_kv_stream_kernel<D, kInt8, 6><<<g, 6 * kWave, 0, stream>>>(a); break;
+      case 7: rope_kv_stream_kernel<D, kInt8, 7><<<g, 7 * kWave, 0, stream>>>(a); break;
+      default: rope_kv_stream_kernel<D, kInt8, 8><<<g, 8 * kWave, 0, stream>>>(a); break;
+    }
+    return;
+  }
   switch (wpt) {
     case 1: rope_kv_kernel<D, kInt8, 1><<<a.num_tokens, 1 * kWave, 0, stream>>>(a); break;
     case 2: rope_kv_kernel<D, kInt8, 2><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
@@ -161,8 +275,9 @@ void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
 }
 
 template <int D>
-void launch_dt(const RopeArgs& a, bool int8, int wpt, hipStream_t stream) {
-  int8 ? launch_d<D, true>(a, wpt, stream) : launch_d<D, false>(a, wpt, stream);
+void launch_dt(const RopeArgs& a, bool int8, int wpt, int form, int stream_wgs, hipStream_t stream) {
+  int8 ? launch_d<D, true>(a, wpt, form, stream_wgs, stream)
+       : launch_d<D, false>(a, wpt, form, stream_wgs, stream);
 }
 
 }  // namespace
@@ -213,11 +328,22 @@ int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_map
   const int heads_per_wave = kWave / (kv->head_dim / 16);
   int wpt = (heads + heads_per_wave - 1) / heads_per_wave;
   wpt = tune_knob(kRopeWpt, wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
+  if (wpt < 1) wpt = 1;
+  if (wpt > 8) wpt = 8;
+  // Launch form (tuning knob): 0 = one token per workgroup, 1 = one wave
+  // per workgroup, 2 = a token-strided grid of RLK_TUNE_ROPE_WGS workgroups
+  // per CU (only when one pass of the workgroup covers every head).
+  int form = tune_knob(kRopeForm, 0);
+  if (form == 2 && wpt * heads_per_wave < heads) form = 0;
+  if (form < 0 || form > 2) form = 0;
+  const int stream_wgs = compute_units() * std::max(1, tune_knob(kRopeWgs, 4));
+  if (form == 1 && static_cast<int64_t>(num_tokens) * wpt > 0x7fffffff)
+    form = 0;
   const bool int8 = kv->dtype == RLK_KV_INT8;
   if (kv->head_dim == 128) {
-    launch_dt<128>(a, int8, wpt, stream);
+    launch_dt<128>(a, int8, wpt, form, stream_wgs, stream);
   } else {
-    launch_dt<64>(a, int8, wpt, stream);
+    launch_dt<64>(a, int8, wpt, form, stream_wgs, stream);
   }
   return launch_status(what);
 }

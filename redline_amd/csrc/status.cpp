@@ -31,16 +31,18 @@ int launch_status(const char* what) {
 }
 
 int compute_units() {
-  static int cus[64] = {0};
+  // One relaxed atomic per device: concurrent first launches may both query
+  // the attribute, and both store the same value.
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cus[dev] = v;  // the same value from any thread
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 namespace {
@@ -85,7 +87,7 @@ constexpr const char* kKnobNames[kNumKnobs] = {
     "RLK_TUNE_GATHER_BS", "RLK_TUNE_GATHER_NT", "RLK_TUNE_NORM_TPR",   "RLK_TUNE_NORM_NT",
     "RLK_TUNE_SWIGLU_BS", "RLK_TUNE_SWIGLU_NT", "RLK_TUNE_ROPE_WPT",   "RLK_TUNE_ATTN_PERSIST",
     "RLK_TUNE_W4_CFG",    "RLK_TUNE_W8_CFG",    "RLK_TUNE_PREFILL_DMA", "RLK_TUNE_PREFILL_QS",
-    "RLK_TUNE_ATTN_PV",
+    "RLK_TUNE_ATTN_PV",   "RLK_TUNE_ROPE_FORM", "RLK_TUNE_ROPE_WGS",
 };
 constexpr int kUnset = INT_MIN;
 std::atomic<int> g_knobs[kNumKnobs];
@@ -121,6 +123,22 @@ extern "C" int rlk_set_tune_knob(const char* name, int value, int set) {
     }
   }
   return rlk::fail(RLK_EINVAL, "rlk_set_tune_knob: unknown knob '%s'", name ? name : "(null)");
+}
+
+extern "C" int rlk_get_tune_knob(const char* name, int* value, int* is_set) {
+  std::call_once(rlk::g_knobs_once, rlk::read_knobs_from_env);
+  if (name != nullptr && value != nullptr && is_set != nullptr) {
+    for (int k = 0; k < rlk::kNumKnobs; ++k) {
+      if (std::strcmp(name, rlk::kKnobNames[k]) == 0) {
+        const int v = rlk::g_knobs[k].load(std::memory_order_relaxed);
+        *is_set = v != rlk::kUnset;
+        *value = *is_set ? v : 0;
+        return RLK_OK;
+      }
+    }
+  }
+  return rlk::fail(RLK_EINVAL, "rlk_get_tune_knob: unknown knob '%s' or null output",
+                   name ? name : "(null)");
 }
 
 extern "C" const char* rlk_version(void) { return "redline_amd 0.1.0 (gfx950)"; }

@@ -113,7 +113,7 @@ def test_gemv_w4_swiglu_llama_gate_up(torch_cuda, m):
     assert_close_f16(got, want, what="llama swiglu")
 
 
-@pytest.mark.parametrize("cfg", range(12))
+@pytest.mark.parametrize("cfg", range(16))
 def test_gemv_w4_launch_policies_agree(torch_cuda, cfg):
     """Every selectable launch policy gives the same result as the default
     (bit-identical is not required: split-K order differs)."""
@@ -127,6 +127,46 @@ def test_gemv_w4_launch_policies_agree(torch_cuda, cfg):
     with tune_knob("RLK_TUNE_W4_CFG", cfg):
         got = run_gemv(torch, x, packed, s, o, g, f32=True)
     assert rel_max_err(got, want) <= 1e-4
+
+
+@pytest.mark.parametrize("cfg", [12, 13, 14, 15])
+@pytest.mark.parametrize("n,k,g", [(592, 1024, 128), (592, 1024, 256), (12368, 512, 128),
+                                   (160, 2048, 512)])
+@pytest.mark.parametrize("m", [1, 9, 17, 32])
+def test_gemv_w4_kslice_shapes(torch_cuda, cfg, n, k, g, m):
+    """The K-slice kernel (each wave one K slice of every tile of its
+    workgroup, x in registers, partials added in LDS) on the shapes it takes:
+    rows in whole 16-row tiles, K a whole number of slices; one tile per
+    workgroup (n = 592: 37 tiles) and several, with the last workgroup
+    partial (n = 12368: 773 tiles); groups of 1, 2 and 4 chunks.  fp32 out
+    against the float64 oracle at the reference's bound, and the SwiGLU
+    epilogue at fp16 tolerance."""
+    torch = torch_cuda
+    say(f"gemv_w4 kslice cfg={cfg} n={n} k={k} g={g} m={m}")
+    rng = np.random.default_rng(cfg * 1000 + m + k)
+    packed, s, o, _ = int4_linear(rng, n, k, g, dense=False)
+    x = randn_f16(rng, (m, k))
+    bias = randn_f16(rng, (n,), 0.1)
+    want = oracle.gemv_w4a16(x, packed, s, o, g, bias)
+    with tune_knob("RLK_TUNE_W4_CFG", cfg):
+        got = run_gemv(torch, x, packed, s, o, g, bias, f32=True)
+        got_sw = run_swiglu(torch, x, packed, s, o, g)
+    assert rel_max_err(got, want) <= 1e-4
+    assert_close_f16(got_sw, oracle.gemv_w4a16_swiglu(x, packed, s, o, g), what="kslice swiglu")
+
+
+@pytest.mark.parametrize("cfg", [12, 13])
+@pytest.mark.parametrize("m", [1, 16, 32])
+def test_gemv_w4_kslice_llama_gate_up(torch_cuda, cfg, m):
+    torch = torch_cuda
+    say(f"gemv_w4_swiglu kslice cfg={cfg} llama m={m}")
+    rng = np.random.default_rng(70 + m)
+    n, k, g = 2 * 14336, 4096, 128
+    packed, s, o, _ = int4_linear(rng, n, k, g, dense=False)
+    x = randn_f16(rng, (m, k))
+    with tune_knob("RLK_TUNE_W4_CFG", cfg):
+        got = run_swiglu(torch, x, packed, s, o, g)
+    assert_close_f16(got, oracle.gemv_w4a16_swiglu(x, packed, s, o, g), what="llama kslice")
 
 
 def test_gemv_w4_deterministic_and_errors(torch_cuda):

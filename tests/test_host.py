@@ -301,8 +301,18 @@ def test_tune_knobs_set_and_clear():
     assert L.rlk_set_tune_knob(b"RLK_TUNE_ROPE_WPT", 0, 0) == 0
     assert L.rlk_set_tune_knob(b"RLK_TUNE_NOPE", 1, 1) == _lib.RLK_EINVAL
     assert b"unknown knob" in L.rlk_last_error()
+    assert _lib.get_tune_knob("RLK_TUNE_ROPE_WPT") is None
     with _lib.tune_knob("RLK_TUNE_W4_CFG", 2):
-        pass
+        assert _lib.get_tune_knob("RLK_TUNE_W4_CFG") == 2
+    assert _lib.get_tune_knob("RLK_TUNE_W4_CFG") is None
+    # a nested override restores the outer value, not "unset"
+    with _lib.tune_knob("RLK_TUNE_W8_CFG", 1):
+        with _lib.tune_knob("RLK_TUNE_W8_CFG", 3):
+            assert _lib.get_tune_knob("RLK_TUNE_W8_CFG") == 3
+        assert _lib.get_tune_knob("RLK_TUNE_W8_CFG") == 1
+    assert _lib.get_tune_knob("RLK_TUNE_W8_CFG") is None
+    v, st = C.c_int(7), C.c_int(7)
+    assert L.rlk_get_tune_knob(b"RLK_TUNE_NOPE", C.byref(v), C.byref(st)) == _lib.RLK_EINVAL
 
 
 def test_embedding_rmsnorm_argument_errors():

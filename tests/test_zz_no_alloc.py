@@ -59,9 +59,11 @@ def test_decode_noalloc_matches_workspace_entry():
     from redline_amd import kernels as K
     rng = np.random.default_rng(11)
     # C2 shape (32 items, 32 heads / 8 kv heads, D 128, contexts to 8192: 32
-    # partitions, 17 MB of partials), then a smaller INT8 call at D 64
+    # partitions, 17 MB of partials), then a smaller INT8 call at D 64, then a
+    # single-partition call (contexts <= 256: no split-K scratch is used)
     for items, hq, hkv, D, max_ctx, int8 in ((32, 32, 8, 128, 8192, False),
-                                             (5, 8, 2, 64, 700, True)):
+                                             (5, 8, 2, 64, 700, True),
+                                             (3, 8, 2, 128, 200, False)):
         say(f"noalloc decode items={items} hq={hq} hkv={hkv} D={D} ctx={max_ctx} int8={int8}")
         case = _case(torch, K, rng, items, hq, hkv, D, max_ctx, int8)
         want = _run(torch, K, case, hq, noalloc=False)
