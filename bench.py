@@ -260,31 +260,39 @@ def kernel_fns(data):
             "stream_copy": data.stream_copy}
 
 
+# Launches per timed graph at least: with fewer, the per-replay overhead of
+# the graph itself (about 1 us) would be charged to each launch (at C4/C5 the
+# rotation holds only R = 3 input sets).
+MIN_GRAPH_LAUNCHES = 24
+
+
 def per_kernel(torch, data, reps, only=None, names=KERNELS, warm=True):
-    """Per-call time of each kernel: a graph of R back-to-back launches (one
-    per rotating input set, so the inputs come from HBM: the cold figure the
-    roofline uses), replayed `reps` times between HIP events on the launch
-    stream; with `warm`, also R launches on input set 0 (the warm figure:
-    inputs left in the caches by the previous launch where they fit)."""
+    """Per-call time of each kernel: a graph of back-to-back launches cycling
+    through the R rotating input sets (so the inputs come from HBM: the cold
+    figure the roofline uses), at least MIN_GRAPH_LAUNCHES of them, replayed
+    `reps` times between HIP events on the launch stream; with `warm`, also
+    as many launches on input set 0 (the warm figure: inputs left in the
+    caches by the previous launch where they fit)."""
     fns = kernel_fns(data)
     nbytes = data.bytes()
     out = {}
+    n = data.R * -(-MIN_GRAPH_LAUNCHES // data.R)
     for name in names:
         if only and name != only:
             continue
         f = fns[name]
-        g = capture(torch, lambda: [f(r) for r in range(data.R)])
-        ms = time_graph(torch, g, reps) / data.R
+        g = capture(torch, lambda: [f(i % data.R) for i in range(n)])
+        ms = time_graph(torch, g, reps) / n
         del g
         gbs = nbytes[name] / (ms * 1e-3) / 1e9
         out[name] = {"us_per_call": round(ms * 1e3, 3), "gb_per_s": round(gbs, 1),
                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_call": nbytes[name]}
         msg = (f"  {data.w.key} {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s "
-               f"({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)  R={data.R}")
+               f"({100 * gbs / HBM_PEAK_GBS:5.1f}% of peak)  R={data.R}, {n} per graph")
         if warm:
-            g = capture(torch, lambda: [f(0) for _ in range(data.R)])
-            ms_w = time_graph(torch, g, reps) / data.R
+            g = capture(torch, lambda: [f(0) for _ in range(n)])
+            ms_w = time_graph(torch, g, reps) / n
             del g
             out[name]["us_per_call_warm"] = round(ms_w * 1e3, 3)
             msg += f"; warm {ms_w * 1e3:9.2f} us"
@@ -298,11 +306,7 @@ SWEEP_KNOBS = {
     "silu_and_mul": {"RLK_TUNE_SWIGLU_BS": [64, 128, 256], "RLK_TUNE_SWIGLU_NT": [0, 1]},
     "rope_and_write_kv": {"RLK_TUNE_ROPE_WPT": [1, 2, 3, 4, 5, 6, 8]},
 }
-# Launch forms of rope_and_write_kv, swept as explicit settings (WPT 0 = the
-# default, waves enough to cover a token's heads in one pass).
-ROPE_FORMS = ([{"RLK_TUNE_ROPE_FORM": 0, "RLK_TUNE_ROPE_WPT": w} for w in (0, 8)] +
-              [{"RLK_TUNE_ROPE_FORM": 1, "RLK_TUNE_ROPE_WPT": w} for w in (0, 3, 2)] +
-              [{"RLK_TUNE_ROPE_FORM": 2, "RLK_TUNE_ROPE_WGS": g} for g in (1, 2, 3, 4, 5, 6, 8)])
+
 
 
 def sweep(torch, data, reps, only=None):
@@ -315,11 +319,7 @@ def sweep(torch, data, reps, only=None):
         if only and kern != only:
             continue
         names = list(knobs)
-        settings = list(itertools.product(*knobs.values()))
-        if kern == "rope_and_write_kv":
-            names = ["RLK_TUNE_ROPE_FORM", "RLK_TUNE_ROPE_WPT", "RLK_TUNE_ROPE_WGS"]
-            settings = [tuple(f.get(n) or None for n in names) for f in ROPE_FORMS]
-        for vals in settings:
+        for vals in itertools.product(*knobs.values()):
             for n, v in zip(names, vals):
                 set_tune_knob(n, v)
             r = per_kernel(torch, data, reps, kern, names=(kern,), warm=False)[kern]

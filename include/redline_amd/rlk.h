@@ -62,8 +62,7 @@ const char* rlk_version(void);
 /* Tuning hook (no counterpart in the reference): sets (set != 0) or clears
  * the launch-policy override `name` (one of RLK_TUNE_GATHER_BS, _GATHER_NT,
  * _NORM_TPR, _NORM_NT, _SWIGLU_BS, _SWIGLU_NT, _ROPE_WPT, _ATTN_PERSIST,
- * _W4_CFG, _W8_CFG, _PREFILL_DMA, _PREFILL_QS, _ATTN_PV, _ROPE_FORM,
- * _ROPE_WGS).  The environment variables of
+ * _W4_CFG, _W8_CFG, _PREFILL_DMA, _PREFILL_QS, _ATTN_PV).  The environment variables of
  * the same names are read once, at the first launch of the process; later
  * changes go through this call only.  Unknown name: RLK_EINVAL.
  * The knobs are process-wide, not per stream or thread: a change applies to

@@ -22,7 +22,6 @@
 // deterministic function of the inputs.
 #include <hip/hip_runtime.h>
 
-#include <algorithm>
 #include <cstdint>
 
 #include "device.hpp"
@@ -176,92 +175,14 @@ __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t t, int wav
   }
 }
 
-// Form 0: one token per workgroup of WPT waves.
+// One token per workgroup of WPT waves.
 template <int D, bool kInt8, int WPT>
 __global__ __launch_bounds__(kWave * WPT) void rope_kv_kernel(RopeArgs a) {
   rope_token<D, kInt8>(a, blockIdx.x, threadIdx.x / kWave, WPT, threadIdx.x % kWave);
 }
 
-// Form 1: one wave per workgroup; workgroup b is wave b % nwaves of token
-// b / nwaves.
 template <int D, bool kInt8>
-__global__ __launch_bounds__(kWave) void rope_kv_wave_kernel(RopeArgs a, int nwaves) {
-  const int64_t t = blockIdx.x / nwaves;
-  rope_token<D, kInt8>(a, t, blockIdx.x - t * nwaves, nwaves, threadIdx.x);
-}
-
-// Form 2: a grid of workgroups of WPT waves that together cover every head
-// of a token (heads <= WPT * heads_per_wave) walks the tokens with a stride
-// of the grid, two-stage pipelined: the next token's activations, position
-// and slot are requested before the current token is rotated and stored.
-template <int D, bool kInt8, int WPT>
-__global__ __launch_bounds__(kWave * WPT) void rope_kv_stream_kernel(RopeArgs a) {
-  constexpr bool NT = true;
-  constexpr int kHalf = D / 2;
-  constexpr int kLPH = kHalf / 8;
-  constexpr int kHeadsPerWave = kWave / kLPH;
-  const int lane = threadIdx.x % kWave;
-  const int h = (threadIdx.x / kWave) * kHeadsPerWave + lane / kLPH;
-  const int p0 = (lane % kLPH) * 8;
-  const int heads = a.hq + 2 * a.hkv;
-  const bool active = h < heads;
-  const int64_t row_elems = static_cast<int64_t>(heads) * D;
-  int64_t t = blockIdx.x;
-  if (t >= a.num_tokens) return;
-  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
-  if (active) {
-    const _Float16* hp = a.qkv + t * row_elems + h * D;
-    v0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
-    v1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
-  }
-  int pos = a.positions[t], slot = a.slots[t];
-  for (;;) {
-    const int64_t tn = t + gridDim.x;
-    const bool more = tn < a.num_tokens;  // uniform over the workgroup
-    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
-    int npos = 0, nslot = -1;
-    if (more) {
-      if (active) {
-        const _Float16* hp = a.qkv + tn * row_elems + h * D;
-        n0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
-        n1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
-      }
-      npos = a.positions[tn];
-      nslot = a.slots[tn];
-    }
-    if (active) {
-      const TokenMeta<D> m = token_meta<D>(a, pos, slot, p0);
-      rope_head<D, kInt8>(a, a.qkv + t * row_elems + h * D, h, p0, v0, v1, m);
-    }
-    if (!more) break;
-    t = tn;
-    v0 = n0;
-    v1 = n1;
-    pos = npos;
-    slot = nslot;
-  }
-}
-
-template <int D, bool kInt8>
-void launch_d(const RopeArgs& a, int wpt, int form, int stream_wgs, hipStream_t stream) {
-  if (form == 1) {
-    rope_kv_wave_kernel<D, kInt8><<<static_cast<unsigned>(a.num_tokens) * wpt, kWave, 0, stream>>>(a, wpt);
-    return;
-  }
-  if (form == 2) {
-    const int g = stream_wgs < a.num_tokens ? stream_wgs : a.num_tokens;
-    switch (wpt) {
-      case 1: rope_kv_stream_kernel<D, kInt8, 1><<<g, 1 * kWave, 0, stream>>>(a); break;
-      case 2: rope_kv_stream_kernel<D, kInt8, 2><<<g, 2 * kWave, 0, stream>>>(a); break;
-      case 3: rope_kv_stream_kernel<D, kInt8, 3><<<g, 3 * kWave, 0, stream>>>(a); break;
-      case 4: rope_kv_stream_kernel<D, kInt8, 4><<<g, 4 * kWave, 0, stream>>>(a); break;
-      case 5: rope_kv_stream_kernel<D, kInt8, 5><<<g, 5 * kWave, 0, stream>>>(a); break;
-      case 6: rope_kv_stream_kernel<D, kInt8, 6><<<g, 6 * kWave, 0, stream>>>(a); break;
-      case 7: rope_kv_stream_kernel<D, kInt8, 7><<<g, 7 * kWave, 0, stream>>>(a); break;
-      default: rope_kv_stream_kernel<D, kInt8, 8><<<g, 8 * kWave, 0, stream>>>(a); break;
-    }
-    return;
-  }
+void launch_d(const RopeArgs& a, int wpt, hipStream_t stream) {
   switch (wpt) {
     case 1: rope_kv_kernel<D, kInt8, 1><<<a.num_tokens, 1 * kWave, 0, stream>>>(a); break;
     case 2: rope_kv_kernel<D, kInt8, 2><<<a.num_tokens, 2 * kWave, 0, stream>>>(a); break;
@@ -275,9 +196,8 @@ void launch_d(const RopeArgs& a, int wpt, int form, int stream_wgs, hipStream_t 
 }
 
 template <int D>
-void launch_dt(const RopeArgs& a, bool int8, int wpt, int form, int stream_wgs, hipStream_t stream) {
-  int8 ? launch_d<D, true>(a, wpt, form, stream_wgs, stream)
-       : launch_d<D, false>(a, wpt, form, stream_wgs, stream);
+void launch_dt(const RopeArgs& a, bool int8, int wpt, hipStream_t stream) {
+  int8 ? launch_d<D, true>(a, wpt, stream) : launch_d<D, false>(a, wpt, stream);
 }
 
 }  // namespace
@@ -330,20 +250,11 @@ int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_map
   wpt = tune_knob(kRopeWpt, wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
   if (wpt < 1) wpt = 1;
   if (wpt > 8) wpt = 8;
-  // Launch form (tuning knob): 0 = one token per workgroup, 1 = one wave
-  // per workgroup, 2 = a token-strided grid of RLK_TUNE_ROPE_WGS workgroups
-  // per CU (only when one pass of the workgroup covers every head).
-  int form = tune_knob(kRopeForm, 0);
-  if (form == 2 && wpt * heads_per_wave < heads) form = 0;
-  if (form < 0 || form > 2) form = 0;
-  const int stream_wgs = compute_units() * std::max(1, tune_knob(kRopeWgs, 4));
-  if (form == 1 && static_cast<int64_t>(num_tokens) * wpt > 0x7fffffff)
-    form = 0;
   const bool int8 = kv->dtype == RLK_KV_INT8;
   if (kv->head_dim == 128) {
-    launch_dt<128>(a, int8, wpt, form, stream_wgs, stream);
+    launch_dt<128>(a, int8, wpt, stream);
   } else {
-    launch_dt<64>(a, int8, wpt, form, stream_wgs, stream);
+    launch_dt<64>(a, int8, wpt, stream);
   }
   return launch_status(what);
 }

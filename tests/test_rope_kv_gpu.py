@@ -378,20 +378,16 @@ def test_rope_extension_null_options_is_plain(torch_cuda):
     assert_bits_equal(outs[0][1], outs[1][1], "k cache")
 
 
-@pytest.mark.parametrize("form,wpt", [(0, 1), (0, 2), (0, 3), (0, 8), (1, 1), (1, 3), (1, 6),
-                                      (2, 5), (2, 6), (2, 8)])
+@pytest.mark.parametrize("wpt", [1, 2, 3, 8])
 @pytest.mark.parametrize("hq,hkv,D,int8,lens", [REF_CASES[0], REF_CASES[1], REF_CASES[4],
                                                 (32, 8, 128, False, [200, 57]),
                                                 (32, 8, 128, True, [130]), (28, 4, 128, False, [90])])
-def test_rope_kv_launch_policies(torch_cuda, form, wpt, hq, hkv, D, int8, lens):
-    """Every launch policy gives the same bits: one token per workgroup of
-    wpt waves (form 0), one wave per workgroup (form 1) and the token-strided
-    pipelined grid (form 2, here with 1 workgroup per CU so that each
-    workgroup walks several tokens; it falls back to form 0 when wpt waves do
-    not cover a token's heads).  The Llama-3.1-8B and Qwen2-7B head counts
-    leave partial head sweeps at every setting."""
+def test_rope_kv_launch_policies(torch_cuda, wpt, hq, hkv, D, int8, lens):
+    """Every launch policy (waves per token) gives the same bits: the
+    Llama-3.1-8B and Qwen2-7B head counts leave partial head sweeps at every
+    setting."""
     from redline_amd._lib import tune_knob
-    say(f"rope policy form={form} wpt={wpt} hq={hq} hkv={hkv} D={D} int8={int8}")
+    say(f"rope policy wpt={wpt} hq={hq} hkv={hkv} D={D} int8={int8}")
     bs = 16
     rng = np.random.default_rng(hq + hkv + D + wpt)
     T = sum(lens)
@@ -400,6 +396,5 @@ def test_rope_kv_launch_policies(torch_cuda, form, wpt, hq, hkv, D, int8, lens):
     slots[rng.integers(0, T)] = -1
     pos = rng.integers(0, 4096, T).astype(np.int32)
     qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
-    with tune_knob("RLK_TUNE_ROPE_WPT", wpt), tune_knob("RLK_TUNE_ROPE_FORM", form), \
-            tune_knob("RLK_TUNE_ROPE_WGS", 1):
+    with tune_knob("RLK_TUNE_ROPE_WPT", wpt):
         run_case(torch_cuda, qkv, pos, slots, hq, hkv, D, nblocks, int8, theta=5e5)
