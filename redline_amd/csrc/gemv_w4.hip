@@ -739,10 +739,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
 // and whose rows are whole 16-row tiles.  A workgroup owns T consecutive
 // 16-row tiles; wave w owns K slice w (chunks w CPW .. w CPW + CPW - 1) of
 // every one of them.  So each wave needs only its own slice of x, which it
-// loads once, straight into the MFMA A-operand layout in registers (no x in
-// LDS: no staging pass, no per-chunk LDS reads of x, no bank conflicts), and
-// computes that slice's per-chunk sum(x) once with MFMAs against a ones
-// operand, for all of its tiles.  The wave then walks its tiles, fetching
+// loads once into registers in the MFMA A-operand layout (whole cache lines,
+// transposed through the wave's own LDS rows; no per-chunk LDS reads of x,
+// no workgroup-wide staging pass), and computes that slice's per-chunk
+// sum(x) once with MFMAs against a ones operand, for all of its tiles.  The wave then walks its tiles, fetching
 // each tile's slice as chunk pairs of full cache lines (the pair kernel's
 // loads and DPP hand-over) through a ring of U tiles' pairs, and leaves one
 // partial 16x16 result per tile in LDS; after one barrier, wave w adds the
@@ -796,16 +796,35 @@ __global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_ks
 
   // x of this wave's slice in the A-operand layout: lane (qd, r16) holds
   // row min(16 mt + r16, m - 1), K (c0 + c) 128 + 32 qd + 8 j .. + 7,
-  // permuted to the codes' nibble order
+  // permuted to the codes' nibble order.  Read straight in that layout, a
+  // load instruction would touch 16 rows x 2 cache lines for 1 KB; instead
+  // each (chunk, tile) block of 16 rows x 256 bytes is fetched as 4 loads of
+  // 4 whole rows (full lines), written to the wave's own LDS rows and read
+  // back in the MFMA layout.  The staging rows lie in the partial-sum region,
+  // which no wave writes before the barrier below.
   f16x8 xa[CPW][MT][4];
+  {
+    constexpr int kXRow = 272;  // bytes per staged row: 256 + 16 (conflict-free column reads)
+    uint8_t* xst = lds + a.slab_off + wave * 16 * kXRow;
+    const int lr = lane / 16, lc = (lane % 16) * 16;  // load: row 4 i + lr, bytes lc
 #pragma unroll
-  for (int c = 0; c < CPW; ++c)
+    for (int c = 0; c < CPW; ++c)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 v[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        xa[c][mt][j] = x_perm(load16(a.x + static_cast<size_t>(min(16 * mt + r16, a.m - 1)) * a.k +
-                                     (c0 + c) * 128 + qd * 32 + 8 * j));
+        for (int i = 0; i < 4; ++i)
+          v[i] = load16(reinterpret_cast<const uint8_t*>(
+                            a.x + static_cast<size_t>(min(16 * mt + 4 * i + lr, a.m - 1)) * a.k +
+                            (c0 + c) * 128) + lc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<u32x4*>(xst + (4 * i + lr) * kXRow + lc) = v[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xa[c][mt][j] = x_perm(*reinterpret_cast<const u32x4*>(xst + r16 * kXRow + qd * 64 + 16 * j));
+      }
+  }
   // scales and offsets of the workgroup's rows, requested before the ring
   constexpr int kSoBatch = 8;
   const int staged = 16 * T * a.groups;
@@ -1021,14 +1040,17 @@ int launch_kslice(W4Args a, hipStream_t stream) {
   const int nw = a.nchunks / CPW;
   const int ntiles = a.n / 16;
   const int cus = compute_units();
-  auto lds_for = [&](int t) {
+  auto lds_for = [&](int t) {  // scales and offsets, then the partial sums (which
+    // double as the waves' x staging rows, 16 x 272 bytes each)
     const size_t so = (static_cast<size_t>(16) * t * (a.groups + 1) * 4 + 15) / 16 * 16;
-    return so + static_cast<size_t>(t) * nw * MT * kWave * sizeof(f32x4);
+    return so + std::max(static_cast<size_t>(t) * nw * MT * kWave * sizeof(f32x4),
+                         static_cast<size_t>(nw) * 16 * 272);
   };
   int T = (ntiles + cus - 1) / cus;
   T = (T + U - 1) / U * U;
   while (T > U && lds_for(T) > kLdsBudget) T -= U;
   if (lds_for(T) > kLdsBudget) return kNoFit;
+
   a.cpp = T;
   a.slab_off = static_cast<int>((static_cast<size_t>(16) * T * (a.groups + 1) * 4 + 15) / 16 * 16);
   const size_t lds = lds_for(T);
@@ -1045,8 +1067,8 @@ int launch_kslice(W4Args a, hipStream_t stream) {
 
 // Launch policies, selectable for tuning sweeps through RLK_TUNE_W4_CFG.
 // Entry 0, the default, is the pair kernel with 4 pairs in flight per wave up
-// to m = 8 and 2 up to m = 16, and the K-slice kernel (4 chunks per slice, one
-// tile's pairs in flight) above; 9, 10 and 11 are the pair kernel with 2, 8
+// to m = 8 (2 where the K-slice kernel does not fit), and the K-slice kernel
+// (4 chunks per slice, two tiles' pairs in flight) above; 9, 10 and 11 are the pair kernel with 2, 8
 // and 4 pairs at every m; 12-15 the K-slice kernel with (chunks per slice,
 // tiles in flight) = (4, 1), (4, 2), (2, 2), (2, 4); 8 is the slab kernel with 8
 // chunk pairs in flight; 1-7 are slab-kernel variants (K-split ways, slots in
@@ -1075,10 +1097,11 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
       case 7: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
       default:
         // measured at the Llama-3.1-8B gate_up shape: the pair kernel with 4
-        // pairs in flight up to m = 8 and 2 up to m = 16; the K-slice kernel
-        // above m = 16 (two activation tiles), where staging x per workgroup
-        // and reading it back from LDS per chunk cost the most
-        if (a.m > 16) st = launch_kslice<4, 1, MT, MODE>(a, s);
+        // pairs in flight up to m = 8; the K-slice kernel with two tiles'
+        // pairs in flight above, where staging x per workgroup and reading it
+        // back from LDS per chunk cost the most (m = 16: 15.3 against 17.1 us,
+        // m = 32: 20.2 against 25.7)
+        if (a.m > 8) st = launch_kslice<4, 2, MT, MODE>(a, s);
         if (st == kNoFit)
           st = a.m <= 8 ? launch_pairs<4, MT, MODE>(a, s) : launch_pairs<2, MT, MODE>(a, s);
         break;
