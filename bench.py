@@ -694,7 +694,7 @@ def main():
 
     if args.profile_calls:
         fns = kernel_fns(data)
-        for name in KERNELS + STEP_EXTRA + ("stream_copy",):
+        for name in KERNELS + STEP_EXTRA:
             if args.only and args.only not in (name, "elementwise"):
                 continue
             for i in range(args.profile_calls):
