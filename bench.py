@@ -694,9 +694,11 @@ def main():
 
     if args.profile_calls:
         fns = kernel_fns(data)
-        for name in KERNELS + STEP_EXTRA:
+        for name in KERNELS + STEP_EXTRA + ("stream_copy",):
             if args.only and args.only not in (name, "elementwise"):
                 continue
+            if name == "stream_copy" and args.only != name:
+                continue  # the yardstick shares gather_rows_kernel's symbol: only on request
             for i in range(args.profile_calls):
                 fns[name](i % data.R)
         if args.only in (None, "paged_attention_decode"):
