@@ -169,6 +169,26 @@ def test_gemv_w4_kslice_llama_gate_up(torch_cuda, cfg, m):
     assert_close_f16(got, oracle.gemv_w4a16_swiglu(x, packed, s, o, g), what="llama kslice")
 
 
+@pytest.mark.parametrize("m", [9, 17])
+def test_gemv_w4_kslice_tiles_cut_to_lds(torch_cuda, m):
+    """The default (K-slice) kernel above m = 8 at a shape whose partial sums
+    for one workgroup per CU would overflow LDS (n = 40960: 2560 tiles, 10 per
+    workgroup; at two activation tiles that is 160 KiB of partials), so the
+    launcher gives each workgroup fewer tiles.  Checked on 1024 sampled
+    (gate, up) column pairs against the oracle."""
+    torch = torch_cuda
+    say(f"gemv_w4_swiglu kslice lds-cut n=40960 m={m}")
+    rng = np.random.default_rng(4096 + m)
+    n, k, g = 40960, 4096, 128
+    packed, s, o, _ = int4_linear(rng, n, k, g, dense=False)
+    x = randn_f16(rng, (m, k))
+    got = run_swiglu(torch, x, packed, s, o, g)
+    cols = np.sort(rng.choice(n // 2, 1024, replace=False))
+    rows = np.stack([2 * cols, 2 * cols + 1], axis=1).reshape(-1)
+    want = oracle.gemv_w4a16_swiglu(x, packed[rows], s[rows], o[rows], g)
+    assert_close_f16(got[:, cols], want, what="kslice lds-cut")
+
+
 def test_gemv_w4_deterministic_and_errors(torch_cuda):
     torch = torch_cuda
     from redline_amd import kernels as K
