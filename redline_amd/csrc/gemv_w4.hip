@@ -58,10 +58,12 @@ struct W4Args {
   void* y;            // [m, y_ld]
   int m;              // activation rows (1 .. 16 MT)
   int n, k, group_size, groups, nchunks;
-  int cpp;            // K chunks per x pass (a multiple of K-split ways x ring depth)
+  int cpp;            // K chunks per x pass (a multiple of K-split ways x ring depth);
+                      // K-slice kernel: 16-row tiles per workgroup
   int npass;
   int xstride;        // halves per staged x row
-  int slab_off;       // bytes from the end of x to the first chunk-pair slab
+  int slab_off;       // bytes from the end of x to the first chunk-pair slab;
+                      // K-slice kernel: bytes from the LDS base to the partial sums
   int y_ld;
   int gq_shift;       // pair kernel: log2(group_size / 128)
   int gpp;            // pair kernel: quantisation groups per x pass
