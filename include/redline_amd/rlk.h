@@ -4,7 +4,10 @@
  * Every device entry point is asynchronous on the given HIP stream, never
  * allocates, frees or synchronises, and is therefore capturable into a HIP
  * graph.  Pointers are device pointers owned by the caller.  fp16 tensors are
- * passed as uint16_t* holding IEEE binary16 bit patterns.
+ * passed as uint16_t* holding IEEE binary16 bit patterns.  Row data moves as
+ * 16-byte vectors, as in the reference's kernels: tensors and row strides must
+ * be 16-byte aligned (hipMalloc'd buffers are), and an output must not overlap
+ * an input unless the entry point says it is updated in place (residual, qkv).
  *
  * Return value: RLK_OK (0) on success; a negative RLK_E* code for an argument
  * error detected on the host before anything is launched; a positive hipError_t
