@@ -1068,11 +1068,12 @@ int launch_kslice(W4Args a, hipStream_t stream) {
 }
 
 // Launch policies, selectable for tuning sweeps through RLK_TUNE_W4_CFG.
-// Entry 0, the default, is the pair kernel with 4 pairs in flight per wave up
-// to m = 8 (2 where the K-slice kernel does not fit), and the K-slice kernel
-// (4 chunks per slice, two tiles' pairs in flight) above; 9, 10 and 11 are the pair kernel with 2, 8
-// and 4 pairs at every m; 12-15 the K-slice kernel with (chunks per slice,
-// tiles in flight) = (4, 1), (4, 2), (2, 2), (2, 4); 8 is the slab kernel with 8
+// Entry 0, the default, is the K-slice kernel (4 chunks per slice, two
+// tiles' pairs in flight) from m = 8 on, and the pair kernel below m = 8 or
+// where the K-slice kernel does not fit (4 pairs in flight up to m = 8, 2
+// above); 9, 10 and 11 are the pair kernel with 2, 8 and 4 pairs at every m;
+// 12-15 the K-slice kernel with (chunks per slice, tiles in flight) = (4, 1),
+// (4, 2), (2, 2), (2, 4); 8 is the slab kernel with 8
 // chunk pairs in flight; 1-7 are slab-kernel variants (K-split ways, slots in
 // flight per wave, most row waves per workgroup, chunks per slot).  Shapes the
 // pair kernel does not take (an odd chunk count, group_size / 128 not a power
@@ -1099,11 +1100,12 @@ int launch_cfg(const W4Args& a, int cfg, hipStream_t s) {
       case 7: st = launch<2, 8, KC, MT, MODE>(a, 4, s); break;
       default:
         // measured at the Llama-3.1-8B gate_up shape: the pair kernel with 4
-        // pairs in flight up to m = 8; the K-slice kernel with two tiles'
-        // pairs in flight above, where staging x per workgroup and reading it
-        // back from LDS per chunk cost the most (m = 16: 15.3 against 17.1 us,
-        // m = 32: 20.2 against 25.7)
-        if (a.m > 8) st = launch_kslice<4, 2, MT, MODE>(a, s);
+        // pairs in flight below m = 8 (m = 4: 14.5-14.8 against 15.1-15.9 us);
+        // the K-slice kernel with two tiles' pairs in flight from m = 8 on,
+        // where staging x per workgroup and reading it back from LDS per chunk
+        // cost the most (m = 8: 15.2-15.3 against 15.4-15.6 us, m = 16:
+        // 15.5-15.7 against 17.3-17.5, m = 32: 20.2 against 25.7)
+        if (a.m >= 8) st = launch_kslice<4, 2, MT, MODE>(a, s);
         if (st == kNoFit)
           st = a.m <= 8 ? launch_pairs<4, MT, MODE>(a, s) : launch_pairs<2, MT, MODE>(a, s);
         break;
