@@ -639,8 +639,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the fused per-layer kernels are row-independent "
-              "and this build has no multi-GPU path (see DESIGN.md, 'How it would shard').",
-              file=sys.stderr)
+              "(rows or heads would shard across GPUs with no exchange) and this build has no "
+              "multi-GPU path.", file=sys.stderr)
         sys.exit(2)
 
     import torch
