@@ -114,6 +114,22 @@ __device__ __forceinline__ f16x8 codes_f16(uint32_t word, uint32_t magic) {
 }
 constexpr float kCodeBias = 64.0f;
 
+// The K-slice kernel's form: 5 VALU per 8 codes instead of 7.  Nibbles in
+// mantissa bits 0..3 of 1024.0 read 1024 + q, in bits 4..7 of 64.0 read
+// 64 + q, so the word needs one shift: (q0, q4) and (q2, q6) take magic
+// m1024, (q1, q5) and (q3, q7) m64 -- the same element order as codes_f16.
+// The biases leave through sum(x * kBias2) per chunk.  The larger bias costs
+// fp32 sum bits (the kernel's relative error grows from ~1e-6 to ~1e-5 at
+// k = 4096; the fp32-output bound is 1e-4).
+__device__ __forceinline__ f16x8 codes_f16_2m(uint32_t word, uint32_t m1024, uint32_t m64) {
+  const uint32_t w8 = word >> 8;
+  const u32x4 r = {and_or(word, 0x000F000Fu, m1024), and_or(word, 0x00F000F0u, m64),
+                   and_or(w8, 0x000F000Fu, m1024), and_or(w8, 0x00F000F0u, m64)};
+  return __builtin_bit_cast(f16x8, r);
+}
+// The bias of each element of codes_f16_2m's output.
+constexpr f16x8 kBias2 = {1024, 1024, 64, 64, 1024, 1024, 64, 64};
+
 // 8 consecutive activations permuted to the codes' order.
 __device__ __forceinline__ f16x8 x_perm(u32x4 v) {
   const f16x8 h = __builtin_bit_cast(f16x8, v);
@@ -744,12 +760,16 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_w4_pairs_kernel(W4Args a)
 // loads once into registers in the MFMA A-operand layout (whole cache lines,
 // transposed through the wave's own LDS rows; no per-chunk LDS reads of x,
 // no workgroup-wide staging pass), and computes that slice's per-chunk
-// sum(x) once with MFMAs against a ones operand, for all of its tiles.  The wave then walks its tiles, fetching
-// each tile's slice as chunk pairs of full cache lines (the pair kernel's
-// loads and DPP hand-over) through a ring of U tiles' pairs, and leaves one
-// partial 16x16 result per tile in LDS; after one barrier, wave w adds the
-// nw partials of tile w (w + nw, ...) in slice order -- a fixed order, so the
-// result is deterministic -- and stores it through the epilogue.  Scales and
+// sum(x) and sum(x * code bias) once, for all of its tiles.  The wave then
+// walks its tiles, fetching each tile's slice as chunk pairs of full cache
+// lines (the pair kernel's loads and DPP hand-over) through a ring of U
+// tiles' pairs.  Codes become fp16 with two magics (codes_f16_2m, 5 VALU per
+// 8 codes); per chunk only acc += s * (x . (bias + q)) runs on the vector
+// ALU, and the offset and bias terms of all the slice's chunks enter each
+// tile as two fp32 MFMAs with K = the chunks.  Each tile leaves one partial
+// 16x16 result in LDS; after one barrier, wave w adds the nw partials of
+// tile w (w + nw, ...) in slice order -- a fixed order, so the result is
+// deterministic -- and stores it through the epilogue.  Scales and
 // offsets of the workgroup's rows are staged once into LDS (coalesced:
 // [n, groups] is contiguous over the workgroup's rows).
 // Waves per workgroup of the K-slice kernel: 16 when a slice's x fits in
@@ -759,6 +779,7 @@ constexpr int kslice_max_waves() { return CPW * MT <= 2 ? 16 : kMaxWaves; }
 
 template <int CPW, int U, int MT, int MODE>
 __global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_kslice_kernel(W4Args a) {
+  static_assert(CPW == 2 || CPW == 4, "a slice's chunks are the K of one fp32 MFMA (at most 4)");
   constexpr int kPPT = CPW / 2;  // chunk pairs per tile and wave
   constexpr int P = kPPT * U;    // ring depth in pairs: U tiles
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -857,29 +878,56 @@ __global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_ks
     so_load(i0);
     so_store(i0);
   }
-  // sum(x) per chunk of the slice and activation row (all 16 columns equal)
+  // Per chunk c of the slice and activation row m: sum(x) and sum(x * bias)
+  // (kBias2), in the A layout of v_mfma_f32_16x16x4f32 (lane (qd, r16): row
+  // m = r16, chunk qd).  x is the B operand here; A row 4 c holds ones and
+  // row 4 c + 1 the biases, so D row 4 c + e, column m, is chunk c's sum e.
   constexpr f16x8 kOnes = {1, 1, 1, 1, 1, 1, 1, 1};
-  f32x4 xs[CPW][MT];
+  constexpr f16x8 kZero = {0, 0, 0, 0, 0, 0, 0, 0};
+  const f16x8 arow = (r16 & 3) == 0 ? kOnes : ((r16 & 3) == 1 ? kBias2 : kZero);
+  float sx[MT], sb[MT];  // this lane's sum(x), sum(x * bias): row 16 mt + r16, chunk qd
+  {
+    f32x4 sums[MT];
 #pragma unroll
-  for (int c = 0; c < CPW; ++c)
+    for (int mt = 0; mt < MT; ++mt) sums[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const f16x8 ac = (r16 >> 2) == c ? arow : kZero;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sums[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, xa[c][mt][j], sums[mt], 0, 0, 0);
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      xs[c][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        xs[c][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c][mt][j], kOnes, xs[c][mt], 0, 0, 0);
+      sx[mt] = sums[mt][0];
+      sb[mt] = sums[mt][1];
     }
-  const uint32_t magic = opaque(0x54005400u);
+  }
+  const uint32_t m1024 = opaque(0x64006400u), m64 = opaque(0x54005400u);
   __syncthreads();  // scales and offsets staged
 
   for (int qb = 0; qb < nq; qb += P) {  // U tiles per round (wave-uniform)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = qb / kPPT + u;  // local tile
-      f32x4 acc[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
       const uint32_t* so_row = so_lds + (t * 16 + r16) * sstride;
+      // The tile starts from its slice's offset terms, the sum over its
+      // chunks c of o_c sum(x)_c - s_c sum(x * bias)_c, as two fp32
+      // products with K = the chunks: lane (qd, r16) brings row r16's o and
+      // -s of chunk qd.
+      f32x4 acc[MT];
+      {
+        const uint32_t so = qd < CPW ? so_row[(c0 + qd) >> a.gq_shift] : 0u;
+        const float o = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16)));
+        const float ns = -static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[mt], o, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sb[mt], ns, acc[mt], 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int p = 0; p < kPPT; ++p) {
         const int s = u * kPPT + p;
@@ -891,20 +939,20 @@ __global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_ks
               static_cast<int>(low ? ring[s][1][e] : ring[s][0][e]), 0x128, 0xF, 0xF, false));  // row_ror:8
         }
         fetch(s, qb + s + P);
-        __builtin_amdgcn_sched_barrier(0x78F);  // only vector-memory instructions stay put
+        // Nothing crosses: left free, the scheduler hoisted the products of
+        // later pairs above the refills and the ring drained once per round.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int c = 2 * p + h;
           const uint32_t so = so_row[(c0 + c) >> a.gq_shift];
           const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so)));
-          const float of = fmaf(-kCodeBias, sc,
-                                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(so >> 16))));
           f32x4 d[MT];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) d[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const f16x8 q = codes_f16(words[h][j], magic);
+            const f16x8 q = codes_f16_2m(words[h][j], m1024, m64);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
               d[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c][mt][j], q, d[mt], 0, 0, 0);
@@ -912,7 +960,7 @@ __global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_ks
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(of, xs[c][mt][e], fmaf(sc, d[mt][e], acc[mt][e]));
+            for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(sc, d[mt][e], acc[mt][e]);
         }
       }
 #pragma unroll
