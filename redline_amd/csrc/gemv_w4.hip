@@ -119,7 +119,7 @@ constexpr float kCodeBias = 64.0f;
 // 64 + q, so the word needs one shift: (q0, q4) and (q2, q6) take magic
 // m1024, (q1, q5) and (q3, q7) m64 -- the same element order as codes_f16.
 // The biases leave through sum(x * kBias2) per chunk.  The larger bias costs
-// fp32 sum bits (the kernel's relative error grows from ~1e-6 to ~1e-5 at
+// fp32 sum bits (the kernel's relative error grows from ~1.5e-6 to ~2e-5 at
 // k = 4096; the fp32-output bound is 1e-4).
 __device__ __forceinline__ f16x8 codes_f16_2m(uint32_t word, uint32_t m1024, uint32_t m64) {
   const uint32_t w8 = word >> 8;

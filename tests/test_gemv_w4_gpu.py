@@ -169,6 +169,27 @@ def test_gemv_w4_kslice_llama_gate_up(torch_cuda, cfg, m):
     assert_close_f16(got, oracle.gemv_w4a16_swiglu(x, packed, s, o, g), what="llama kslice")
 
 
+@pytest.mark.parametrize("m", [9, 32])
+def test_gemv_w4_kslice_fp32_k4096_row_scales(torch_cuda, m):
+    """fp32 output of the default kernel above m = 8 at k = 4096 (the
+    Llama-3.1-8B hidden size), activation rows scaled from 1e-3 to 1e3: its
+    codes carry a bias of 1024 on half the elements, which the per-chunk
+    sum(x * bias) takes out again in fp32, so each row's error stays relative
+    to that row.  Every row within the reference's 1e-4 of its own largest
+    output."""
+    torch = torch_cuda
+    say(f"gemv_w4 kslice fp32 k=4096 row scales m={m}")
+    rng = np.random.default_rng(500 + m)
+    n, k, g = 1024, 4096, 128
+    packed, s, o, _ = int4_linear(rng, n, k, g, dense=False)
+    scales = np.logspace(-3, 3, m).astype(np.float32)
+    x = (randn_f16(rng, (m, k)).astype(np.float32) * scales[:, None]).astype(np.float16)
+    want = oracle.gemv_w4a16(x, packed, s, o, g)
+    got = run_gemv(torch, x, packed, s, o, g, f32=True)
+    for r in range(m):
+        assert rel_max_err(got[r], want[r]) <= 1e-4, (r, rel_max_err(got[r], want[r]))
+
+
 @pytest.mark.parametrize("m", [9, 17])
 def test_gemv_w4_kslice_tiles_cut_to_lds(torch_cuda, m):
     """The default (K-slice) kernel above m = 8 at a shape whose partial sums
