@@ -201,26 +201,77 @@ __device__ __forceinline__ int step_dim(int step, int j) {
   return kInt8 ? 64 * (step / 2) + 16 * j + 8 * (step % 2) : 32 * step + 8 * j;
 }
 
+// FP16 K rows through whole-line loads: the two loads of one 128-byte line
+// of the tile's 16 rows take 8 rows each -- lanes r < 8 fetch their own
+// row's first half-line and row r + 8's second, lanes r >= 8 row r - 8's
+// second half and their own first -- and keys_exchange hands each second
+// half to its row's lane (DPP row_ror:8).  FP16: 104.3 -> 103.3 us at C2.
+// The INT8 form, bound by its instruction stream, keeps the half-line loads
+// (the exchange cost it 59.0 -> 59.8 us).  Ordinary loads either way: with
+// the streaming hint the whole-line form took 111 / 68.6 us.
+template <int D, bool kInt8>
+constexpr bool kKeysFull = !kInt8 && D * 2 >= 128;
+
 template <int D, bool kInt8, bool kClamp>
 __device__ __forceinline__ void issue_keys(KBatch<D, kInt8>& kb, const void* base,
                                            const int* cells, int n, const LaneCoord& c) {
   __builtin_amdgcn_sched_barrier(0);  // as in issue_rows
   const int lane = c.tid % kWave, r = lane % 16, j = lane / 16;
   constexpr int kRowBytes = D * (kInt8 ? 1 : 2);
+  if constexpr (kKeysFull<D, kInt8>) {
+    const bool low = r < 8;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int key = mma_key<D>(c, t, r);
-    const uint32_t cell = cells[kClamp ? min(key, n - 1) : key];  // cells are >= 0
-    const char* row = static_cast<const char*>(base) + 16 * j + static_cast<uint64_t>(cell) * kRowBytes;
-    // Ordinary (temporal) loads: an instruction takes 64 bytes of each of 16
-    // rows, half of a cache line, and the next one takes the other half;
-    // with the streaming hint the second half was fetched again (the V rows,
-    // read as whole lines, keep it).
+    for (int t = 0; t < 2; ++t) {
+      const int k0 = mma_key<D>(c, t, low ? r : r - 8), k1 = mma_key<D>(c, t, low ? r + 8 : r);
+      const uint32_t c0 = cells[kClamp ? min(k0, n - 1) : k0], c1 = cells[kClamp ? min(k1, n - 1) : k1];
+      const char* r0 = static_cast<const char*>(base) + static_cast<uint64_t>(c0) * kRowBytes + 16 * j + (low ? 0 : 64);
+      const char* r1 = static_cast<const char*>(base) + static_cast<uint64_t>(c1) * kRowBytes + 16 * j + (low ? 64 : 0);
 #pragma unroll
-    for (int x = 0; x < KBatch<D, kInt8>::kLoads; ++x)
-      kb.r[t][x] = *reinterpret_cast<const u32x4*>(row + 64 * x);
+      for (int L = 0; L < KBatch<D, kInt8>::kLoads / 2; ++L) {
+        kb.r[t][2 * L] = *reinterpret_cast<const u32x4*>(r0 + 128 * L);
+        kb.r[t][2 * L + 1] = *reinterpret_cast<const u32x4*>(r1 + 128 * L);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key = mma_key<D>(c, t, r);
+      const uint32_t cell = cells[kClamp ? min(key, n - 1) : key];  // cells are >= 0
+      const char* row = static_cast<const char*>(base) + 16 * j + static_cast<uint64_t>(cell) * kRowBytes;
+      // Ordinary (temporal) loads: an instruction takes 64 bytes of each of
+      // 16 rows, half of a cache line, and the next one takes the other
+      // half; with the streaming hint the second half was fetched again
+      // (INT8: 75.5 -> 62.0 us with ordinary loads).
+#pragma unroll
+      for (int x = 0; x < KBatch<D, kInt8>::kLoads; ++x)
+        kb.r[t][x] = *reinterpret_cast<const u32x4*>(row + 64 * x);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// The K rows in the matrix-core layout (lane (j, r): pieces [64 x + 16 j,
+// +16) of row r) from the whole-line loads of issue_keys.
+template <int D, bool kInt8>
+__device__ __forceinline__ KBatch<D, kInt8> keys_exchange(const KBatch<D, kInt8>& kb, const LaneCoord& c) {
+  if constexpr (!kKeysFull<D, kInt8>) {
+    return kb;
+  } else {
+    const bool low = (c.tid % 16) < 8;
+    KBatch<D, kInt8> out;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int L = 0; L < KBatch<D, kInt8>::kLoads / 2; ++L)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t a = kb.r[t][2 * L][e], b = kb.r[t][2 * L + 1][e];
+          out.r[t][2 * L][e] = low ? a : b;
+          out.r[t][2 * L + 1][e] = static_cast<uint32_t>(
+              __builtin_amdgcn_mov_dpp(static_cast<int>(low ? b : a), 0x128, 0xF, 0xF, false));  // row_ror:8
+        }
+    return out;
+  }
 }
 
 // v of lane `g` of each row of 16, to the whole row (DPP row_newbcast)
@@ -258,7 +309,7 @@ struct PvOperand<D, G, true> {
 // v_dot2_f32_f16.  `then` runs once the K rows are consumed (the persistent
 // form requests the next unit's K rows into the same registers there).
 template <int D, int G, bool kInt8, bool kMma, class Then>
-__device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _Float16* qs,
+__device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb_in, const _Float16* qs,
                                             const float* ksc, const float* vsc, float scale, int n,
                                             const LaneCoord& c, PvOperand<D, G, kMma>& po,
                                             float (&stat)[kWaves][G][2], Then then) {
@@ -271,6 +322,7 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
   // instead of a subtract per pair of codes
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const KBatch<D, kInt8> kr = keys_exchange<D, kInt8>(kb_in, c);
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) {
     f16x8 qb = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -280,10 +332,10 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb, const _
     for (int t = 0; t < 2; ++t) {
       f16x8 a;
       if constexpr (kInt8) {
-        const u32x4 w = kb.r[t][st / 2];
+        const u32x4 w = kr.r[t][st / 2];
         a = int8x8_to_f16_biased(st % 2 ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
       } else {
-        a = __builtin_bit_cast(f16x8, kb.r[t][st]);
+        a = __builtin_bit_cast(f16x8, kr.r[t][st]);
       }
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb, acc[t], 0, 0, 0);
     }
