@@ -978,6 +978,138 @@ __global__ __launch_bounds__((64 * kslice_max_waves<CPW, MT>())) void gemv_w4_ks
   }
 }
 
+// The INT8 weights' K-slice kernel (gemv_w8a16 from m = 8 on): the INT4
+// K-slice kernel's decomposition over an int8 [n, k] with one scale per row.
+// Wave w owns K slice w (CPW lines of 128 K = 128 bytes of each row) of the
+// workgroup's T tiles; a line of the tile's 16 rows comes as the pair
+// kernel's two full-line loads and DPP hand-over, so a lane holds 16 codes of
+// its row at bytes 16 qd (MFMA steps 0, 1) and 64 + 16 qd (steps 2, 3):
+// step s covers K 64 (s / 2) + 16 qd + 8 (s % 2) .. + 7, the A operand x in
+// that (natural) order.  Codes enter the MFMAs biased (1152 + code, 6 VALU
+// per 8 codes, int8x8_to_f16_biased); each tile's sum starts from -1152
+// sum(x) of the slice, so the products leave x . code.  The row scale and
+// the bias apply once, to the reduced sum (gemv_weight_only.cu:36).
+template <int CPW, int U, int MT, int MODE>
+__global__ __launch_bounds__(64 * kMaxWaves) void gemv_w8_kslice_kernel(W4Args a) {
+  constexpr int P = CPW * U;  // ring depth in lines: U tiles
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int threads = blockDim.x, nw = threads / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, qd = lane >> 4;
+  const bool low = (lane & 8) == 0;
+  const int T = a.cpp;  // tiles per workgroup, a multiple of U
+  const int ntiles = a.n / 16;
+  const int tile0 = blockIdx.x * T;
+  f32x4* red = reinterpret_cast<f32x4*>(lds);  // [T][nw][MT][64 lanes]
+  const int kb = a.k;
+  const int l0 = wave * CPW;  // first line of this wave's slice
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.w), 0, static_cast<int>(static_cast<uint32_t>(a.n) * static_cast<uint32_t>(kb)),
+      kBufferFlags);
+  const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, 0, kBufferFlags);
+  const int pc0 = (low ? qd : 4 + qd) * 16, pc1 = (low ? 4 + qd : qd) * 16;
+  const int vo0 = (low ? r16 : r16 - 8) * kb + pc0;
+  const int vo1 = (low ? r16 + 8 : r16) * kb + pc1;
+  const int nq = T * CPW;  // (tile, line) steps of this wave
+  u32x4 ring[P][2];
+  auto fetch = [&](int s, int q) {
+    const int t = tile0 + q / CPW;
+    const __amdgpu_buffer_rsrc_t res = (q < nq && t < ntiles) ? wres : none;
+    const int soff = t * 16 * kb + (l0 + q % CPW) * 128;
+    ring[s][0] = __builtin_amdgcn_raw_buffer_load_b128(res, vo0, soff, kNtLoad);
+    ring[s][1] = __builtin_amdgcn_raw_buffer_load_b128(res, vo1, soff, kNtLoad);
+  };
+
+  // x of the slice in the A layout above, staged as in the INT4 kernel
+  // (16 rows x 256 bytes per line and activation tile, whole-line loads,
+  // read back transposed from the wave's own LDS rows)
+  f16x8 xa[CPW][MT][4];
+  {
+    constexpr int kXRow = 272;
+    uint8_t* xst = lds + wave * 16 * kXRow;
+    const int lr = lane / 16, lc = (lane % 16) * 16;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[i] = load16(reinterpret_cast<const uint8_t*>(
+                            a.x + static_cast<size_t>(min(16 * mt + 4 * i + lr, a.m - 1)) * a.k +
+                            (l0 + c) * 128) + lc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<u32x4*>(xst + (4 * i + lr) * kXRow + lc) = v[i];
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+          xa[c][mt][st] = __builtin_bit_cast(
+              f16x8, *reinterpret_cast<const u32x4*>(xst + r16 * kXRow + 128 * (st >> 1) + 32 * qd + 16 * (st & 1)));
+      }
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) fetch(p, p);
+  // -1152 sum(x) of the slice per activation row (all 16 columns equal)
+  const f16x8 kM1152 = {-1152, -1152, -1152, -1152, -1152, -1152, -1152, -1152};
+  f32x4 base[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    base[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        base[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c][mt][st], kM1152, base[mt], 0, 0, 0);
+  }
+  __syncthreads();  // every wave is done with its staging rows (they hold partial sums next)
+
+  for (int qb = 0; qb < nq; qb += P) {  // U tiles per round (wave-uniform)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = qb / CPW + u;  // local tile
+      f32x4 acc[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = base[mt];
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) {
+        const int s = u * CPW + c;
+        u32x4 words[2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          words[0][e] = low ? ring[s][0][e] : ring[s][1][e];
+          words[1][e] = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(
+              static_cast<int>(low ? ring[s][1][e] : ring[s][0][e]), 0x128, 0xF, 0xF, false));  // row_ror:8
+        }
+        fetch(s, qb + s + P);
+        __builtin_amdgcn_sched_barrier(0);  // the refill stays where it is issued
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const u32x4 w = words[st >> 1];
+          const f16x8 q = int8x8_to_f16_biased((st & 1) ? u32x2{w.z, w.w} : u32x2{w.x, w.y});
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c][mt][st], q, acc[mt], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((t * nw + wave) * MT + mt) * kWave + lane] = acc[mt];
+    }
+  }
+  __syncthreads();  // every slice's partial of every tile is in LDS
+  for (int t = wave; t < T; t += nw) {
+    const int row = (tile0 + t) * 16 + r16;
+    if (tile0 + t >= ntiles) break;
+    const float sc = static_cast<float>(__builtin_bit_cast(_Float16, a.scales[row]));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 sum = red[((t * nw) * MT + mt) * kWave + lane];
+      for (int w = 1; w < nw; ++w) sum += red[((t * nw + w) * MT + mt) * kWave + lane];
+      store_tile<MODE>(a, sum * sc, 16 * mt + 4 * qd, row, r16);
+    }
+  }
+}
+
 // LDS a workgroup may take: the device allows 160 KiB per workgroup.
 constexpr size_t kLdsBudget = 160 * 1024;
 constexpr int kNoFit = 1;  // launch(): the policy's smallest x pass exceeds the LDS budget
@@ -1220,18 +1352,58 @@ int gemv_w4(const char* what, const uint16_t* x, int m, const uint8_t* w, const 
   return st != RLK_OK ? st : launch_status(what);
 }
 
-// INT8 weight-only GEMV (gemv_weight_only.cu:64-93): the pair kernel's INT8
-// form with P = 4 pairs in flight (measured at the Llama-3.1-8B gate_up shape,
-// m = 1..32: equal to or faster than 2 and 8); RLK_TUNE_W8_CFG = 1, 2, 3
-// selects P = 2, 4, 8 for sweeps.
+// The INT8 K-slice kernel's launch: nw = k / 128 / CPW waves (at most 8), T
+// tiles per workgroup -- about one workgroup per compute unit, fewer when
+// their partials would not fit the LDS budget.
+template <int CPW, int U, int MT, int MODE>
+int launch_kslice_w8(W4Args a, hipStream_t stream) {
+  if (a.n % 16 != 0 || a.k % (128 * CPW) != 0 || a.k / (128 * CPW) > kMaxWaves) return kNoFit;
+  const int nw = a.k / (128 * CPW);
+  const int ntiles = a.n / 16;
+  const int cus = compute_units();
+  auto lds_for = [&](int t) {  // the partial sums, which double as the x staging rows
+    return std::max(static_cast<size_t>(t) * nw * MT * kWave * sizeof(f32x4),
+                    static_cast<size_t>(nw) * 16 * 272);
+  };
+  int T = (ntiles + cus - 1) / cus;
+  T = (T + U - 1) / U * U;
+  while (T > U && lds_for(T) > kLdsBudget) T -= U;
+  if (lds_for(T) > kLdsBudget) return kNoFit;
+  a.cpp = T;
+  const size_t lds = lds_for(T);
+  auto kernel = gemv_w8_kslice_kernel<CPW, U, MT, MODE>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = grant_dynamic_lds(reinterpret_cast<const void*>(kernel), kLdsBudget);
+    if (e != hipSuccess)
+      return fail(RLK_EUNSUPPORTED, "gemv_w8a16: %zu bytes of LDS refused (%s)", lds,
+                  hipGetErrorString(e));
+  }
+  kernel<<<(ntiles + T - 1) / T, 64 * nw, lds, stream>>>(a);
+  return RLK_OK;
+}
+
+// INT8 weight-only GEMV (gemv_weight_only.cu:64-93): the K-slice kernel with
+// one tile's lines in flight where it fits (rows in whole tiles, K a multiple
+// of 512 up to 4096: at the Llama-3.1-8B gate_up shape 23.2 / 23.4 / 23.6 /
+// 26.4 us at m = 1 / 8 / 16 / 32 against 25.0 / 25.7 / 26.5 / 30.7 for the
+// pair kernel, same run), else the pair kernel's INT8 form with P = 4 pairs
+// in flight (equal to or faster than 2 and 8).  RLK_TUNE_W8_CFG = 1, 2, 3
+// selects the pair kernel with P = 2, 4, 8, and 4, 5, 6 the K-slice kernel
+// with (lines per slice, tiles in flight) = (4, 1), (4, 2), (2, 2).
 template <int MT, int MODE>
 int dispatch_w8(const W4Args& a, hipStream_t s) {
+  int st = kNoFit;
   switch (tune_knob(kW8Cfg, 0)) {
     case 1: return launch_pairs<2, MT, MODE, true>(a, s);
     case 2: return launch_pairs<4, MT, MODE, true>(a, s);
     case 3: return launch_pairs<8, MT, MODE, true>(a, s);
-    default: return launch_pairs<4, MT, MODE, true>(a, s);
+    case 4: st = launch_kslice_w8<4, 1, MT, MODE>(a, s); break;
+    case 5: st = launch_kslice_w8<4, 2, MT, MODE>(a, s); break;
+    case 6: st = launch_kslice_w8<2, 2, MT, MODE>(a, s); break;
+    default: st = launch_kslice_w8<4, 1, MT, MODE>(a, s); break;
   }
+  if (st == kNoFit) st = launch_pairs<4, MT, MODE, true>(a, s);
+  return st;
 }
 
 int gemv_w8(const uint16_t* x, int m, const int8_t* w, const uint16_t* scales, const uint16_t* bias,

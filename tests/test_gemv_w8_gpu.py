@@ -92,7 +92,7 @@ def test_gemv_w8_llama_projections(torch_cuda, n, k, m):
     assert_close_f16(got, want, what="llama w8")
 
 
-@pytest.mark.parametrize("cfg", range(4))
+@pytest.mark.parametrize("cfg", range(7))
 def test_gemv_w8_launch_policies_agree(torch_cuda, cfg):
     say(f"gemv_w8 cfg={cfg}")
     rng = np.random.default_rng(cfg)
@@ -104,6 +104,30 @@ def test_gemv_w8_launch_policies_agree(torch_cuda, cfg):
         with tune_knob("RLK_TUNE_W8_CFG", cfg):
             got = run_w8(torch_cuda, x, q, s, None, True)
         assert rel_max_err(got, want) <= 1e-4, m
+
+
+@pytest.mark.parametrize("cfg", [4, 5, 6])
+@pytest.mark.parametrize("n,k", [(592, 1024), (12368, 512), (160, 2048), (14336, 4096)])
+@pytest.mark.parametrize("m", [1, 9, 17, 32])
+def test_gemv_w8_kslice_shapes(torch_cuda, cfg, n, k, m):
+    """The INT8 K-slice kernel (each wave one K slice of 512 or 256 codes of
+    every tile of its workgroup, codes biased by 1152 and taken out through
+    the slice's sum of x) on the shapes it takes: rows in whole 16-row tiles,
+    K a whole number of slices (the others fall back to the pair kernel);
+    one tile per workgroup and several, the last workgroup partial.  fp32
+    with a bias at the reference's bound, and fp16."""
+    say(f"gemv_w8 kslice cfg={cfg} n={n} k={k} m={m}")
+    rng = np.random.default_rng(cfg * 1000 + m + k)
+    q = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    s = rng.uniform(0.001, 0.01, n).astype(np.float16)
+    bias = randn_f16(rng, (n,), 0.02)
+    x = randn_f16(rng, (m, k))
+    want = oracle.gemv_w8a16(x, q, s, bias)
+    with tune_knob("RLK_TUNE_W8_CFG", cfg):
+        got = run_w8(torch_cuda, x, q, s, bias, True)
+        got16 = run_w8(torch_cuda, x, q, s, bias, False)
+    assert rel_max_err(got, want) <= 1e-4
+    assert_close_f16(got16, want, what="w8 kslice f16")
 
 
 def test_gemv_w8_deterministic_and_errors(torch_cuda):
