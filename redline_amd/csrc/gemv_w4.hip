@@ -13,7 +13,6 @@
 //   * each lane holds 8 codes of its weight row per step (4 bytes), turned
 //     into exact fp16 values 64 + q by OR-ing each nibble into the mantissa of
 //     64.0 -- one VALU op per two codes plus shifts, no converts;
-//   * an MFMA against an all-ones B gives sum(x) per activation row;
 //   * once per scale window (a K range inside one quantisation group) the fp32
 //     partial is folded in as acc += s * (x . (64 + q)) + (o - 64 s) * sum(x)
 //     -- the reference's s * sum(x q) + o * sum(x) -- so the codes are never
@@ -24,20 +23,25 @@
 // activations are permuted to the nibble order (0, 4, 1, 5, 2, 6, 3, 7) that
 // the code unpacking produces.
 //
-// Work split.  Activations are the expensive operand to fetch: every weight
-// tile needs all of x, and per-wave x loads (16 rows x 64 bytes per load
-// instruction) cost more than the weights themselves -- the load path pays per
-// cache line an instruction touches, not per byte.  So a workgroup stages x
-// once in LDS, already permuted, and all its waves read their A fragments
-// from there; the grid is sized to about one workgroup per compute unit, so x
-// is staged about once per CU.  Each wave owns one 16-row tile over the full K
-// (K-split ways S > 1 are a tuning option) and keeps a P-deep ring of
-// non-temporal weight loads in flight, started before the staging so that both
-// overlap.  Scales and offsets of the workgroup's rows are staged in LDS too,
-// for the same per-line reason.  When x does not fit the LDS budget, K is
-// walked in passes (x re-staged per pass, accumulators kept).  128-K chunks
-// (group_size % 128 == 0, the common case) are one scale window each; other
-// group sizes (32, 64, 96, ...) use 32-K chunks.
+// Kernels (the launch policy picks by m and shape; the kernels' own comments
+// give the details):
+//   * the pair kernel (m < 8): a workgroup stages x once in LDS, already
+//     permuted, with sum(x) per chunk and row taken during the staging, and
+//     each wave walks one 16-row tile over the full K with a ring of chunk
+//     pairs in flight, loaded as full 128-byte lines (8 rows per load
+//     instruction) and handed to the owning lanes by a DPP row rotation.
+//     Activations are the expensive operand to fetch -- the load path pays
+//     per cache line an instruction touches -- so x is staged once per CU;
+//   * the K-slice kernel (m >= 8): wave w owns K slice w of every tile of its
+//     workgroup, so it needs only its slice of x, in registers; codes take
+//     two magics (codes_f16_2m) and the offset terms enter per tile as fp32
+//     MFMAs; partials meet in LDS in a fixed order;
+//   * the slab kernel for the remaining shapes (odd chunk counts, group sizes
+//     whose /128 is not a power of two, 32-K chunks).
+// The pair and slab kernels walk K in x passes when x does not fit the LDS
+// budget (x re-staged per pass, accumulators kept).
+// The INT8 weight-only GEMV (gemv_w8a16) runs the K-slice decomposition too
+// (gemv_w8_kslice_kernel), or the pair kernel's INT8 form.
 #include <algorithm>
 #include <type_traits>
 #include <utility>
