@@ -77,6 +77,16 @@ __device__ __forceinline__ TokenMeta<D> token_meta(const RopeArgs& a, int pos, i
   return m;
 }
 
+// The extension's QKV bias: fp16(x + b) per element.  The exact sum of two
+// fp16 values fits a double, and its rounding to fp16 equals the rounding of
+// the fp32 sum (an fp32 rounding happens only when the operands' exponents
+// differ by more than 13, and then the smaller is below a quarter of the
+// larger's fp16 spacing), so one packed fp16 add per pair of elements gives
+// fp16(float(x) + float(b)) exactly.
+__device__ __forceinline__ u32x4 add_bias(u32x4 v, u32x4 b) {
+  return __builtin_bit_cast(u32x4, __builtin_bit_cast(f16x8, v) + __builtin_bit_cast(f16x8, b));
+}
+
 // One head h of a token row: the lane's 8 pairs (v0 = elements p0..p0+7,
 // v1 = the partners D/2 later) are biased, rotated (q, k) and stored back in
 // place (q) or into the KV cell of the token's slot (k, v; FP16 or INT8 with
@@ -90,10 +100,6 @@ __device__ __forceinline__ void rope_head(const RopeArgs& a, _Float16* hp, int h
   constexpr int kLPH = kHalf / 8;
   f32x8 x0 = unpack8(v0);
   f32x8 x1 = unpack8(v1);
-  if (a.bias != nullptr) {  // extension: QKV bias, fp16-rounded sum
-    x0 = round_f16(x0 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + p0)));
-    x1 = round_f16(x1 + unpack8(*reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0)));
-  }
   if (h < a.hq + a.hkv) {  // q and k heads rotate; v passes through
     const f32x8 y0 = x0 * m.c - x1 * m.s;
     const f32x8 y1 = x1 * m.c + x0 * m.s;
@@ -176,7 +182,54 @@ __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t t, int wav
       v0 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + p0));
       v1 = ld16<NT>(reinterpret_cast<const u32x4*>(hp + kHalf + p0));
     }
+    if (a.bias != nullptr) {  // extension: QKV bias
+      v0 = add_bias(v0, *reinterpret_cast<const u32x4*>(a.bias + h * D + p0));
+      v1 = add_bias(v1, *reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0));
+    }
     rope_head<D, kInt8>(a, hp, h, p0, v0, v1, m);
+  }
+}
+
+// With a QKV bias: K tokens per workgroup, one head per lane group (the
+// heads fit the workgroup's waves), so each lane loads its head's bias once
+// and keeps it for the K tokens.  The bias costs what the activation loads
+// do in the load path -- a load instruction of a wave touches 8 lines, one
+// per head -- though every byte of it hits in cache: without the bias loads
+// the C5 call takes 49.4 us, with them 52.2.  Two tokens per workgroup halve
+// them but lose more elsewhere (52.9 us).
+template <int D, bool kInt8, int WPT, int K>
+__global__ __launch_bounds__(kWave * WPT) void rope_kv_bias_kernel(RopeArgs a) {
+  constexpr bool NT = true;
+  constexpr int kHalf = D / 2;
+  constexpr int kLPH = kHalf / 8;
+  constexpr int kHeadsPerWave = kWave / kLPH;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int h = wave * kHeadsPerWave + lane / kLPH;
+  const int p0 = (lane % kLPH) * 8;
+  const int heads = a.hq + 2 * a.hkv;
+  if (h >= heads) return;  // whole heads: every lane of a head leaves together
+  const u32x4 b0 = *reinterpret_cast<const u32x4*>(a.bias + h * D + p0);
+  const u32x4 b1 = *reinterpret_cast<const u32x4*>(a.bias + h * D + kHalf + p0);
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * K;
+  const int nt = static_cast<int>(min(static_cast<int64_t>(K), a.num_tokens - t0));
+  // every token's loads first (distinct rows: the in-place q stores of one
+  // token cannot alias the next token's loads), then the tokens in order
+  u32x4 v[K][2];
+  TokenMeta<D> m[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (j < nt) {
+      const u32x4* hp = reinterpret_cast<const u32x4*>(a.qkv + ((t0 + j) * heads + h) * D);
+      v[j][0] = ld16<NT>(reinterpret_cast<const u32x4*>(reinterpret_cast<const _Float16*>(hp) + p0));
+      v[j][1] = ld16<NT>(reinterpret_cast<const u32x4*>(reinterpret_cast<const _Float16*>(hp) + kHalf + p0));
+      m[j] = token_meta<D>(a, a.positions[t0 + j], a.slots[t0 + j], p0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (j < nt)
+      rope_head<D, kInt8>(a, a.qkv + ((t0 + j) * heads + h) * D, h, p0, add_bias(v[j][0], b0),
+                          add_bias(v[j][1], b1), m[j]);
   }
 }
 
@@ -252,6 +305,38 @@ int rope_launch(uint16_t* qkv, const int32_t* positions, const int32_t* slot_map
   const int heads = num_heads + 2 * kv->num_kv_heads;
   const int heads_per_wave = kWave / (kv->head_dim / 16);
   int wpt = (heads + heads_per_wave - 1) / heads_per_wave;
+  // With a bias and every head in one pass: rope_kv_bias_kernel, one token
+  // per workgroup (RLK_TUNE_ROPE_BIAS_TOK: 2 tokens, or 0 for the general
+  // kernel; C5: 52.2 us against 52.9 and 52.6)
+  const int kb = tune_knob(kRopeBiasTok, 1);
+  if (bias != nullptr && kb > 0 && wpt <= 8 && tune_knob(kRopeWpt, 0) == 0) {
+    const bool i8 = kv->dtype == RLK_KV_INT8;
+    auto go = [&](auto kernel, int k) {
+      kernel<<<(num_tokens + k - 1) / k, wpt * kWave, 0, stream>>>(a);
+    };
+#define RLK_ROPE_BIAS_CASE(W)                                                                   \
+  case W:                                                                                       \
+    if (kv->head_dim == 128) {                                                                  \
+      if (kb >= 2) i8 ? go(rope_kv_bias_kernel<128, true, W, 2>, 2) : go(rope_kv_bias_kernel<128, false, W, 2>, 2); \
+      else i8 ? go(rope_kv_bias_kernel<128, true, W, 1>, 1) : go(rope_kv_bias_kernel<128, false, W, 1>, 1); \
+    } else {                                                                                    \
+      if (kb >= 2) i8 ? go(rope_kv_bias_kernel<64, true, W, 2>, 2) : go(rope_kv_bias_kernel<64, false, W, 2>, 2); \
+      else i8 ? go(rope_kv_bias_kernel<64, true, W, 1>, 1) : go(rope_kv_bias_kernel<64, false, W, 1>, 1); \
+    }                                                                                           \
+    return launch_status(what);
+    switch (wpt) {
+      RLK_ROPE_BIAS_CASE(1)
+      RLK_ROPE_BIAS_CASE(2)
+      RLK_ROPE_BIAS_CASE(3)
+      RLK_ROPE_BIAS_CASE(4)
+      RLK_ROPE_BIAS_CASE(5)
+      RLK_ROPE_BIAS_CASE(6)
+      RLK_ROPE_BIAS_CASE(7)
+      RLK_ROPE_BIAS_CASE(8)
+      default: break;
+    }
+#undef RLK_ROPE_BIAS_CASE
+  }
   wpt = tune_knob(kRopeWpt, wpt < 1 ? 1 : (wpt > 8 ? 8 : wpt));
   if (wpt < 1) wpt = 1;
   if (wpt > 8) wpt = 8;

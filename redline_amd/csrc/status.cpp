@@ -87,7 +87,7 @@ constexpr const char* kKnobNames[kNumKnobs] = {
     "RLK_TUNE_GATHER_BS", "RLK_TUNE_GATHER_NT", "RLK_TUNE_NORM_TPR",   "RLK_TUNE_NORM_NT",
     "RLK_TUNE_SWIGLU_BS", "RLK_TUNE_SWIGLU_NT", "RLK_TUNE_ROPE_WPT",   "RLK_TUNE_ATTN_PERSIST",
     "RLK_TUNE_W4_CFG",    "RLK_TUNE_W8_CFG",    "RLK_TUNE_PREFILL_DMA", "RLK_TUNE_PREFILL_QS",
-    "RLK_TUNE_ATTN_PV",
+    "RLK_TUNE_ATTN_PV",   "RLK_TUNE_ROPE_BIAS_TOK",
 };
 constexpr int kUnset = INT_MIN;
 std::atomic<int> g_knobs[kNumKnobs];

@@ -30,7 +30,7 @@ hipError_t grant_dynamic_lds(const void* kernel, size_t bytes);
 // rlk_set_tune_knob.
 enum Knob {
   kGatherBs, kGatherNt, kNormTpr, kNormNt, kSwigluBs, kSwigluNt, kRopeWpt, kAttnPersist,
-  kW4Cfg, kW8Cfg, kPrefillDma, kPrefillQs, kAttnPv, kNumKnobs
+  kW4Cfg, kW8Cfg, kPrefillDma, kPrefillQs, kAttnPv, kRopeBiasTok, kNumKnobs
 };
 
 // The override of `knob`, or `fallback` when none is set.

@@ -348,6 +348,29 @@ def test_rope_extension_bias_and_fp16_scale(torch_cuda, int8, scale16):
             assert_bits_equal(got.view(cpu.dtype), cpu.reshape(-1)[cells], "scales")
 
 
+@pytest.mark.parametrize("tok", [0, 1, 2])
+@pytest.mark.parametrize("hq,hkv,D,int8", [(28, 4, 128, False), (28, 4, 128, True), (32, 4, 64, False),
+                                           (64, 8, 64, True)])
+def test_rope_bias_token_policies(torch_cuda, tok, hq, hkv, D, int8):
+    """The QKV bias through each launch form (RLK_TUNE_ROPE_BIAS_TOK: 0 the
+    general kernel, 1 and 2 tokens per workgroup with the bias kept in
+    registers), on an odd token count (the last workgroup of the two-token
+    form holds one token) with a skipped slot; bits against the oracle."""
+    from redline_amd._lib import tune_knob
+    say(f"rope bias tok={tok} hq={hq} hkv={hkv} D={D} int8={int8}")
+    bs = 16
+    rng = np.random.default_rng(tok * 7 + hq + D)
+    T = 37
+    nblocks = 2 + T // bs + 2
+    slots = rng.permutation(np.arange(bs, nblocks * bs, dtype=np.int32))[:T]
+    slots[5] = -1
+    pos = rng.integers(0, 4096, T).astype(np.int32)
+    qkv = randn_f16(rng, (T, (hq + 2 * hkv) * D))
+    bias = randn_f16(rng, ((hq + 2 * hkv) * D,), 0.02)
+    with tune_knob("RLK_TUNE_ROPE_BIAS_TOK", tok):
+        run_case(torch_cuda, qkv, pos, slots, hq, hkv, D, nblocks, int8, theta=1e6, bias=bias)
+
+
 def test_rope_extension_null_options_is_plain(torch_cuda):
     torch = torch_cuda
     import ctypes as C
