@@ -949,18 +949,20 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
 // Merges the split-K partials of one (item, head), one lane per output dim
 // (the merge rule of attention.cu:193-210).  A partition's partial row is
 // sum_k e^(s_k - m_i) v_k, not divided by its sum l_i; the output is
-// sum_i e^(m_i - M) row_i / sum_i e^(m_i - M) l_i with M = max_i m_i.  The workspace addresses depend only on the
-// (item, head), so the statistics of the first D partitions and the first
-// kEarly partial rows are requested before the context is known (token ->
-// position is two dependent reads), and masked once the partition count is:
-// the merge then costs about two memory round trips instead of five.
-// Entries past the count are never used (they may hold anything).
+// sum_i e^(m_i - M) row_i / sum_i e^(m_i - M) l_i with M = max_i m_i.  The
+// workspace addresses depend only on the (item, head), so the statistics of
+// the first D partitions and the first kEarly partial rows are requested
+// before the context is known (token -> position is two dependent reads) and
+// masked once the partition count is.  The next kLate rows then go out
+// together, rows past the count re-reading the last one (weight 0), and the
+// rest kUnroll at a time: up to kEarly + kLate partitions cost three memory
+// round trips.  Entries past the count are never used (they may hold anything).
 constexpr int kReduceMaxParts = 4096;  // weights kept in LDS (contexts up to 1M keys)
 
 template <int D>
 __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
-  constexpr int kEarly = 16;  // partial rows requested up front
-  constexpr int kUnroll = 8;  // rows in flight per step past them
+  constexpr int kEarly = 4, kLate = 28;
+  constexpr int kUnroll = 8;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ float wgt[kReduceMaxParts];
@@ -978,6 +980,9 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   const int ctx = p.positions[token] + 1;
   const int num_parts = min((ctx + kPart - 1) / kPart, mp);
   if (num_parts <= 1) return;  // uniform: written directly by the attention kernel
+  float v1[kLate];
+#pragma unroll
+  for (int u = 0; u < kLate; ++u) v1[u] = src[static_cast<int64_t>(min(kEarly + u, num_parts - 1)) * D];
 
   float mx = d < num_parts ? m0 : -FLT_MAX;
   for (int i = d + D; i < num_parts; i += D) mx = fmaxf(mx, w.ws_max[base + i]);
@@ -1010,7 +1015,10 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
 #pragma unroll
   for (int u = 0; u < kEarly; ++u)
     if (u < num_parts) o += wgt[u] * v0[u];
-  int i = kEarly;
+#pragma unroll
+  for (int u = 0; u < kLate; ++u)
+    if (kEarly + u < num_parts) o += wgt[kEarly + u] * v1[u];
+  int i = kEarly + kLate;
   for (; i + kUnroll <= num_parts; i += kUnroll) {
     float v[kUnroll];
 #pragma unroll
