@@ -190,6 +190,53 @@ def test_decode_attention_llama_b32(torch_cuda, int8, attention_form):
     assert_close_f16(got, want, what="attention C2")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("int8", [False, True])
+def test_decode_attention_long_contexts(torch_cuda, D, int8, attention_form):
+    """Contexts past 32 partitions (the merge's batched rows, then its loop)
+    and past D partitions (its statistics loop): 40000, 9000, 8200 and 257
+    keys, 157 / 36 / 33 / 2 partitions, random cache contents."""
+    torch = torch_cuda
+    from redline_amd import kernels as K
+    say(f"attention long contexts D={D} int8={int8} form={attention_form}")
+    hq, hkv, bs = 8, 2, 16
+    ctx = np.array([40000, 9000, 8200, 257])
+    n = len(ctx)
+    nb = (ctx + bs - 1) // bs
+    max_blocks = int(nb.max())
+    rng = np.random.default_rng(17 + D + int8)
+    pool = rng.permutation(np.arange(1, 1 + int(nb.sum()), dtype=np.int32))
+    tables = np.zeros((n, max_blocks), np.int32)  # rows padded with block 0
+    off = 0
+    for i, b in enumerate(nb):
+        tables[i, :b] = pool[off:off + b]
+        off += b
+    cache = K.KVCache(1, 1 + int(nb.sum()), hkv, D, bs, K.KVDType.kINT8 if int8 else K.KVDType.kFP16)
+    k, v, ks, vs = cache.tensors(0)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    if int8:
+        k.copy_(torch.randint(-127, 128, k.shape, generator=g, device="cuda", dtype=torch.int8))
+        v.copy_(torch.randint(-127, 128, v.shape, generator=g, device="cuda", dtype=torch.int8))
+        ks.copy_(torch.rand(ks.shape, generator=g, device="cuda") * 0.02 + 1e-3)
+        vs.copy_(torch.rand(vs.shape, generator=g, device="cuda") * 0.02 + 1e-3)
+    else:
+        k.copy_(torch.randn(k.shape, generator=g, device="cuda").half())
+        v.copy_(torch.randn(v.shape, generator=g, device="cuda").half())
+    stride = (hq + 2 * hkv) * D
+    qkv = randn_f16(rng, (n, stride))
+    pos = (ctx - 1).astype(np.int32)
+    ids = np.arange(n, dtype=np.int32)
+    max_parts = int((ctx.max() + 255) // 256)
+    got = run_attention(torch, K, dev(torch, qkv), stride, hq, 1 / np.sqrt(D), cache,
+                        dev(torch, tables), max_blocks, dev(torch, pos), dev(torch, ids),
+                        dev(torch, ids), n, n, max_parts)
+    want = oracle.paged_attention_decode(
+        qkv, stride, hq, 1 / np.sqrt(D), k.cpu().numpy(), v.cpu().numpy(),
+        None if ks is None else ks.cpu().numpy(), None if vs is None else vs.cpu().numpy(), tables,
+        pos, ids, ids, n, int8)
+    assert_close_f16(got, want, what="attention long contexts")
+
+
 @pytest.mark.parametrize("hq,hkv,D,lens", [(8, 2, 128, [33, 280]), (4, 2, 64, [520]),
                                            (32, 8, 128, [300, 17])])
 def test_decode_attention_int8_fp16_scales(torch_cuda, hq, hkv, D, lens, attention_form):
