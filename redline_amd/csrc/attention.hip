@@ -838,21 +838,18 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   UnitPos nxt = u0 + 1 < u1 ? advance(cur) : cur;
   // INT8 scales of key tid of unit n+1, requested in unit n-1 and written to
   // LDS in unit n (the cells of unit n+2 are written there too)
-  uint32_t sk_next = 0, sv_next = 0;
+  // The first two units' block-table entries and the first q piece go out
+  // together; unit 0's scales reach LDS only after its K/V rows are requested.
+  uint32_t sk_next = 0, sv_next = 0, ks0, vs0;
   {
-    uint32_t ks0, vs0;
-    write_cells<kInt8>(s.cell[0], args, tid, table_entry(p, tid, it_seq[cur.item], cur.part, keys_in(cur)),
-                       cur.part, cur.kvh, ks0, vs0, keys_in(cur));
-    if (kInt8 && tid < kPart) {
-      s.ksc[0][tid] = p.scale * scale_value(ks0, args.scale16);
-      s.vsc[0][tid] = scale_value(vs0, args.scale16);
-    }
+    const int blk0 = table_entry(p, tid, it_seq[cur.item], cur.part, keys_in(cur));
+    const int blk1 = u0 + 1 < u1 ? table_entry(p, tid, it_seq[nxt.item], nxt.part, keys_in(nxt)) : -1;
+    u32x4 q0 = {0, 0, 0, 0};
+    if (q_piece<D, G>(tid)) q0 = load_q_piece<D, G>(p, tid, it_tok[cur.item], cur.kvh);
+    write_cells<kInt8>(s.cell[0], args, tid, blk0, cur.part, cur.kvh, ks0, vs0, keys_in(cur));
+    write_cells<kInt8>(s.cell[1], args, tid, blk1, nxt.part, nxt.kvh, sk_next, sv_next, keys_in(nxt));
+    if (q_piece<D, G>(tid)) store16(s.q[0] + (tid - kPart) * 8, q0);
   }
-  if (u0 + 1 < u1)
-    write_cells<kInt8>(s.cell[1], args, tid, table_entry(p, tid, it_seq[nxt.item], nxt.part, keys_in(nxt)),
-                       nxt.part, nxt.kvh, sk_next, sv_next, keys_in(nxt));
-  if (q_piece<D, G>(tid))
-    store16(s.q[0] + (tid - kPart) * 8, load_q_piece<D, G>(p, tid, it_tok[cur.item], cur.kvh));
   __syncthreads();
 
   KBatch<D, kInt8> kb;
@@ -861,6 +858,13 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     const LaneCoord c = lane_coord<D, !kInt8>();
     issue_keys<D, kInt8, false>(kb, p.kv.k, s.cell[0], keys_in(cur), c);
     issue_rows<D, kInt8, false>(vb, p.kv.v, s.cell[0], keys_in(cur), c);
+  }
+  if constexpr (kInt8) {
+    if (tid < kPart) {
+      s.ksc[0][tid] = p.scale * scale_value(ks0, args.scale16);
+      s.vsc[0][tid] = scale_value(vs0, args.scale16);
+    }
+    __syncthreads();
   }
   for (int u = u0; u < u1; ++u) {
     const int b = (u - u0) & 1;
