@@ -312,7 +312,8 @@ template <int D, int G, bool kInt8, bool kMma, class Then>
 __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb_in, const _Float16* qs,
                                             const float* ksc, const float* vsc, float scale, int n,
                                             const LaneCoord& c, PvOperand<D, G, kMma>& po,
-                                            float (&stat)[kWaves][G][2], Then then) {
+                                            float (&stat)[kWaves][G][2], bool carry, float& cf,
+                                            Then then) {
   constexpr int kSteps = D / 32, kP = Geo<D>::kPasses;
   const int lane = c.tid % kWave, g = lane % 16, rho = lane / 16;
   // q of one MFMA step at a time (B: column g = head g), so only one step's
@@ -362,6 +363,12 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb_in, cons
 #pragma unroll
     for (int x = 1; x < 8; ++x) m = fmaxf(m, e[x / 4][x % 4]);
     m = rows_max<true>(rows_max<false>(m));
+    if (carry) {  // uniform: continue from the wave's (m, l) of the previous partition
+      const float m1 = g < G ? stat[c.wave][g][0] : m;
+      const float mm = fmaxf(m, m1);
+      cf = __expf(m1 - mm);
+      m = mm;
+    }
     l = 0.f;
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
@@ -373,6 +380,7 @@ __device__ __forceinline__ void wave_softmax(const KBatch<D, kInt8>& kb_in, cons
   if (n >= kPart) softmax(std::false_type{});
   else softmax(std::true_type{});
   l = rows_sum<true>(rows_sum<false>(l));
+  if (carry && g < G) l += stat[c.wave][g][1] * cf;
   if (rho == 0 && g < G) {
     stat[c.wave][g][0] = m;
     stat[c.wave][g][1] = l;
@@ -535,7 +543,7 @@ __device__ __forceinline__ void int8_cols_to_f16_biased(const uint32_t (&w)[8], 
 template <int D, int G, bool kInt8, class Then>
 __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const PvOperand<D, G, true>& po,
                                             const LaneCoord& c, float (&red)[kWaves][G][D + kRedPad],
-                                            Then then) {
+                                            bool carry, float cf, Then then) {
   constexpr int kTiles = D / 16;
   const int lane = c.tid % kWave, rho = lane / 16, m = lane % 16;
   f16x8 a[kTiles];
@@ -606,7 +614,8 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * rho + i;
         const int dim = D == 128 ? 8 * r + dt : 8 * (r % 8) + 4 * (r / 8) + dt;
-        red[c.wave][m][dim] = o[i];
+        float& dst = red[c.wave][m][dim];
+        dst = carry ? fmaf(dst, cf, o[i]) : o[i];  // carry: rescale the previous partition's sum
       }
     }
   }
@@ -618,18 +627,22 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
 
 // Combines the waves of a unit: M = max m_w, L = sum e^(m_w - M) l_w,
 // o = sum e^(m_w - M) o_w; written as the output row o / L (one partition)
-// or as the unit's split-K partial row o with its (M, L).  With D a multiple
+// or as the unit's split-K partial row o with its (M, L) in slot `part`.  A
+// unit that ran through partitions part .. part_end marks slots part + 1 ..
+// part_end empty (sum -1, which no sum of exponentials takes; the merge skips
+// them).  With D a multiple
 // of 64 every lane of a wave serves the same head g, so the weights are
 // computed once per wave: lane l takes wave l % 8's statistics, the max is a
 // reduction over 8 lanes, and lanes 0-7 leave e^(m_w - M) and l_w in the
 // wave's own LDS slots `wgt`, which the wave reads back (LDS accesses of one
 // wave complete in order; no barrier).  The sums run in wave order as fmas,
 // so every lane forms the same L and o as a per-lane loop over the waves.
-template <int D, int G>
+template <int D, int G, bool kMark = false>
 __device__ __forceinline__ void combine_waves(const AttnArgs& args, const float (&red)[kWaves][G][D + kRedPad],
                                               const float (&stat)[kWaves][G][2],
                                               float (&wgt)[kWaves][2][kWaves], int tid, int item,
-                                              int token, int num_parts, int part, int kvh) {
+                                              int token, int num_parts, int part, int kvh,
+                                              int part_end = -1) {
   static_assert(kWaves == 8 && D % kWave == 0, "one head per wave, 8 waves per workgroup");
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
@@ -661,6 +674,8 @@ __device__ __forceinline__ void combine_waves(const AttnArgs& args, const float 
         w.ws_max[row] = M;
         w.ws_sum[row] = L;
       }
+      if constexpr (kMark)
+        for (int j = 1 + d; j <= part_end - part; j += D) w.ws_sum[row + j] = -1.f;
     }
   }
 }
@@ -740,19 +755,28 @@ __device__ __forceinline__ int table_entry(const rlk_attention_params& p, int ti
 
 // Persistent form.  Every workgroup first reads each decode item's token,
 // sequence and context into LDS and prefix-sums the partitions per item; the
-// work units (item, partition, kv head) -- only those inside a context -- are
-// then split into contiguous ranges, one per workgroup.  Kv head runs fastest.
-// The INT8 scales of a partition's keys are fetched once, by the threads that
-// resolve its cells, into LDS next to the cells.
+// work units -- only those inside a context -- are then split into contiguous
+// ranges, one per workgroup.  With kSeg (the FP16 MFMA form) the units run
+// (item, kv head, partition), partition fastest, so a range holds runs of
+// consecutive partitions of one (item, kv head): each wave carries its (m, l)
+// and partial output through a run (rescaled by e^(m_prev - M) at each
+// partition), and the waves are combined once per run, into the workspace slot
+// of its first partition; the run's other slots are marked empty.  The other
+// forms run (item, partition, kv head), kv head fastest (a partition's block
+// table entries and neighbouring K/V rows stay together), and combine every
+// unit.  The INT8 scales of
+// a partition's keys are fetched once, by the threads that resolve its cells,
+// into LDS next to the cells.
 //
-// The units of a range are software-pipelined across their two row batches:
+// The partitions of a range are software-pipelined across their two row
+// batches:
 //   wait K(n) -> q . k -> request K(n+1) -> softmax -> wait V(n) -> P . V
-//   -> request V(n+1) -> slot sums -> barrier -> combine, write cells(n+2)
-//   -> barrier
+//   -> request V(n+1) -> slot sums -> barrier -> combine (at a run's end),
+//   write cells(n+2) -> barrier
 // so each batch is requested as soon as its registers are free and one is
 // always in flight while the other is consumed, in the registers a
-// non-pipelined unit needs.  Cells and q of later units are staged in LDS
-// (double-buffered), their block-table entries and q requested a unit ahead.
+// non-pipelined unit needs.  Cells and q of later partitions are staged in
+// LDS (double-buffered), their block-table entries and q requested one ahead.
 constexpr int kMaxItemsLds = 2048;
 
 struct UnitPos {
@@ -761,6 +785,7 @@ struct UnitPos {
 
 template <int D, int G, bool kInt8, bool kMma>
 __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_persistent(AttnArgs args) {
+  constexpr bool kSeg = kMma && !kInt8;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
   __shared__ UnitLds<D, G> s;
@@ -812,32 +837,48 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
   const int chunk = (total + gridDim.x - 1) / gridDim.x;
   const int u0 = blockIdx.x * chunk, u1 = min(u0 + chunk, total);
   if (u0 >= u1) return;
-  // first unit: binary search of its partition among the items
+  // first unit: binary search of its item (item i's units start at it_pfx[i] * hkv)
   const int pu = u0 / hkv;
   int lo = 0, hi = items - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) / 2;
     if (it_pfx[mid] <= pu) lo = mid; else hi = mid - 1;
   }
-  auto advance = [&](UnitPos q) {
-    if (++q.kvh == hkv) {
-      q.kvh = 0;
-      if (++q.part == it_pfx[q.item + 1] - it_pfx[q.item]) {
-        q.part = 0;
-        ++q.item;
-      }
-    }
-    return q;
-  };
   auto keys_in = [&](const UnitPos& q) { return min(kPart, it_ctx[q.item] - q.part * kPart); };
   auto num_parts = [&](const UnitPos& q) {
     return min((it_ctx[q.item] + kPart - 1) / kPart, w.max_partitions);
   };
+  auto advance = [&](UnitPos q) {
+    if constexpr (kSeg) {  // partition fastest
+      if (++q.part == it_pfx[q.item + 1] - it_pfx[q.item]) {
+        q.part = 0;
+        if (++q.kvh == hkv) {
+          q.kvh = 0;
+          ++q.item;
+        }
+      }
+    } else {  // kv head fastest
+      if (++q.kvh == hkv) {
+        q.kvh = 0;
+        if (++q.part == it_pfx[q.item + 1] - it_pfx[q.item]) {
+          q.part = 0;
+          ++q.item;
+        }
+      }
+    }
+    return q;
+  };
 
-  UnitPos cur = {lo, pu - it_pfx[lo], u0 - pu * hkv};
+  UnitPos cur;
+  if constexpr (kSeg) {
+    const int r = u0 - it_pfx[lo] * hkv, np = min((it_ctx[lo] + kPart - 1) / kPart, w.max_partitions);
+    cur = {lo, r - (r / np) * np, r / np};
+  } else {
+    cur = {lo, pu - it_pfx[lo], u0 - pu * hkv};
+  }
   UnitPos nxt = u0 + 1 < u1 ? advance(cur) : cur;
   // INT8 scales of key tid of unit n+1, requested in unit n-1 and written to
-  // LDS in unit n (the cells of unit n+2 are written there too)
+  // LDS in unit n (the cells of unit n+2 are written there too).
   // The first two units' block-table entries and the first q piece go out
   // together; unit 0's scales reach LDS only after its K/V rows are requested.
   uint32_t sk_next = 0, sv_next = 0, ks0, vs0;
@@ -866,6 +907,8 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     }
     __syncthreads();
   }
+  int run_first = cur.part;  // first partition of the current run
+  bool carry = false;        // the previous unit belongs to the same run
   for (int u = u0; u < u1; ++u) {
     const int b = (u - u0) & 1;
     const bool has1 = u + 1 < u1, has2 = u + 2 < u1;
@@ -876,10 +919,13 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
     const int blk2 = has2 ? table_entry(p, c.tid, it_seq[nn.item], nn.part, keys_in(nn)) : -1;
     u32x4 qn = {0, 0, 0, 0};
     if (has1 && q_piece<D, G>(c.tid)) qn = load_q_piece<D, G>(p, c.tid, it_tok[nxt.item], nxt.kvh);
+    // the run ends here unless the next unit is the next partition of this (item, kv head)
+    const bool run_end = !kSeg || !has1 || nxt.item != cur.item || nxt.kvh != cur.kvh;
 
     PvOperand<D, G, kMma> po;
+    float cf = 1.f;
     wave_softmax<D, G, kInt8, kMma>(kb, s.q[b], s.ksc[b], s.vsc[b], p.scale, keys_in(cur), c, po,
-                                    s.stat, [&] {
+                                    s.stat, carry, cf, [&] {
       issue_keys<D, kInt8, false>(kb, p.kv.k, has1 ? s.cell[b ^ 1] : zero_cells, 0, c);
     });
     // q(n+1) goes to the buffer q(n-1) used: free since the barriers of unit n-1
@@ -888,7 +934,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
       issue_rows<D, kInt8, false>(vb, p.kv.v, has1 ? s.cell[b ^ 1] : zero_cells, 0, c);
     };
     if constexpr (kMma) {
-      wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, next_rows);
+      wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, carry, cf, next_rows);
     } else {
       wave_pv<D, G, kInt8>(vb, s.vsc[b], po, c, s.red, next_rows);
     }
@@ -902,9 +948,14 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
       s.vsc[b ^ 1][c.tid] = scale_value(sv_next, args.scale16);
     }
     if (has2) write_cells<kInt8>(s.cell[b], args, c.tid, blk2, nn.part, nn.kvh, sk_next, sv_next, keys_in(nn));
-    combine_waves<D, G>(args, s.red, s.stat, s.wgt, c.tid, cur.item, it_tok[cur.item], num_parts(cur),
-                        cur.part, cur.kvh);
+    if (run_end)  // uniform
+      combine_waves<D, G, kSeg>(args, s.red, s.stat, s.wgt, c.tid, cur.item, it_tok[cur.item],
+                                num_parts(cur), kSeg ? run_first : cur.part, cur.kvh, cur.part);
     __syncthreads();
+    if constexpr (kSeg) {
+      carry = !run_end;
+      run_first = run_end ? nxt.part : run_first;
+    }
     cur = nxt;
     nxt = nn;
   }
@@ -939,9 +990,11 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   issue_keys<D, kInt8, true>(kb, p.kv.k, s.cell[0], n, c);
   issue_rows<D, kInt8, true>(vb, p.kv.v, s.cell[0], n, c);
   PvOperand<D, G, kMma> po;
-  wave_softmax<D, G, kInt8, kMma>(kb, s.q[0], s.ksc[0], s.vsc[0], p.scale, n, c, po, s.stat, [] {});
+  float cf = 1.f;
+  wave_softmax<D, G, kInt8, kMma>(kb, s.q[0], s.ksc[0], s.vsc[0], p.scale, n, c, po, s.stat, false, cf,
+                                  [] {});
   if constexpr (kMma) {
-    wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, [] {});
+    wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, false, cf, [] {});
   } else {
     wave_pv<D, G, kInt8>(vb, s.vsc[0], po, c, s.red, [] {});
   }
@@ -963,9 +1016,13 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
 // round trips.  Entries past the count are never used (they may hold anything).
 constexpr int kReduceMaxParts = 4096;  // weights kept in LDS (contexts up to 1M keys)
 
-template <int D>
+template <int D, bool kRuns>
 __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
-  constexpr int kEarly = 4, kLate = 28;
+  // kRuns: slots absorbed by a persistent workgroup's run hold the sum -1
+  // and take no part (weight marker -1, rows never accumulated); slot 0 is
+  // always a run's own, so only it is requested before the slots' states
+  // are known, and later rows past the count or of absorbed slots re-read it
+  constexpr int kEarly = kRuns ? 1 : 4, kLate = kRuns ? 31 : 28;
   constexpr int kUnroll = 8;
   const rlk_attention_params& p = args.p;
   const rlk_decode_attention_work& w = args.w;
@@ -977,6 +1034,8 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   const float* src = w.ws_out + base * D + d;
   const float m0 = d < mp ? w.ws_max[base + d] : -FLT_MAX;
   const float l0 = d < mp ? w.ws_sum[base + d] : 0.f;
+  // every wave's view of slots 0..63 (wave 0's own l0)
+  const float lw = kRuns && wv > 0 && lane < mp ? w.ws_sum[base + lane] : l0;
   float v0[kEarly];
 #pragma unroll
   for (int u = 0; u < kEarly; ++u) v0[u] = u < mp ? src[static_cast<int64_t>(u) * D] : 0.f;
@@ -984,12 +1043,18 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   const int ctx = p.positions[token] + 1;
   const int num_parts = min((ctx + kPart - 1) / kPart, mp);
   if (num_parts <= 1) return;  // uniform: written directly by the attention kernel
+  // bit j: slot j < 64 holds a partial of its own
+  const uint64_t own = kRuns ? __ballot(lane < num_parts && !(lw < 0.f)) : ~0ull;
   float v1[kLate];
 #pragma unroll
-  for (int u = 0; u < kLate; ++u) v1[u] = src[static_cast<int64_t>(min(kEarly + u, num_parts - 1)) * D];
+  for (int u = 0; u < kLate; ++u) {
+    const int j = min(kEarly + u, num_parts - 1);
+    v1[u] = src[static_cast<int64_t>(kRuns && j < 64 && !((own >> j) & 1) ? 0 : j) * D];
+  }
 
-  float mx = d < num_parts ? m0 : -FLT_MAX;
-  for (int i = d + D; i < num_parts; i += D) mx = fmaxf(mx, w.ws_max[base + i]);
+  float mx = d < num_parts && !(kRuns && l0 < 0.f) ? m0 : -FLT_MAX;
+  for (int i = d + D; i < num_parts; i += D)
+    if (!(kRuns && w.ws_sum[base + i] < 0.f)) mx = fmaxf(mx, w.ws_max[base + i]);
   mx = rows_max<true>(rows_max<false>(group_max<16>(mx)));
   if (lane == 0) part_red[wv] = mx;
   __syncthreads();
@@ -1000,13 +1065,16 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   float total = 0.f;
   if (d < num_parts) {
     const float f = __expf(m0 - mx);
-    wgt[d] = f;
-    total = f * l0;
+    const bool absorbed = kRuns && l0 < 0.f;
+    wgt[d] = absorbed ? -1.f : f;
+    if (!absorbed) total = f * l0;
   }
   for (int i = d + D; i < num_parts; i += D) {
+    const float li = w.ws_sum[base + i];
     const float f = __expf(w.ws_max[base + i] - mx);
-    wgt[i] = f;
-    total += f * w.ws_sum[base + i];
+    const bool absorbed = kRuns && li < 0.f;
+    wgt[i] = absorbed ? -1.f : f;
+    if (!absorbed) total += f * li;
   }
   total = wave_sum(total);
   if (lane == 0) part_red[wv] = total;
@@ -1018,19 +1086,21 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
   float o = 0.f;
 #pragma unroll
   for (int u = 0; u < kEarly; ++u)
-    if (u < num_parts) o += wgt[u] * v0[u];
+    if (u < num_parts && !(kRuns && wgt[u] == -1.f)) o += wgt[u] * v0[u];
 #pragma unroll
   for (int u = 0; u < kLate; ++u)
-    if (kEarly + u < num_parts) o += wgt[kEarly + u] * v1[u];
+    if (kEarly + u < num_parts && !(kRuns && wgt[kEarly + u] == -1.f)) o += wgt[kEarly + u] * v1[u];
   int i = kEarly + kLate;
   for (; i + kUnroll <= num_parts; i += kUnroll) {
     float v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) v[u] = src[static_cast<int64_t>(i + u) * D];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) o += wgt[i + u] * v[u];
+    for (int u = 0; u < kUnroll; ++u)
+      if (!(kRuns && wgt[i + u] == -1.f)) o += wgt[i + u] * v[u];
   }
-  for (; i < num_parts; ++i) o += wgt[i] * src[static_cast<int64_t>(i) * D];
+  for (; i < num_parts; ++i)
+    if (!(kRuns && wgt[i] == -1.f)) o += wgt[i] * src[static_cast<int64_t>(i) * D];
   reinterpret_cast<_Float16*>(p.out)[static_cast<int64_t>(token) * p.num_heads * D + h * D + d] =
       static_cast<_Float16>(o / total);
 }
@@ -1038,8 +1108,9 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(AttnArgs args) {
 // The persistent form (two workgroups per CU) serves batches of up to
 // kMaxItemsLds decode items, the grid form larger ones.  RLK_TUNE_ATTN_PERSIST
 // overrides: workgroups per CU for the persistent form, or 0 for the grid form.
+// Returns whether the partials were written by runs (absorbed slots marked).
 template <int D, int G, bool kMma>
-void launch_gm(const AttnArgs& a, bool int8, hipStream_t stream) {
+bool launch_gm(const AttnArgs& a, bool int8, hipStream_t stream) {
   const int mode = tune_knob(kAttnPersist, 2);
   if (mode > 0 && a.w.num_items <= kMaxItemsLds) {
     const int64_t units = static_cast<int64_t>(a.w.num_items) * a.w.max_partitions * a.p.kv.num_kv_heads;
@@ -1049,7 +1120,7 @@ void launch_gm(const AttnArgs& a, bool int8, hipStream_t stream) {
     } else {
       decode_attention_persistent<D, G, false, kMma><<<blocks, kThreads, 0, stream>>>(a);
     }
-    return;
+    return kMma && !int8;
   }
   const dim3 grid(a.w.max_partitions, a.p.kv.num_kv_heads, a.w.num_items);
   if (int8) {
@@ -1057,35 +1128,40 @@ void launch_gm(const AttnArgs& a, bool int8, hipStream_t stream) {
   } else {
     decode_attention_kernel<D, G, false, kMma><<<grid, kThreads, 0, stream>>>(a);
   }
+  return false;
 }
 
 // P . V on the matrix cores (the default: at C2 8% faster with an INT8 cache
 // in the persistent form, 11% in the grid form, equal with FP16), or on
 // v_dot2 (RLK_TUNE_ATTN_PV = 0).
 template <int D, int G>
-void launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
-  if (tune_knob(kAttnPv, 1) == 1) {
-    launch_gm<D, G, true>(a, int8, stream);
-  } else {
-    launch_gm<D, G, false>(a, int8, stream);
-  }
+bool launch_g(const AttnArgs& a, bool int8, hipStream_t stream) {
+  if (tune_knob(kAttnPv, 1) == 1) return launch_gm<D, G, true>(a, int8, stream);
+  return launch_gm<D, G, false>(a, int8, stream);
 }
 
 template <int D>
 bool launch_d(const AttnArgs& a, int G, bool int8, hipStream_t stream) {
+  bool runs;
   switch (G) {
-    case 1: launch_g<D, 1>(a, int8, stream); break;
-    case 2: launch_g<D, 2>(a, int8, stream); break;
-    case 3: launch_g<D, 3>(a, int8, stream); break;
-    case 4: launch_g<D, 4>(a, int8, stream); break;
-    case 5: launch_g<D, 5>(a, int8, stream); break;
-    case 6: launch_g<D, 6>(a, int8, stream); break;
-    case 7: launch_g<D, 7>(a, int8, stream); break;
-    case 8: launch_g<D, 8>(a, int8, stream); break;
+    case 1: runs = launch_g<D, 1>(a, int8, stream); break;
+    case 2: runs = launch_g<D, 2>(a, int8, stream); break;
+    case 3: runs = launch_g<D, 3>(a, int8, stream); break;
+    case 4: runs = launch_g<D, 4>(a, int8, stream); break;
+    case 5: runs = launch_g<D, 5>(a, int8, stream); break;
+    case 6: runs = launch_g<D, 6>(a, int8, stream); break;
+    case 7: runs = launch_g<D, 7>(a, int8, stream); break;
+    case 8: runs = launch_g<D, 8>(a, int8, stream); break;
     default: return false;
   }
-  if (a.w.max_partitions > 1)
-    decode_reduce_kernel<D><<<dim3(a.w.num_items, a.p.num_heads), D, 0, stream>>>(a);
+  if (a.w.max_partitions > 1) {
+    const dim3 grid(a.w.num_items, a.p.num_heads);
+    if (runs) {
+      decode_reduce_kernel<D, true><<<grid, D, 0, stream>>>(a);
+    } else {
+      decode_reduce_kernel<D, false><<<grid, D, 0, stream>>>(a);
+    }
+  }
   return true;
 }
 

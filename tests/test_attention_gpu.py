@@ -190,17 +190,28 @@ def test_decode_attention_llama_b32(torch_cuda, int8, attention_form):
     assert_close_f16(got, want, what="attention C2")
 
 
+LONG_CASES = {
+    # past 32 partitions (the merge's batched rows, then its loop) and past D
+    # partitions (its statistics loop): 157 / 36 / 33 / 2 partitions
+    "few": [40000, 9000, 8200, 257],
+    # enough units that a persistent workgroup runs through several
+    # consecutive partitions of one (item, kv head), its range boundaries
+    # splitting items: 2 to 157 partitions per item
+    "runs": [40000, 9000, 300, 25000, 513, 17000, 4097, 30001, 257, 12000, 33000, 768,
+             21000, 6000, 39000, 1100],
+}
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("int8", [False, True])
-def test_decode_attention_long_contexts(torch_cuda, D, int8, attention_form):
-    """Contexts past 32 partitions (the merge's batched rows, then its loop)
-    and past D partitions (its statistics loop): 40000, 9000, 8200 and 257
-    keys, 157 / 36 / 33 / 2 partitions, random cache contents."""
+@pytest.mark.parametrize("lens", ["few", "runs"])
+def test_decode_attention_long_contexts(torch_cuda, D, int8, lens, attention_form):
+    """Long contexts (LONG_CASES), random cache contents."""
     torch = torch_cuda
     from redline_amd import kernels as K
-    say(f"attention long contexts D={D} int8={int8} form={attention_form}")
+    say(f"attention long contexts {lens} D={D} int8={int8} form={attention_form}")
     hq, hkv, bs = 8, 2, 16
-    ctx = np.array([40000, 9000, 8200, 257])
+    ctx = np.array(LONG_CASES[lens])
     n = len(ctx)
     nb = (ctx + bs - 1) // bs
     max_blocks = int(nb.max())
