@@ -540,10 +540,10 @@ __device__ __forceinline__ void int8_cols_to_f16_biased(const uint32_t (&w)[8], 
 // Output: lane (rho, g) receives rows 4 rho + i of head column g, i.e. head
 // g's partial output at the dims of rows 4 rho + i, written to red[wave] for
 // g < G.  `then` runs once the V rows are consumed.
-template <int D, int G, bool kInt8, class Then>
+template <int D, int G, bool kInt8, bool kCarry, class Then>
 __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const PvOperand<D, G, true>& po,
                                             const LaneCoord& c, float (&red)[kWaves][G][D + kRedPad],
-                                            bool carry, float cf, Then then) {
+                                            float cf, Then then) {
   constexpr int kTiles = D / 16;
   const int lane = c.tid % kWave, rho = lane / 16, m = lane % 16;
   f16x8 a[kTiles];
@@ -610,12 +610,19 @@ __device__ __forceinline__ void wave_pv_mma(const RowBatch<D, kInt8>& vb, const 
   for (int dt = 0; dt < kTiles; ++dt) {
     const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], po.b, o0, 0, 0, 0);
     if (m < G) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      auto dim = [&](int i) {
         const int r = 4 * rho + i;
-        const int dim = D == 128 ? 8 * r + dt : 8 * (r % 8) + 4 * (r / 8) + dt;
-        float& dst = red[c.wave][m][dim];
-        dst = carry ? fmaf(dst, cf, o[i]) : o[i];  // carry: rescale the previous partition's sum
+        return D == 128 ? 8 * r + dt : 8 * (r % 8) + 4 * (r / 8) + dt;
+      };
+      if constexpr (kCarry) {  // onto the run's partial so far, rescaled by e^(m_prev - M) (cf)
+        float prev[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) prev[i] = red[c.wave][m][dim(i)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[c.wave][m][dim(i)] = fmaf(prev[i], cf, o[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[c.wave][m][dim(i)] = o[i];
       }
     }
   }
@@ -934,7 +941,11 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_p
       issue_rows<D, kInt8, false>(vb, p.kv.v, has1 ? s.cell[b ^ 1] : zero_cells, 0, c);
     };
     if constexpr (kMma) {
-      wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, carry, cf, next_rows);
+      if (carry) {  // uniform
+        wave_pv_mma<D, G, kInt8, true>(vb, po, c, s.red, cf, next_rows);
+      } else {
+        wave_pv_mma<D, G, kInt8, false>(vb, po, c, s.red, cf, next_rows);
+      }
     } else {
       wave_pv<D, G, kInt8>(vb, s.vsc[b], po, c, s.red, next_rows);
     }
@@ -994,7 +1005,7 @@ __global__ __launch_bounds__(kThreads, (G <= 4 ? 4 : 2)) void decode_attention_k
   wave_softmax<D, G, kInt8, kMma>(kb, s.q[0], s.ksc[0], s.vsc[0], p.scale, n, c, po, s.stat, false, cf,
                                   [] {});
   if constexpr (kMma) {
-    wave_pv_mma<D, G, kInt8>(vb, po, c, s.red, false, cf, [] {});
+    wave_pv_mma<D, G, kInt8, false>(vb, po, c, s.red, cf, [] {});
   } else {
     wave_pv<D, G, kInt8>(vb, s.vsc[0], po, c, s.red, [] {});
   }
