@@ -250,7 +250,8 @@ typedef struct rlk_decode_attention_work {
  * through the caller's workspace.  Replaces kernels::paged_attention_decode,
  * src/cuda/kernels/attention.cu:70-210,362-398.
  * num_items <= 0: no-op.  head_dim not in {64, 128} or G > 8: RLK_EUNSUPPORTED.
- * max_partitions > 1 needs ws_out / ws_max / ws_sum.
+ * max_partitions > 1 needs ws_out / ws_max / ws_sum (scratch: what they hold
+ * after a call is unspecified).
  * Contract: max_partitions >= ceil((positions[t] + 1) / 256) for every item.
  * Keys past max_partitions * 256 are not read, and no error is reported (the
  * launcher cannot see device-side positions without synchronising). */
