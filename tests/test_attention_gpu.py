@@ -202,13 +202,10 @@ LONG_CASES = {
 }
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("lens,D", [("few", 64), ("few", 128), ("runs", 128)])
 @pytest.mark.parametrize("int8", [False, True])
-@pytest.mark.parametrize("lens", ["few", "runs"])
 def test_decode_attention_long_contexts(torch_cuda, D, int8, lens, attention_form):
     """Long contexts (LONG_CASES), random cache contents."""
-    if lens == "runs" and D != 128:
-        pytest.skip("the runs case is taken at D = 128 (the FP16 runs form is shared by D = 64)")
     torch = torch_cuda
     from redline_amd import kernels as K
     say(f"attention long contexts {lens} D={D} int8={int8} form={attention_form}")
