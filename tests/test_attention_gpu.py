@@ -202,7 +202,7 @@ LONG_CASES = {
 }
 
 
-@pytest.mark.parametrize("lens,D", [("few", 64), ("few", 128), ("runs", 128)])
+@pytest.mark.parametrize("lens,D", [("few", 64), ("few", 128), ("runs", 64), ("runs", 128)])
 @pytest.mark.parametrize("int8", [False, True])
 def test_decode_attention_long_contexts(torch_cuda, D, int8, lens, attention_form):
     """Long contexts (LONG_CASES), random cache contents."""
